@@ -1,0 +1,384 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Mamba SSM forward path (one GPU).
+
+Metric: SSM tokens/s on 1xMI355X (prefill + decode) + % of HBM/MFMA roofline.
+
+Workloads (--workload picks one, default cfg2):
+  cfg1  Mamba-1 causal conv1d + selective scan, fp32, B=1 L=256 D=512 N=16 (parity case)
+  cfg2  Mamba-1 block forward, fp32, d=768 D=1536 N=16 R=48 K=4, B=4 L=2048 (in_proj ->
+        conv/SiLU -> x_proj/dt_proj -> scan (D skip, SiLU(z) gate) -> out_proj)
+  cfg3  Mamba-2 SSD prefill core, B=8 L=4096 H=64 P=64 N=128 G=1; --dtype f32|bf16
+  cfg4  Mamba-2 24-layer decode, d=1024 H=32 P=64 N=128 V=32000, 64 cached sequences,
+        one greedy step (24 layers + LM head + argmax) per bench step, fp32
+  cfg5  Mamba-2 SSD long-context prefill core, B=1 L=65536 H=32 P=64 N=128, bf16
+A step is one pass of the path over one batch of synthetic input that is already resident in
+HBM. Timing: W untimed warmup steps, then K steps between HIP events on the stream the
+library launches on (torch's current stream, handed to the library context).
+
+The roofline object names the dominant kernel (stage) of the step, its algorithmic FLOPs or
+bytes per launch, and its average duration from HIP events recorded around it inside the
+library during a second, profiled pass of K steps. The cpu_baseline object times the CPU
+restatement (oracle/) single-threaded on a bounded slice of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0}   # dense MFMA, TFLOP/s
+
+METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--dtype", default=None, choices=["f32", "bf16"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- timing helpers
+
+def timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps   # ms per step
+
+
+def profiled_stages(dev, torch, fn, steps):
+    dev.profile(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    rep = dev.profile_report()
+    dev.profile(False)
+    return {k: (n, ms / n) for k, (n, ms) in rep.items()}   # stage -> (launches, avg ms)
+
+
+def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None):
+    """Achieved rate of one kernel/stage against its binding peak."""
+    t = avg_ms * 1e-3
+    if bound is None:
+        ai = flops / nbytes if (flops and nbytes) else 0.0
+        ridge = PEAK_TFLOPS[prec] * 1e12 / (HBM_PEAK_GBS * 1e9)
+        bound = "mfma" if ai > ridge else "hbm"
+    if bound == "mfma":
+        ach = flops / t / 1e12
+        peak = PEAK_TFLOPS[prec]
+        unit = "TFLOP/s"
+    else:
+        ach = nbytes / t / 1e9
+        peak = HBM_PEAK_GBS
+        unit = "GB/s"
+    return {"kernel": name, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": None, "avg_ms": round(avg_ms, 5),
+            "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
+
+
+def cpu_time(fn, budget_s=20.0):
+    """Run fn at least once and until ~budget; return seconds per call."""
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 3:
+            return el / n
+
+
+# ---------------------------------------------------------------- workloads
+
+def w_cfg2(torch, np, dev, args):
+    from ssmjs_amd import backend
+    B, L, d, N, R, K = 4, 2048, 768, 16, 48, 4
+    D = 2 * d
+    T = B * L
+    cfg = {"vocabSize": 16, "dModel": d, "numLayers": 1, "dState": N, "dConv": K, "expand": 2,
+           "nHeads": 12, "dtRank": R, "layers": [{"type": "mamba1"}]}
+    m = backend.Model(dev, cfg, seed=1002)
+    g = torch.Generator(device="cuda").manual_seed(1002)
+    x = torch.randn(B, L, d, device="cuda", generator=g)
+    y = torch.empty_like(x)
+
+    from ssmjs_amd import _lib
+
+    def step():
+        _lib.call("ssm_mixer_forward_device", m.handle, 0, x.data_ptr(), y.data_ptr(), B, L)
+
+    steps, warm = args.steps or 20, args.warmup if args.warmup is not None else 5
+    ms = timed(torch, step, steps, warm)
+    st = profiled_stages(dev, torch, step, steps)
+    RN = R + 2 * N
+    alg = {
+        "m1.in_proj": (2.0 * T * d * 2 * D, 4.0 * (T * d + 2 * D * d + T * 2 * D)),
+        "m1.conv": (None, 4.0 * (T * D * 2 + D * (K + 1))),
+        "m1.x_proj": (2.0 * T * D * RN, 4.0 * (T * D + RN * D + T * RN)),
+        "m1.dt_proj": (2.0 * T * R * D, 4.0 * (T * R + D * R + T * D)),
+        "m1.scan": (None, 4.0 * (T * D * 4 + T * 2 * N + D * (N + 2))),
+        "m1.out_proj": (2.0 * T * D * d, 4.0 * (T * D + d * D + T * d)),
+    }
+    stages = {}
+    for k, (n, avg) in st.items():
+        f, b = alg[k]
+        bound = "hbm" if f is None else None
+        stages[k] = roofline(k, avg, f, b, "f32", bound)
+    dom = max(stages.values(), key=lambda r: r["avg_ms"])
+    out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+           "dtype": "f32",
+           "config": {"workload": "cfg2: Mamba-1 block forward (in_proj, conv1d+SiLU, "
+                                  "x_proj/dt_proj, selective scan + D skip + SiLU(z) gate, "
+                                  "out_proj)", "batch": B, "seq_len": L, "d_model": d,
+                      "d_inner": D, "d_state": N, "dt_rank": R, "d_conv": K,
+                      "tokens_per_step": T},
+           "roofline": dom, "stages": stages}
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        blob = m.export_weights()
+        om = O.Model(blob)
+        Ls = 512
+        xs = x[:1, :Ls].cpu().numpy()
+        sec = cpu_time(lambda: om.mixer(0, xs))
+        out["cpu_baseline"] = {"value": Ls / sec, "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"B=1, L={Ls} slice of the cfg2 input through the same "
+                                         "block weights; single-threaded C oracle (fp64 "
+                                         "accumulate), oracle/ssm_oracle.c"}
+    m.destroy()
+    return out
+
+
+def w_cfg1(torch, np, dev, args):
+    from ssmjs_amd import kernels
+    B, L, D, N, K = 1, 256, 512, 16, 4
+    r = np.random.default_rng(1001)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()  # noqa
+    x = t(r.standard_normal((B, L, D)))
+    w = t(r.uniform(-0.5, 0.5, (D, K)))
+    z, Bm, Cm = (t(r.standard_normal(s)) for s in ((B, L, D), (B, L, N), (B, L, N)))
+    dt = t(0.5 * r.standard_normal((B, L, D)) - 1.0)
+    A = t(-np.tile(np.arange(1, N + 1), (D, 1)))
+    Dk = t(np.ones(D))
+    u = torch.empty_like(x)
+    y = torch.empty_like(x)
+
+    def step():
+        kernels.causal_conv1d(x, w, None, True, out=u)
+        kernels.selective_scan(u, dt, A, Bm, Cm, Dk, z, None, True, out=y)
+
+    steps, warm = args.steps or 200, args.warmup if args.warmup is not None else 20
+    ms = timed(torch, step, steps, warm)
+    nbytes = 4.0 * (B * L * D * 2 + B * L * D * 4 + B * L * 2 * N)
+    out = {"value": B * L / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+           "dtype": "f32",
+           "config": {"workload": "cfg1: Mamba-1 causal conv1d+SiLU then selective scan",
+                      "batch": B, "seq_len": L, "d_inner": D, "d_state": N, "d_conv": K},
+           "roofline": roofline("conv1d+selective_scan", ms, None, nbytes, bound="hbm")}
+    out["roofline"]["note"] = "working set fits in the 256 MB MALL; launch-latency bound"
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        xn, wn, zn, Bn, Cn, dtn, An = (a.cpu().numpy() for a in (x, w, z, Bm, Cm, dt, A))
+
+        def cpu():
+            un = O.causal_conv1d(xn, wn, None)
+            O.selective_scan(un, dtn, An, Bn, Cn, np.ones(D, np.float32), zn, None, True)
+        sec = cpu_time(cpu, 10.0)
+        out["cpu_baseline"] = {"value": B * L / sec, "unit": "tokens/s", "cores": 1,
+                               "kind": "port", "sample": "the full cfg1 workload, single-threaded "
+                                                         "C oracle"}
+    return out
+
+
+def ssd_inputs(torch, B, L, H, P, N, dtype, bc_std, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    x = torch.randn(B, L, H, P, device="cuda", generator=g).to(tdt)
+    Bm = (torch.randn(B, L, 1, N, device="cuda", generator=g) * bc_std).to(tdt)
+    Cm = (torch.randn(B, L, 1, N, device="cuda", generator=g) * bc_std).to(tdt)
+    dt = torch.randn(B, L, H, device="cuda", generator=g) - 3.0     # softplus(N(0,1) - 3)
+    A = -torch.empty(H, device="cuda").uniform_(1.0, 16.0, generator=g)
+    Dk = torch.ones(H, device="cuda")
+    return x, dt, A, Bm, Cm, Dk
+
+
+def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype):
+    from ssmjs_amd import kernels
+    P, N = 64, 128
+    dtype = args.dtype or default_dtype
+    x, dt, A, Bm, Cm, Dk = ssd_inputs(torch, B, L, H, P, N, dtype, bc_std, 1003)
+    y = torch.empty(B, L, H, P, device="cuda")
+    hT = torch.empty(B, H, P, N, device="cuda")
+    ws = kernels.ssd_workspace(B, L, H, P, 1, N, "cuda")
+
+    def step():
+        kernels.ssd_chunk_scan(x, dt, A, Bm, Cm, Dk, None, True, h0=None, hT=hT, out=y,
+                               workspace=ws)
+
+    steps, warm = args.steps or 20, args.warmup if args.warmup is not None else 3
+    ms = timed(torch, step, steps, warm)
+    T = B * L
+    esz = 2 if dtype == "bf16" else 4
+    Q = 256
+    nchunk = T / Q
+    flops = (2.0 * Q * Q * N / 2 * nchunk          # C B^T (causal, shared across heads, G=1)
+             + 2.0 * Q * Q * P / 2 * nchunk * H    # intra-chunk (CB^T . L) X
+             + 2.0 * Q * P * N * nchunk * H * 2)   # chunk states + state-to-output
+    nbytes = esz * (T * H * P + 2.0 * T * N) + 4.0 * (T * H + T * H * P + B * H * P * N)
+    out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+           "dtype": dtype,
+           "config": {"workload": name, "batch": B, "seq_len": L, "heads": H, "head_dim": P,
+                      "d_state": N, "groups": 1, "chunk_len": Q, "input_dtype": dtype,
+                      "accumulate": "f32"},
+           "roofline": roofline("ssd_chunk_scan", ms, flops, nbytes,
+                                "bf16" if dtype == "bf16" else "f32")}
+    out["roofline"]["mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 /
+                                         PEAK_TFLOPS["bf16" if dtype == "bf16" else "f32"], 4)
+    out["roofline"]["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        Ls = 256
+        xs = x[:1, :Ls, :8].float().cpu().numpy()
+        a = (xs, dt[:1, :Ls, :8].cpu().numpy(), A[:8].cpu().numpy(),
+             Bm[:1, :Ls].float().cpu().numpy(), Cm[:1, :Ls].float().cpu().numpy(),
+             Dk[:8].cpu().numpy())
+        sec = cpu_time(lambda: O.ssd(*a), 10.0)
+        # tokens/s for all H heads: the sample ran 8 of H heads
+        out["cpu_baseline"] = {"value": Ls / (sec * H / 8), "unit": "tokens/s", "cores": 1,
+                               "kind": "port",
+                               "sample": f"B=1, L={Ls}, 8 of {H} heads of the same inputs, "
+                                         "scaled to all heads; single-threaded C oracle "
+                                         "(sequential SSD recurrence)"}
+    return out
+
+
+def w_cfg4(torch, np, dev, args):
+    from ssmjs_amd import _lib, backend
+    Bsz, d, nl, H, N, V = 64, 1024, 24, 32, 128, 32000
+    cfg = {"vocabSize": V, "dModel": d, "numLayers": nl, "dState": N, "dConv": 4, "expand": 2,
+           "nHeads": H, "nGroups": 1, "layers": [{"type": "mamba2"}] * nl}
+    m = backend.Model(dev, cfg, seed=1004)
+    st = m.new_state(Bsz)
+    n = _lib.lib().ssm_state_floats(st._h)
+    r = np.random.default_rng(1004)
+    st.write((0.1 * r.standard_normal(n, dtype=np.float32)).astype(np.float32))
+    ids = torch.from_numpy(r.integers(0, V, Bsz).astype(np.int32)).cuda()
+    nxt = torch.empty(Bsz, dtype=torch.int32, device="cuda")
+    bufs = [ids, nxt]
+    k = [0]
+
+    def step():
+        a, b = bufs[k[0] % 2], bufs[(k[0] + 1) % 2]
+        _lib.call("ssm_decode_step_device", m.handle, st._h, a.data_ptr(), None, b.data_ptr())
+        k[0] += 1
+
+    steps, warm = args.steps or 256, args.warmup if args.warmup is not None else 8
+    ms = timed(torch, step, steps, warm)
+    stg = profiled_stages(dev, torch, step, min(steps, 32))
+    D, P = 2 * d, 64
+    cd, nin = D + 2 * N, 2 * D + 2 * N + H
+    state_b = 4.0 * Bsz * H * P * N * 2
+    alg = {
+        "m2.step.in_proj": (2.0 * Bsz * d * nin, 4.0 * (nin * d + Bsz * (d + nin))),
+        "m2.step.conv": (None, 4.0 * Bsz * cd * (1 + 3 * 2 + 1) + 4.0 * cd * 5),
+        "m2.step.state_update": (None, state_b + 4.0 * Bsz * (D * 2 + 2 * N + H)),
+        "m2.step.gated_norm": (None, 4.0 * Bsz * D * 3),
+        "m2.step.out_proj": (2.0 * Bsz * D * d, 4.0 * (d * D + Bsz * (D + 2 * d))),
+    }
+    stages = {}
+    for kk, (nl_, avg) in stg.items():
+        if kk in alg:
+            f, b = alg[kk]
+            stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None)
+    step_bytes = nl * sum(v[1] for v in alg.values()) + 4.0 * V * d
+    dom = max(stages.values(), key=lambda r_: r_["avg_ms"])
+    out = {"value": Bsz / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+           "dtype": "f32",
+           "config": {"workload": "cfg4: Mamba-2 24-layer recurrent decode, one greedy token "
+                                  "for each of 64 cached sequences per step",
+                      "batch": Bsz, "d_model": d, "layers": nl, "heads": H, "head_dim": P,
+                      "d_state": N, "vocab": V, "tokens_per_step": Bsz},
+           "roofline": dom, "stages": stages,
+           "step_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        # one decode step of the same model for 1 sequence, scaled to 64 sequences
+        blob = m.export_weights()
+        om = O.Model(blob)
+        ost = om.new_state(1)
+        tok = np.array([1], np.uint32)
+        sec = cpu_time(lambda: ost.decode(tok), 10.0)
+        out["cpu_baseline"] = {"value": 1.0 / sec, "unit": "tokens/s", "cores": 1,
+                               "kind": "port",
+                               "sample": "one recurrent decode step of 1 sequence through the same "
+                                         "24-layer weights (single-threaded C oracle)"}
+        del blob, om
+    st.destroy()
+    m.destroy()
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(--gpus must be 1).", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from ssmjs_amd import backend
+    dev = backend.Device(0)
+    # One explicit stream for torch and the library: the events in timed() and every kernel
+    # the library launches are then ordered on the same queue (the null stream's handle is 0,
+    # which the library reads as "use your own stream").
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    dev.set_stream(stream.cuda_stream)
+    log(f"[bench] device {dev.arch} with {dev.compute_units} CUs; workload {args.workload}")
+    if args.workload == "cfg1":
+        r = w_cfg1(torch, np, dev, args)
+    elif args.workload == "cfg2":
+        r = w_cfg2(torch, np, dev, args)
+    elif args.workload == "cfg3":
+        r = ssd_workload(torch, np, dev, args, 8, 4096, 64, 1.0,
+                         "cfg3: Mamba-2 SSD prefill core (chunked SSD, fused)", "bf16")
+    elif args.workload == "cfg4":
+        r = w_cfg4(torch, np, dev, args)
+    else:
+        r = ssd_workload(torch, np, dev, args, 1, 65536, 32, 128 ** -0.25,
+                         "cfg5: Mamba-2 SSD long-context prefill core", "bf16")
+    line = {"metric": METRIC, "value": round(r.pop("value"), 3), "unit": "tokens/s",
+            "n_gpus": 1, "steps": r.pop("steps"), "warmup": r.pop("warmup"),
+            "ms_per_step": round(r.pop("ms_per_step"), 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": r.pop("dtype"),
+            "data": "synthetic (seeded; random-init weights of the named architecture)"}
+    line.update(r)
+    dev.destroy()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -68,6 +68,7 @@ def _declare(L):
     L.orc_model_close.argtypes = [C.c_void_p]
     L.orc_model_vocab.argtypes = [C.c_void_p]
     L.orc_model_forward.argtypes = [C.c_void_p, _u32p, C.c_int, C.c_int, _fp]
+    L.orc_mixer_forward.argtypes = [C.c_void_p, C.c_int, _fp, C.c_int, C.c_int, _fp]
     L.orc_state_new.argtypes = [C.c_void_p, C.c_int]
     L.orc_state_new.restype = C.c_void_p
     L.orc_state_free.argtypes = [C.c_void_p]
@@ -215,6 +216,14 @@ class Model:
         B, L = ids.shape
         out = np.empty((B, L, self.vocab), np.float32)
         lib().orc_model_forward(self._h, ids.ctypes.data_as(_u32p), B, L, _f(out))
+        return out
+
+    def mixer(self, layer, x):
+        """Mixer of `layer` (no norm / residual) on hidden states x (B, L, d)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        B, L, _ = x.shape
+        out = np.empty_like(x)
+        lib().orc_mixer_forward(self._h, layer, _f(x), B, L, _f(out))
         return out
 
     def new_state(self, B):

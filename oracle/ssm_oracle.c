@@ -523,6 +523,10 @@ static void mixer_forward(const orc_model* m, const orc_layer* Ly, const float* 
     }
 }
 
+void orc_mixer_forward(const orc_model* m, int layer, const float* x, int B, int L, float* out) {
+    mixer_forward(m, &m->layers[layer], x, out, B, L, NULL, NULL, 0);
+}
+
 /* Shared trunk: embeddings -> layers -> final norm; hidden (B*L, d) out. */
 static void trunk(const orc_model* m, orc_state* s, const uint32_t* ids, int B, int L, float* hid) {
     int d = m->d;

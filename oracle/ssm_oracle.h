@@ -101,6 +101,9 @@ orc_model* orc_model_open(const void* blob, size_t size, char* err, int errlen);
 void orc_model_close(orc_model* m);
 int orc_model_vocab(const orc_model* m);
 
+/* One mixer (no norm, no residual) of layer `layer` over hidden states x (B,L,d) -> out. */
+void orc_mixer_forward(const orc_model* m, int layer, const float* x, int B, int L, float* out);
+
 /* Full prefill forward: ids (B,L) -> logits (B,L,V) (zero initial state). */
 void orc_model_forward(const orc_model* m, const uint32_t* ids, int B, int L, float* logits);
 

@@ -1,0 +1,56 @@
+// Shared helpers for the gfx950 SSM kernels and the C ABI (include/ssm_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ssm_hip.h"
+
+namespace ssm {
+
+// Thread-local message behind ssm_last_error().
+void set_error(const char* fmt, ...);
+ssm_status fail(ssm_status code, const char* fmt, ...);
+// Map a HIP error from a launch or runtime call to SSM_ERR_HIP (or GPU_UNAVAILABLE / OOM).
+ssm_status from_hip(hipError_t e, const char* what);
+// hipGetLastError after a launch.
+ssm_status check_launch(const char* what);
+
+inline long cdiv(long a, long b) { return (a + b - 1) / b; }
+
+}  // namespace ssm
+
+#define SSM_HIP_TRY(expr)                                                   \
+    do {                                                                    \
+        hipError_t _e = (expr);                                             \
+        if (_e != hipSuccess) return ::ssm::from_hip(_e, #expr);            \
+    } while (0)
+
+#define SSM_REQUIRE(cond, ...)                                              \
+    do {                                                                    \
+        if (!(cond)) return ::ssm::fail(SSM_ERR_INVALID_ARG, __VA_ARGS__);  \
+    } while (0)
+
+// ---------------------------------------------------------------- device math
+namespace ssm {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// v_exp_f32: 2^x.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// softplus(x) = log(1 + e^x), written as max(x,0) + log1p(e^-|x|) so it neither overflows
+// nor loses the small tail; x > 20 returns x (the float32 value of log1p(e^-20) is below
+// half an ulp of 20).
+__device__ __forceinline__ float softplus(float x) {
+    if (x > 20.f) return x;
+    return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
+}
+
+__device__ __forceinline__ float silu(float z) { return z / (1.f + expf(-z)); }
+
+}  // namespace ssm

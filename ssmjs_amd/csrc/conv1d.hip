@@ -1,0 +1,197 @@
+// K1: causal depthwise conv1d (+bias, +SiLU) for gfx950.
+//
+// Replaces the conv stage of MambaCode.js's Mamba-1/2 layers (called through model.forward,
+// src/session/streaming.ts:31-35). HBM-bound: every input element is read once (plus a K-1
+// row halo per time run, served from L2) and every output written once.
+//
+// Layout: x, y (B, L, C) row-major with row strides ldx/ldy (x is usually a column slice of
+// the in_proj output). A thread owns VEC adjacent channels and a run of TT time steps and
+// slides a K-deep register window down the run; threadIdx.x walks channels so a wave reads
+// 64*VEC*4 contiguous bytes per time step.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kTT = 16;      // time steps per thread
+constexpr int kRuns = 4;     // threadIdx.y extent (time runs per block)
+constexpr int kChan = 64;    // threadIdx.x extent (channel groups per block)
+
+template <int VEC>
+struct vec_t;
+template <>
+struct vec_t<1> { using type = float; };
+template <>
+struct vec_t<4> { using type = float4; };
+
+template <int VEC>
+__device__ __forceinline__ void load_v(const float* p, float (&v)[VEC]) {
+    if constexpr (VEC == 4) {
+        float4 q = *reinterpret_cast<const float4*>(p);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+        v[0] = *p;
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_v(float* p, const float (&v)[VEC]) {
+    if constexpr (VEC == 4) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+        *p = v[0];
+    }
+}
+
+template <int K, int VEC>
+__global__ __launch_bounds__(256) void conv1d_fwd(const float* __restrict__ x, long ldx,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ bias,
+                                                  float* __restrict__ y, long ldy, int L, int C,
+                                                  int silu, const float* __restrict__ state_in) {
+    const int c0 = (blockIdx.x * kChan + threadIdx.x) * VEC;
+    const int t0 = (blockIdx.y * kRuns + threadIdx.y) * kTT;
+    const int b = blockIdx.z;
+    if (c0 >= C || t0 >= L) return;
+    const float* xb = x + (long)b * L * ldx + c0;
+    float* yb = y + (long)b * L * ldy + c0;
+
+    float wk[K][VEC], bv[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) wk[k][v] = w[(long)(c0 + v) * K + k];
+        bv[v] = bias ? bias[c0 + v] : 0.f;
+    }
+    // window[k] holds x[t - (K-1) + k] for the next output t
+    float win[K][VEC];
+#pragma unroll
+    for (int k = 0; k < K - 1; ++k) {
+        const int ts = t0 - (K - 1) + k;
+        if (ts >= 0) {
+            load_v<VEC>(xb + (long)ts * ldx, win[k]);
+        } else {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                win[k][v] = state_in
+                                ? state_in[((long)b * C + c0 + v) * (K - 1) + (K - 1) + ts]
+                                : 0.f;
+        }
+    }
+    const int tend = min(t0 + kTT, L);
+    for (int t = t0; t < tend; ++t) {
+        load_v<VEC>(xb + (long)t * ldx, win[K - 1]);
+        float out[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+            float acc = bv[v];
+#pragma unroll
+            for (int k = 0; k < K; ++k) acc = fmaf(wk[k][v], win[k][v], acc);
+            out[v] = silu ? ssm::silu(acc) : acc;
+        }
+        store_v<VEC>(yb + (long)t * ldy, out);
+#pragma unroll
+        for (int k = 0; k < K - 1; ++k)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) win[k][v] = win[k + 1][v];
+    }
+}
+
+// state_out[b,c,j] = x[b, L-(K-1)+j, c] (or the carried state when L < K-1). One thread per
+// (b,c); j ascends, and the source index of an in-place shift is always ahead of j.
+__global__ void conv1d_state_out(const float* __restrict__ x, long ldx, int B, int L, int C,
+                                 int K, const float* state_in, float* state_out) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)B * C) return;
+    const int b = (int)(i / C), c = (int)(i % C);
+    for (int j = 0; j < K - 1; ++j) {
+        const int ts = L - (K - 1) + j;
+        float v;
+        if (ts >= 0) v = x[((long)b * L + ts) * ldx + c];
+        else if (state_in) v = state_in[i * (K - 1) + (K - 1) + ts];
+        else v = 0.f;
+        state_out[i * (K - 1) + j] = v;
+    }
+}
+
+// One decode token: thread per (b, c).
+__global__ void conv1d_update_kernel(const float* __restrict__ x, long ldx,
+                                     const float* __restrict__ w, const float* __restrict__ bias,
+                                     float* __restrict__ y, long ldy, float* __restrict__ state,
+                                     int B, int C, int K, int silu) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)B * C) return;
+    const int b = (int)(i / C), c = (int)(i % C);
+    float* st = state + i * (K - 1);
+    const float xn = x[(long)b * ldx + c];
+    float acc = bias ? bias[c] : 0.f;
+    for (int k = 0; k < K - 1; ++k) acc = fmaf(w[(long)c * K + k], st[k], acc);
+    acc = fmaf(w[(long)c * K + K - 1], xn, acc);
+    for (int k = 0; k + 1 < K - 1; ++k) st[k] = st[k + 1];
+    if (K > 1) st[K - 2] = xn;
+    y[(long)b * ldy + c] = silu ? ssm::silu(acc) : acc;
+}
+
+template <int K>
+ssm_status launch_fwd(const float* x, long ldx, const float* w, const float* bias, float* y,
+                      long ldy, int B, int L, int C, int silu, const float* state_in,
+                      hipStream_t st) {
+    const bool v4 = (C % 4 == 0) && (ldx % 4 == 0) && (ldy % 4 == 0) &&
+                    ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    const dim3 block(kChan, kRuns);
+    if (v4) {
+        dim3 grid((unsigned)ssm::cdiv(C / 4, kChan), (unsigned)ssm::cdiv(L, kRuns * kTT), B);
+        conv1d_fwd<K, 4><<<grid, block, 0, st>>>(x, ldx, w, bias, y, ldy, L, C, silu, state_in);
+    } else {
+        dim3 grid((unsigned)ssm::cdiv(C, kChan), (unsigned)ssm::cdiv(L, kRuns * kTT), B);
+        conv1d_fwd<K, 1><<<grid, block, 0, st>>>(x, ldx, w, bias, y, ldy, L, C, silu, state_in);
+    }
+    return ssm::check_launch("conv1d_fwd");
+}
+
+}  // namespace
+
+extern "C" ssm_status ssm_causal_conv1d(const float* x, long ldx, const float* w,
+                                        const float* bias, float* y, long ldy, int B, int L,
+                                        int C, int K, int silu, const float* state_in,
+                                        float* state_out, void* stream) {
+    SSM_REQUIRE(x && w && y, "ssm_causal_conv1d: null x/w/y");
+    SSM_REQUIRE(B >= 0 && L >= 0 && C >= 0 && K >= 1 && K <= 8, "ssm_causal_conv1d: bad shape");
+    SSM_REQUIRE(ldx >= C && ldy >= C, "ssm_causal_conv1d: row stride below C");
+    SSM_REQUIRE(!state_out || state_out != (float*)x, "ssm_causal_conv1d: state_out aliases x");
+    hipStream_t st = (hipStream_t)stream;
+    if (B == 0 || C == 0) return SSM_OK;
+    if (L > 0) {
+        ssm_status s;
+        switch (K) {
+            case 1: s = launch_fwd<1>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            case 2: s = launch_fwd<2>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            case 3: s = launch_fwd<3>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            case 4: s = launch_fwd<4>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            case 5: s = launch_fwd<5>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            case 6: s = launch_fwd<6>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            case 7: s = launch_fwd<7>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+            default: s = launch_fwd<8>(x, ldx, w, bias, y, ldy, B, L, C, silu, state_in, st); break;
+        }
+        if (s != SSM_OK) return s;
+    }
+    if (state_out && K > 1) {
+        const long n = (long)B * C;
+        conv1d_state_out<<<(unsigned)ssm::cdiv(n, 256), 256, 0, st>>>(x, ldx, B, L, C, K,
+                                                                       state_in, state_out);
+        return ssm::check_launch("conv1d_state_out");
+    }
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_conv1d_update(const float* x, long ldx, const float* w,
+                                        const float* bias, float* y, long ldy, float* state,
+                                        int B, int C, int K, int silu, void* stream) {
+    SSM_REQUIRE(x && w && y && (state || K == 1), "ssm_conv1d_update: null pointer");
+    SSM_REQUIRE(B >= 0 && C >= 0 && K >= 1 && K <= 8 && ldx >= C && ldy >= C,
+                "ssm_conv1d_update: bad shape");
+    if (B == 0 || C == 0) return SSM_OK;
+    const long n = (long)B * C;
+    conv1d_update_kernel<<<(unsigned)ssm::cdiv(n, 256), 256, 0, (hipStream_t)stream>>>(
+        x, ldx, w, bias, y, ldy, state, B, C, K, silu);
+    return ssm::check_launch("conv1d_update");
+}

@@ -1,0 +1,24 @@
+// Launch helpers shared between the glue kernels (glue.hip) and the model code (model.hip).
+#pragma once
+#include "common.hpp"
+
+enum {
+    SSM_INIT_CONST = 0,
+    SSM_INIT_UNIFORM = 1,      // U(a0, a1)
+    SSM_INIT_NORMAL = 2,       // N(0, a0^2)
+    SSM_INIT_ARANGE_LOG = 3,   // log(1 + (i mod row)): S4D-real A_log for Mamba-1
+    SSM_INIT_LOG_UNIFORM = 4,  // log U(a0, a1): Mamba-2 A_log
+    SSM_INIT_DT_BIAS = 5,      // softplus^-1(dt), dt log-uniform in [a0, a1]
+};
+
+namespace ssm {
+ssm_status launch_embed(const uint32_t* ids, const float* emb, float* out, long T, int d, int V,
+                        int* bad, hipStream_t st);
+ssm_status launch_gather_rows(const float* x, long row_stride, long first, float* out, int rows,
+                              int d, hipStream_t st);
+ssm_status launch_argmax(const float* x, long ldx, int rows, int n, uint32_t* out,
+                         hipStream_t st);
+ssm_status launch_init(float* p, long n, int kind, float a0, float a1, uint64_t seed,
+                       uint64_t tensor_id, int row, hipStream_t st);
+ssm_status launch_neg_exp(const float* x, float* y, long n, hipStream_t st);
+}  // namespace ssm

@@ -1,0 +1,1089 @@
+// Model-level C ABI: device context, HybridMambaModel weights and forward/prefill/decode,
+// recurrent state, checkpoint load/export and greedy generation.
+//
+// Mirrors what the reference's session layer calls on MambaCode.js (see include/ssm_hip.h):
+// new HybridMambaModel (src/session/session.ts:359), model.forward (src/session/streaming.ts:
+// 31-35), model.generate (session.ts:421-425), loadWeights / exportWeights (session.ts:394,518,
+// 575). The architecture matches the canonical Mamba / Mamba-2 blocks:
+//   embedding -> n_layers x [x += mixer(RMSNorm(x))] -> RMSNorm -> tied LM head
+//   mamba1 mixer: in_proj -> (x, z); x = SiLU(conv(x)); (dt, B, C) = x_proj(x);
+//                 dt = dt_proj(dt); y = scan(x, dt, A, B, C, D, z, softplus(dt + bias)); out_proj
+//   mamba2 mixer: in_proj -> (z, xBC, dt); xBC = SiLU(conv(xBC)); y = SSD(x, dt, A, B, C, D);
+//                 y = RMSNorm_grouped(y * SiLU(z)); out_proj
+// Projections are rocBLAS SGEMMs on the context stream; the residual add is folded into the
+// out_proj GEMM (beta = 1).
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "glue.hpp"
+
+// ------------------------------------------------------------------ errors
+namespace ssm {
+
+static thread_local std::string g_err;
+
+void set_error(const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+}
+
+ssm_status fail(ssm_status code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+ssm_status from_hip(hipError_t e, const char* what) {
+    ssm_status code = SSM_ERR_HIP;
+    if (e == hipErrorOutOfMemory) code = SSM_ERR_OUT_OF_MEMORY;
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) code = SSM_ERR_GPU_UNAVAILABLE;
+    return fail(code, "%s: %s", what, hipGetErrorString(e));
+}
+
+ssm_status check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SSM_OK : from_hip(e, what);
+}
+
+}  // namespace ssm
+
+#define SSM_TRY(expr)                       \
+    do {                                    \
+        ssm_status _s = (expr);             \
+        if (_s != SSM_OK) return _s;        \
+    } while (0)
+
+extern "C" const char* ssm_last_error(void) { return ssm::g_err.c_str(); }
+
+extern "C" const char* ssm_status_name(ssm_status s) {
+    switch (s) {
+        case SSM_OK: return "OK";
+        case SSM_ERR_GPU_UNAVAILABLE: return "GPU_UNAVAILABLE";
+        case SSM_ERR_CHECKPOINT_INVALID: return "CHECKPOINT_INVALID";
+        case SSM_ERR_DESTROYED: return "SESSION_DESTROYED";
+        default: return "UNKNOWN";
+    }
+}
+
+extern "C" int ssm_abi_version(void) { return 1; }
+
+// ------------------------------------------------------------------ context
+struct ssm_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    rocblas_handle blas = nullptr;
+    bool destroyed = false;
+    char arch[64] = {0};
+    int cus = 0;
+    size_t mem = 0;
+    // opt-in stage profiler: (stage, start, stop) event pairs on the context stream
+    bool prof = false;
+    struct Mark { const char* name; hipEvent_t a, b; };
+    std::vector<Mark> marks;
+};
+
+namespace {
+
+// Records a start event on construction and a stop event on destruction when profiling.
+struct Stage {
+    ssm_ctx* c;
+    size_t idx = (size_t)-1;
+    Stage(ssm_ctx* ctx, const char* name) : c(ctx) {
+        if (!c->prof) return;
+        ssm_ctx::Mark mk{name, nullptr, nullptr};
+        if (hipEventCreate(&mk.a) != hipSuccess || hipEventCreate(&mk.b) != hipSuccess) return;
+        hipEventRecord(mk.a, c->stream);
+        c->marks.push_back(mk);
+        idx = c->marks.size() - 1;
+    }
+    ~Stage() {
+        if (idx != (size_t)-1) hipEventRecord(c->marks[idx].b, c->stream);
+    }
+};
+
+ssm_status blas_status(rocblas_status s, const char* what) {
+    if (s == rocblas_status_success) return SSM_OK;
+    return ssm::fail(SSM_ERR_HIP, "%s: rocBLAS status %d", what, (int)s);
+}
+
+ssm_status ctx_enter(ssm_ctx* c) {
+    if (!c) return ssm::fail(SSM_ERR_INVALID_ARG, "null context");
+    if (c->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "context has been destroyed");
+    SSM_HIP_TRY(hipSetDevice(c->device));
+    return SSM_OK;
+}
+
+// Y (M, Nout) [ld ldy] = X (M, K) [ld ldx] * W^T, W (Nout, K) row-major; Y = beta*Y + ...
+ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, const float* W,
+                float* Y, long ldy, float beta) {
+    if (M == 0 || Nout == 0) return SSM_OK;
+    const float one = 1.f;
+    return blas_status(rocblas_sgemm(c->blas, rocblas_operation_transpose, rocblas_operation_none,
+                                     Nout, M, K, &one, W, K, X, (rocblas_int)ldx, &beta, Y,
+                                     (rocblas_int)ldy),
+                       "sgemm");
+}
+
+}  // namespace
+
+extern "C" ssm_status ssm_ctx_create(int device_ordinal, ssm_ctx** out) {
+    if (!out) return ssm::fail(SSM_ERR_INVALID_ARG, "ssm_ctx_create: null out");
+    *out = nullptr;
+    if (const char* f = std::getenv("SSM_HIP_FAULT"))
+        if (std::strcmp(f, "nodevice") == 0)
+            return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "no HIP device (SSM_HIP_FAULT=nodevice)");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "no HIP device available (%s)",
+                         e != hipSuccess ? hipGetErrorString(e) : "device count 0");
+    if (device_ordinal < 0 || device_ordinal >= n)
+        return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "device %d out of range (%d devices)",
+                         device_ordinal, n);
+    ssm_ctx* c = new ssm_ctx();
+    c->device = device_ordinal;
+    hipDeviceProp_t prop;
+    if ((e = hipSetDevice(device_ordinal)) != hipSuccess ||
+        (e = hipGetDeviceProperties(&prop, device_ordinal)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking)) != hipSuccess) {
+        delete c;
+        return ssm::from_hip(e, "ssm_ctx_create");
+    }
+    std::snprintf(c->arch, sizeof c->arch, "%s", prop.gcnArchName);
+    c->cus = prop.multiProcessorCount;
+    c->mem = prop.totalGlobalMem;
+    c->stream = c->own;
+    if (rocblas_create_handle(&c->blas) != rocblas_status_success ||
+        rocblas_set_stream(c->blas, c->stream) != rocblas_status_success) {
+        hipStreamDestroy(c->own);
+        delete c;
+        return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "rocBLAS handle creation failed");
+    }
+    *out = c;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_ctx_destroy(ssm_ctx* c) {
+    if (!c) return SSM_OK;
+    if (!c->destroyed) {
+        hipSetDevice(c->device);
+        hipStreamSynchronize(c->stream);
+        rocblas_destroy_handle(c->blas);
+        hipStreamDestroy(c->own);
+        c->destroyed = true;
+    }
+    // The struct is kept (not freed) so that models still holding it see SESSION_DESTROYED.
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_ctx_set_stream(ssm_ctx* c, void* stream) {
+    SSM_TRY(ctx_enter(c));
+    c->stream = stream ? (hipStream_t)stream : c->own;
+    return blas_status(rocblas_set_stream(c->blas, c->stream), "rocblas_set_stream");
+}
+
+extern "C" void* ssm_ctx_stream(ssm_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+extern "C" ssm_status ssm_ctx_profile(ssm_ctx* c, int enable) {
+    SSM_TRY(ctx_enter(c));
+    c->prof = enable != 0;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_ctx_profile_report(ssm_ctx* c, char* buf, size_t cap) {
+    SSM_TRY(ctx_enter(c));
+    SSM_HIP_TRY(hipStreamSynchronize(c->stream));
+    std::vector<std::string> names;
+    std::vector<double> tot;
+    std::vector<long> cnt;
+    for (const ssm_ctx::Mark& mk : c->marks) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, mk.a, mk.b) != hipSuccess) ms = 0.f;
+        size_t i = 0;
+        while (i < names.size() && names[i] != mk.name) ++i;
+        if (i == names.size()) { names.push_back(mk.name); tot.push_back(0.0); cnt.push_back(0); }
+        tot[i] += ms;
+        cnt[i] += 1;
+        hipEventDestroy(mk.a);
+        hipEventDestroy(mk.b);
+    }
+    c->marks.clear();
+    std::string out;
+    char line[256];
+    for (size_t i = 0; i < names.size(); ++i) {
+        std::snprintf(line, sizeof line, "%s %ld %.6f\n", names[i].c_str(), cnt[i], tot[i]);
+        out += line;
+    }
+    if (buf && cap) std::snprintf(buf, cap, "%s", out.c_str());
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_ctx_synchronize(ssm_ctx* c) {
+    SSM_TRY(ctx_enter(c));
+    SSM_HIP_TRY(hipStreamSynchronize(c->stream));
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_ctx_info(ssm_ctx* c, char* arch, int arch_len, int* cus,
+                                   size_t* mem) {
+    SSM_TRY(ctx_enter(c));
+    if (arch && arch_len > 0) std::snprintf(arch, arch_len, "%s", c->arch);
+    if (cus) *cus = c->cus;
+    if (mem) *mem = c->mem;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_malloc(ssm_ctx* c, size_t bytes, void** dptr) {
+    SSM_TRY(ctx_enter(c));
+    SSM_REQUIRE(dptr, "ssm_malloc: null out");
+    SSM_HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
+    return SSM_OK;
+}
+extern "C" ssm_status ssm_free(ssm_ctx* c, void* p) {
+    SSM_TRY(ctx_enter(c));
+    SSM_HIP_TRY(hipStreamSynchronize(c->stream));
+    SSM_HIP_TRY(hipFree(p));
+    return SSM_OK;
+}
+extern "C" ssm_status ssm_memcpy_h2d(ssm_ctx* c, void* dst, const void* src, size_t n) {
+    SSM_TRY(ctx_enter(c));
+    SSM_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+    SSM_HIP_TRY(hipStreamSynchronize(c->stream));
+    return SSM_OK;
+}
+extern "C" ssm_status ssm_memcpy_d2h(ssm_ctx* c, void* dst, const void* src, size_t n) {
+    SSM_TRY(ctx_enter(c));
+    SSM_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
+    SSM_HIP_TRY(hipStreamSynchronize(c->stream));
+    return SSM_OK;
+}
+
+// ------------------------------------------------------------------ model
+namespace {
+
+struct LayerW {
+    int type = 0;
+    // offsets (floats) into the weight buffer; -1 when absent for the layer type
+    long norm = -1, in_proj = -1, conv_w = -1, conv_b = -1, x_proj = -1, dt_w = -1, dt_b = -1,
+         A_log = -1, Dsk = -1, gnorm = -1, out_proj = -1;
+    long A = -1;  // offset into the A buffer (-exp(A_log))
+};
+
+struct Dims {
+    int V, d, nl, N, K, expand, H, G, R, chunk, mimo, eos;
+    float eps;
+    int D, P, cd, nin;
+};
+
+constexpr uint32_t kVersion = 1;
+
+size_t header_bytes(int nl) { return 80 + (size_t)((nl + 15) / 16) * 16; }
+
+}  // namespace
+
+struct ssm_model {
+    ssm_ctx* ctx = nullptr;
+    Dims dm{};
+    std::vector<int> types;
+    std::vector<LayerW> layers;
+    long emb = 0, norm_f = 0;
+    size_t nfloats = 0, nA = 0;
+    float* w = nullptr;      // weights in checkpoint payload order
+    float* Ab = nullptr;     // A = -exp(A_log), per layer
+    // workspace, grown on demand
+    char* ws = nullptr;
+    size_t ws_bytes = 0;
+    int* d_flag = nullptr;   // out-of-range token id flag
+    uint32_t* d_ids = nullptr;
+    size_t ids_cap = 0;
+    bool destroyed = false;
+};
+
+struct ssm_state {
+    ssm_model* m = nullptr;
+    int B = 0;
+    float* buf = nullptr;
+    size_t floats = 0;
+    std::vector<float*> ssm, conv;
+    std::vector<size_t> ssm_n, conv_n;
+    uint32_t* d_tok = nullptr;   // (B) ids for device decode steps
+    uint32_t* d_gen = nullptr;   // generation ids ring
+    size_t gen_cap = 0;
+    float* d_logits = nullptr;   // (B, V)
+    bool destroyed = false;
+};
+
+namespace {
+
+ssm_status model_enter(ssm_model* m) {
+    if (!m) return ssm::fail(SSM_ERR_INVALID_ARG, "null model");
+    if (m->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "model has been destroyed");
+    return ctx_enter(m->ctx);
+}
+
+ssm_status state_enter(ssm_state* s) {
+    if (!s) return ssm::fail(SSM_ERR_INVALID_ARG, "null state");
+    if (s->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "state has been destroyed");
+    return model_enter(s->m);
+}
+
+void build_layout(ssm_model* m) {
+    const Dims& d = m->dm;
+    long off = 0, aoff = 0;
+    m->emb = off; off += (long)d.V * d.d;
+    m->layers.assign(d.nl, LayerW());
+    for (int l = 0; l < d.nl; ++l) {
+        LayerW& L = m->layers[l];
+        L.type = m->types[l];
+        L.norm = off; off += d.d;
+        if (L.type == SSM_LAYER_MAMBA1) {
+            L.in_proj = off; off += 2L * d.D * d.d;
+            L.conv_w = off; off += (long)d.D * d.K;
+            L.conv_b = off; off += d.D;
+            L.x_proj = off; off += (long)(d.R + 2 * d.N) * d.D;
+            L.dt_w = off; off += (long)d.D * d.R;
+            L.dt_b = off; off += d.D;
+            L.A_log = off; off += (long)d.D * d.N;
+            L.Dsk = off; off += d.D;
+            L.out_proj = off; off += (long)d.d * d.D;
+            L.A = aoff; aoff += (long)d.D * d.N;
+        } else {
+            L.in_proj = off; off += (long)d.nin * d.d;
+            L.conv_w = off; off += (long)d.cd * d.K;
+            L.conv_b = off; off += d.cd;
+            L.dt_b = off; off += d.H;
+            L.A_log = off; off += d.H;
+            L.Dsk = off; off += d.H;
+            L.gnorm = off; off += d.D;
+            L.out_proj = off; off += (long)d.d * d.D;
+            L.A = aoff; aoff += d.H;
+        }
+    }
+    m->norm_f = off; off += d.d;
+    m->nfloats = (size_t)off;
+    m->nA = (size_t)aoff;
+}
+
+ssm_status refresh_A(ssm_model* m) {
+    hipStream_t st = m->ctx->stream;
+    for (const LayerW& L : m->layers) {
+        const long n = L.type == SSM_LAYER_MAMBA1 ? (long)m->dm.D * m->dm.N : m->dm.H;
+        SSM_TRY(ssm::launch_neg_exp(m->w + L.A_log, m->Ab + L.A, n, st));
+    }
+    return SSM_OK;
+}
+
+ssm_status random_init(ssm_model* m, uint64_t seed) {
+    const Dims& d = m->dm;
+    hipStream_t st = m->ctx->stream;
+    uint64_t tid = 0;
+    auto I = [&](long off, long n, int kind, float a0, float a1, int row = 1) {
+        return ssm::launch_init(m->w + off, n, kind, a0, a1, seed, tid++, row, st);
+    };
+    const float kb = 1.f / std::sqrt((float)d.K);
+    SSM_TRY(I(m->emb, (long)d.V * d.d, SSM_INIT_NORMAL, 0.02f, 0.f));
+    for (const LayerW& L : m->layers) {
+        SSM_TRY(I(L.norm, d.d, SSM_INIT_CONST, 1.f, 0.f));
+        if (L.type == SSM_LAYER_MAMBA1) {
+            SSM_TRY(I(L.in_proj, 2L * d.D * d.d, SSM_INIT_NORMAL, 0.02f, 0.f));
+            SSM_TRY(I(L.conv_w, (long)d.D * d.K, SSM_INIT_UNIFORM, -kb, kb));
+            SSM_TRY(I(L.conv_b, d.D, SSM_INIT_UNIFORM, -kb, kb));
+            SSM_TRY(I(L.x_proj, (long)(d.R + 2 * d.N) * d.D, SSM_INIT_NORMAL, 0.02f, 0.f));
+            const float ds = 1.f / std::sqrt((float)d.R);
+            SSM_TRY(I(L.dt_w, (long)d.D * d.R, SSM_INIT_UNIFORM, -ds, ds));
+            SSM_TRY(I(L.dt_b, d.D, SSM_INIT_DT_BIAS, 1e-3f, 1e-1f));
+            SSM_TRY(I(L.A_log, (long)d.D * d.N, SSM_INIT_ARANGE_LOG, 0.f, 0.f, d.N));
+            SSM_TRY(I(L.Dsk, d.D, SSM_INIT_CONST, 1.f, 0.f));
+            SSM_TRY(I(L.out_proj, (long)d.d * d.D, SSM_INIT_NORMAL, 0.02f, 0.f));
+        } else {
+            SSM_TRY(I(L.in_proj, (long)d.nin * d.d, SSM_INIT_NORMAL, 0.02f, 0.f));
+            SSM_TRY(I(L.conv_w, (long)d.cd * d.K, SSM_INIT_UNIFORM, -kb, kb));
+            SSM_TRY(I(L.conv_b, d.cd, SSM_INIT_UNIFORM, -kb, kb));
+            SSM_TRY(I(L.dt_b, d.H, SSM_INIT_DT_BIAS, 1e-3f, 1e-1f));
+            SSM_TRY(I(L.A_log, d.H, SSM_INIT_LOG_UNIFORM, 1.f, 16.f));
+            SSM_TRY(I(L.Dsk, d.H, SSM_INIT_CONST, 1.f, 0.f));
+            SSM_TRY(I(L.gnorm, d.D, SSM_INIT_CONST, 1.f, 0.f));
+            SSM_TRY(I(L.out_proj, (long)d.d * d.D, SSM_INIT_NORMAL, 0.02f, 0.f));
+        }
+    }
+    SSM_TRY(I(m->norm_f, d.d, SSM_INIT_CONST, 1.f, 0.f));
+    return refresh_A(m);
+}
+
+// Workspace plan for T = B*L tokens (bytes, 256-aligned carve-outs).
+struct Ws {
+    float *hid, *nrm, *a, *b, *c, *d, *e, *last, *logits;
+    void* scan;
+    size_t scan_bytes;
+};
+
+size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
+    const Dims& d = m->dm;
+    const size_t T = (size_t)B * L;
+    size_t na = 0, nb = 0, nc = 0, ndd = 0, ne = 0, scan = 0;
+    bool has1 = false, has2 = false;
+    for (int t : m->types) (t == SSM_LAYER_MAMBA1 ? has1 : has2) = true;
+    if (has1) {
+        na = std::max(na, T * 2 * d.D);             // xz
+        nb = std::max(nb, T * d.D);                 // xc
+        nc = std::max(nc, T * (d.R + 2 * d.N));     // dbl
+        ndd = std::max(ndd, T * d.D);               // dt
+        ne = std::max(ne, T * d.D);                 // y
+        scan = std::max(scan, ssm_selective_scan_workspace(B, L, d.D, d.N));
+    }
+    if (has2) {
+        na = std::max(na, T * d.nin);               // zx
+        nb = std::max(nb, T * d.cd);                // xbc
+        nc = std::max(nc, T * d.D);                 // y
+        ndd = std::max(ndd, T * d.D);               // yn
+        scan = std::max(scan, ssm_ssd_workspace(B, L, d.H, d.P, d.G, d.N));
+    }
+    const size_t nlog = full_logits ? T * d.V : (size_t)B * d.V;
+    size_t off = 0;
+    size_t o_hid = off; off += al(4 * T * d.d);
+    size_t o_nrm = off; off += al(4 * T * d.d);
+    size_t o_a = off; off += al(4 * na);
+    size_t o_b = off; off += al(4 * nb);
+    size_t o_c = off; off += al(4 * nc);
+    size_t o_d = off; off += al(4 * ndd);
+    size_t o_e = off; off += al(4 * ne);
+    size_t o_last = off; off += al(4 * (size_t)B * d.d);
+    size_t o_log = off; off += al(4 * nlog);
+    size_t o_scan = off; off += al(scan);
+    if (out) {
+        char* base = m->ws;
+        out->hid = (float*)(base + o_hid); out->nrm = (float*)(base + o_nrm);
+        out->a = (float*)(base + o_a); out->b = (float*)(base + o_b);
+        out->c = (float*)(base + o_c); out->d = (float*)(base + o_d);
+        out->e = (float*)(base + o_e); out->last = (float*)(base + o_last);
+        out->logits = (float*)(base + o_log);
+        out->scan = base + o_scan; out->scan_bytes = scan;
+    }
+    return off;
+}
+
+ssm_status ensure_ws(ssm_model* m, int B, int L, bool full_logits, Ws* w) {
+    const size_t need = plan_ws(m, B, L, full_logits, nullptr);
+    if (need > m->ws_bytes) {
+        SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        if (m->ws) SSM_HIP_TRY(hipFree(m->ws));
+        m->ws = nullptr;
+        m->ws_bytes = 0;
+        SSM_HIP_TRY(hipMalloc((void**)&m->ws, need));
+        m->ws_bytes = need;
+    }
+    plan_ws(m, B, L, full_logits, w);
+    return SSM_OK;
+}
+
+ssm_status ensure_ids(ssm_model* m, size_t n) {
+    if (n > m->ids_cap) {
+        SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        if (m->d_ids) SSM_HIP_TRY(hipFree(m->d_ids));
+        m->d_ids = nullptr;
+        SSM_HIP_TRY(hipMalloc((void**)&m->d_ids, n * sizeof(uint32_t)));
+        m->ids_cap = n;
+    }
+    return SSM_OK;
+}
+
+// One mixer over (B, L) tokens: reads x (T, d) [normalised], adds its output into out (T, d)
+// with beta (0: overwrite, 1: residual add). ssm/conv state may be null (zero initial state).
+ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, float beta, int B,
+                 int L, float* ssm_st, float* conv_st, const Ws& w) {
+    const Dims& d = m->dm;
+    ssm_ctx* c = m->ctx;
+    hipStream_t st = c->stream;
+    const int T = B * L;
+    const float* W = m->w;
+    const float* A = m->Ab + Ly.A;
+    if (Ly.type == SSM_LAYER_MAMBA1) {
+        float *xz = w.a, *xc = w.b, *dbl = w.c, *dtv = w.d, *y = w.e;
+        const int RN = d.R + 2 * d.N;
+        { Stage g(c, "m1.in_proj"); SSM_TRY(gemm(c, T, 2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
+        { Stage g(c, "m1.conv");
+          SSM_TRY(ssm_causal_conv1d(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, B, L, d.D,
+                                    d.K, 1, conv_st, conv_st, st)); }
+        { Stage g(c, "m1.x_proj"); SSM_TRY(gemm(c, T, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
+        { Stage g(c, "m1.dt_proj"); SSM_TRY(gemm(c, T, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
+        { Stage g(c, "m1.scan");
+          SSM_TRY(ssm_selective_scan(xc, d.D, dtv, d.D, W + Ly.dt_b, 1, A, dbl + d.R, RN,
+                                     dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D, y, d.D, B,
+                                     L, d.D, d.N, ssm_st, ssm_st, w.scan, w.scan_bytes, st)); }
+        { Stage g(c, "m1.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, y, d.D, W + Ly.out_proj, out, d.d, beta)); }
+    } else {
+        float *zx = w.a, *xbc = w.b, *y = w.c, *yn = w.d;
+        const int GN = d.G * d.N;
+        { Stage g(c, "m2.in_proj"); SSM_TRY(gemm(c, T, d.nin, d.d, x, d.d, W + Ly.in_proj, zx, d.nin, 0.f)); }
+        { Stage g(c, "m2.conv");
+          SSM_TRY(ssm_causal_conv1d(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc, d.cd, B, L,
+                                    d.cd, d.K, 1, conv_st, conv_st, st)); }
+        { Stage g(c, "m2.ssd");
+          SSM_TRY(ssm_ssd_chunk_scan(SSM_F32, xbc, d.cd, zx + d.D + d.cd, d.nin, W + Ly.dt_b, 1,
+                                     0.f, INFINITY, A, xbc + d.D, d.cd, xbc + d.D + GN, d.cd,
+                                     W + Ly.Dsk, y, d.D, B, L, d.H, d.P, d.G, d.N, ssm_st, ssm_st,
+                                     w.scan, w.scan_bytes, st)); }
+        { Stage g(c, "m2.gated_norm");
+          SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, T, d.D, d.G, d.eps,
+                                    st)); }
+        { Stage g(c, "m2.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, beta)); }
+    }
+    return SSM_OK;
+}
+
+// One-token mixer step for B sequences with the recurrent state.
+ssm_status mixer_step(ssm_model* m, const LayerW& Ly, const float* x, float* out, int B,
+                      float* ssm_st, float* conv_st, const Ws& w) {
+    const Dims& d = m->dm;
+    ssm_ctx* c = m->ctx;
+    hipStream_t st = c->stream;
+    const float* W = m->w;
+    const float* A = m->Ab + Ly.A;
+    if (Ly.type == SSM_LAYER_MAMBA1) {
+        float *xz = w.a, *xc = w.b, *dbl = w.c, *dtv = w.d, *y = w.e;
+        const int RN = d.R + 2 * d.N;
+        { Stage g(c, "m1.step.in_proj"); SSM_TRY(gemm(c, B, 2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
+        { Stage g(c, "m1.step.conv");
+          SSM_TRY(ssm_conv1d_update(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, conv_st, B,
+                                    d.D, d.K, 1, st)); }
+        { Stage g(c, "m1.step.x_proj"); SSM_TRY(gemm(c, B, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
+        { Stage g(c, "m1.step.dt_proj"); SSM_TRY(gemm(c, B, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
+        { Stage g(c, "m1.step.state_update");
+          SSM_TRY(ssm_m1_state_update(xc, d.D, dtv, d.D, W + Ly.dt_b, 1, A, dbl + d.R, RN,
+                                      dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D, y, d.D,
+                                      ssm_st, B, d.D, d.N, st)); }
+        { Stage g(c, "m1.step.out_proj"); SSM_TRY(gemm(c, B, d.d, d.D, y, d.D, W + Ly.out_proj, out, d.d, 1.f)); }
+    } else {
+        float *zx = w.a, *xbc = w.b, *y = w.c, *yn = w.d;
+        const int GN = d.G * d.N;
+        { Stage g(c, "m2.step.in_proj"); SSM_TRY(gemm(c, B, d.nin, d.d, x, d.d, W + Ly.in_proj, zx, d.nin, 0.f)); }
+        { Stage g(c, "m2.step.conv");
+          SSM_TRY(ssm_conv1d_update(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc, d.cd,
+                                    conv_st, B, d.cd, d.K, 1, st)); }
+        { Stage g(c, "m2.step.state_update");
+          SSM_TRY(ssm_m2_state_update(xbc, d.cd, zx + d.D + d.cd, d.nin, W + Ly.dt_b, 1, 0.f,
+                                      INFINITY, A, xbc + d.D, d.cd, xbc + d.D + GN, d.cd,
+                                      W + Ly.Dsk, nullptr, 0, y, d.D, ssm_st, B, d.H, d.P, d.G,
+                                      d.N, st)); }
+        { Stage g(c, "m2.step.gated_norm");
+          SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, B, d.D, d.G, d.eps,
+                                    st)); }
+        { Stage g(c, "m2.step.out_proj"); SSM_TRY(gemm(c, B, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, 1.f)); }
+    }
+    return SSM_OK;
+}
+
+// embeddings -> layers -> final norm; result in w.nrm (T, d).
+ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s, const Ws& w) {
+    const Dims& d = m->dm;
+    hipStream_t st = m->ctx->stream;
+    const long T = (long)B * L;
+    SSM_TRY(ssm::launch_embed(d_ids, m->w + m->emb, w.hid, T, d.d, d.V, m->d_flag, st));
+    for (int l = 0; l < d.nl; ++l) {
+        const LayerW& Ly = m->layers[l];
+        SSM_TRY(ssm_rmsnorm(w.hid, d.d, m->w + Ly.norm, w.nrm, d.d, (int)T, d.d, d.eps, st));
+        float* ss = s ? s->ssm[l] : nullptr;
+        float* cs = s ? s->conv[l] : nullptr;
+        if (L == 1 && s)
+            SSM_TRY(mixer_step(m, Ly, w.nrm, w.hid, B, ss, cs, w));
+        else
+            SSM_TRY(mixer(m, Ly, w.nrm, w.hid, 1.f, B, L, ss, cs, w));
+    }
+    return ssm_rmsnorm(w.hid, d.d, m->w + m->norm_f, w.nrm, d.d, (int)T, d.d, d.eps, st);
+}
+
+ssm_status check_flag(ssm_model* m) {
+    int bad = 0;
+    SSM_HIP_TRY(hipMemcpyAsync(&bad, m->d_flag, sizeof(int), hipMemcpyDeviceToHost,
+                               m->ctx->stream));
+    SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    if (bad) {
+        SSM_HIP_TRY(hipMemsetAsync(m->d_flag, 0, sizeof(int), m->ctx->stream));
+        return ssm::fail(SSM_ERR_INVALID_ARG, "token id out of range [0, %d)", m->dm.V);
+    }
+    return SSM_OK;
+}
+
+ssm_status validate_config(const ssm_config* cfg, Dims* out, std::vector<int>* types) {
+    SSM_REQUIRE(cfg, "null config");
+    Dims d{};
+    d.V = cfg->vocab_size; d.d = cfg->d_model; d.nl = cfg->n_layers; d.N = cfg->d_state;
+    d.K = cfg->d_conv; d.expand = cfg->expand; d.H = cfg->n_heads; d.G = cfg->n_groups;
+    d.chunk = cfg->chunk_len; d.mimo = cfg->mimo_group; d.eos = cfg->eos_id;
+    d.R = cfg->dt_rank > 0 ? cfg->dt_rank : (d.d + 15) / 16;
+    d.eps = cfg->norm_eps > 0.f ? cfg->norm_eps : 1e-5f;
+    SSM_REQUIRE(d.V > 0 && d.d > 0 && d.nl >= 0 && d.N > 0 && d.K >= 1 && d.K <= 8 &&
+                    d.expand > 0 && d.H > 0 && d.G > 0,
+                "config: non-positive dimension");
+    // resolveModelConfig's own check (src/session/presets.ts:97-101)
+    if (d.d % d.H != 0)
+        return ssm::fail(SSM_ERR_INVALID_ARG, "dModel (%d) must be divisible by nHeads (%d).",
+                         d.d, d.H);
+    d.D = d.expand * d.d;
+    d.P = d.D / d.H;
+    d.cd = d.D + 2 * d.G * d.N;
+    d.nin = 2 * d.D + 2 * d.G * d.N + d.H;
+    types->assign(d.nl, SSM_LAYER_MAMBA1);
+    for (int l = 0; l < d.nl; ++l) {
+        const int t = cfg->layer_types ? cfg->layer_types[l] : SSM_LAYER_MAMBA1;
+        if (t == SSM_LAYER_MAMBA1 || t == SSM_LAYER_MAMBA2) {
+            (*types)[l] = t;
+            continue;
+        }
+        return ssm::fail(SSM_ERR_UNSUPPORTED,
+                         "layer %d: type %s is not implemented by the MI355X backend "
+                         "(mamba1 and mamba2 are)", l,
+                         t == SSM_LAYER_MAMBA3 ? "mamba3" : t == SSM_LAYER_ATTENTION ? "attention"
+                                                                                   : "unknown");
+    }
+    for (int t : *types)
+        if (t == SSM_LAYER_MAMBA2) {
+            SSM_REQUIRE(d.H % d.G == 0, "nHeads (%d) must be divisible by nGroups (%d)", d.H, d.G);
+            SSM_REQUIRE(d.N % 4 == 0, "mamba2 layers need dState divisible by 4");
+        }
+    *out = d;
+    return SSM_OK;
+}
+
+}  // namespace
+
+extern "C" ssm_status ssm_model_create(ssm_ctx* ctx, const ssm_config* cfg, uint64_t seed,
+                                       ssm_model** out) {
+    SSM_REQUIRE(out, "ssm_model_create: null out");
+    *out = nullptr;
+    SSM_TRY(ctx_enter(ctx));
+    ssm_model* m = new ssm_model();
+    m->ctx = ctx;
+    ssm_status s = validate_config(cfg, &m->dm, &m->types);
+    if (s != SSM_OK) { delete m; return s; }
+    build_layout(m);
+    hipError_t e;
+    if ((e = hipMalloc((void**)&m->w, m->nfloats * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc((void**)&m->Ab, (m->nA ? m->nA : 1) * sizeof(float))) != hipSuccess ||
+        (e = hipMalloc((void**)&m->d_flag, sizeof(int))) != hipSuccess ||
+        (e = hipMemsetAsync(m->d_flag, 0, sizeof(int), ctx->stream)) != hipSuccess) {
+        hipFree(m->w); hipFree(m->Ab); hipFree(m->d_flag);
+        delete m;
+        return ssm::from_hip(e, "ssm_model_create");
+    }
+    s = random_init(m, seed);
+    if (s == SSM_OK) {
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) s = ssm::from_hip(e, "ssm_model_create");
+    }
+    if (s != SSM_OK) {
+        hipFree(m->w); hipFree(m->Ab); hipFree(m->d_flag);
+        delete m;
+        return s;
+    }
+    *out = m;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_model_destroy(ssm_model* m) {
+    if (!m || m->destroyed) return SSM_OK;
+    if (!m->ctx->destroyed) {
+        hipSetDevice(m->ctx->device);
+        hipStreamSynchronize(m->ctx->stream);
+        hipFree(m->w); hipFree(m->Ab); hipFree(m->ws); hipFree(m->d_flag); hipFree(m->d_ids);
+    }
+    m->destroyed = true;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_model_config(ssm_model* m, ssm_config* out) {
+    SSM_TRY(model_enter(m));
+    SSM_REQUIRE(out, "null out");
+    const Dims& d = m->dm;
+    out->vocab_size = d.V; out->d_model = d.d; out->n_layers = d.nl; out->d_state = d.N;
+    out->d_conv = d.K; out->expand = d.expand; out->n_heads = d.H; out->n_groups = d.G;
+    out->chunk_len = d.chunk; out->mimo_group = d.mimo; out->eos_id = d.eos; out->dt_rank = d.R;
+    out->norm_eps = d.eps;
+    return SSM_OK;
+}
+
+namespace {
+void write_header(const ssm_model* m, int f16, unsigned char* p) {
+    const Dims& d = m->dm;
+    const size_t hb = header_bytes(d.nl);
+    std::memset(p, 0, hb);
+    std::memcpy(p, "SSMW", 4);
+    const uint32_t ver = kVersion, dt = f16 ? 1 : 0, hb32 = (uint32_t)hb;
+    const uint64_t pay = m->nfloats * (f16 ? 2 : 4);
+    std::memcpy(p + 4, &ver, 4); std::memcpy(p + 8, &dt, 4); std::memcpy(p + 12, &hb32, 4);
+    std::memcpy(p + 16, &pay, 8);
+    const int32_t f[9] = {d.V, d.d, d.nl, d.N, d.K, d.expand, d.H, d.G, d.R};
+    std::memcpy(p + 24, f, 36);
+    std::memcpy(p + 60, &d.eps, 4);
+    const int32_t g[3] = {d.chunk, d.eos, d.mimo};
+    std::memcpy(p + 64, g, 12);
+    for (int l = 0; l < d.nl; ++l) p[80 + l] = (unsigned char)m->types[l];
+}
+
+// IEEE binary16 <-> binary32, round to nearest even.
+uint16_t f2h(float f) {
+    uint32_t x; std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t mag = x & 0x7fffffffu;
+    if (mag >= 0x7f800000u) return (uint16_t)(sign | (mag > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (mag >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   // rounds to >= 65520 -> inf
+    if (mag < 0x38800000u) {                                      // subnormal or zero in half
+        const float af = std::fabs(f);
+        const float scaled = af * 16777216.0f;                    // * 2^24: half ulp units
+        return (uint16_t)(sign | (uint32_t)std::nearbyint(scaled));
+    }
+    const uint32_t e = ((mag >> 23) - 112) << 10;
+    const uint32_t mant = mag & 0x7fffffu;
+    uint32_t h = e | (mant >> 13);
+    const uint32_t rest = mant & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+float h2f(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15), e = (h >> 10) & 0x1f, mnt = h & 0x3ff;
+    float v;
+    if (e == 0) v = std::ldexp((float)mnt, -24);
+    else if (e == 31) v = mnt ? NAN : INFINITY;
+    else v = std::ldexp((float)(mnt | 0x400), (int)e - 25);
+    return s ? -v : v;
+}
+}  // namespace
+
+extern "C" ssm_status ssm_model_export_weights(ssm_model* m, int f16, void* buf, size_t cap,
+                                               size_t* bytes) {
+    SSM_TRY(model_enter(m));
+    const size_t hb = header_bytes(m->dm.nl);
+    const size_t total = hb + m->nfloats * (f16 ? 2 : 4);
+    if (bytes) *bytes = total;
+    if (!buf) return SSM_OK;
+    SSM_REQUIRE(cap >= total, "ssm_model_export_weights: buffer of %zu bytes needed", total);
+    unsigned char* p = (unsigned char*)buf;
+    write_header(m, f16, p);
+    if (!f16) {
+        SSM_HIP_TRY(hipMemcpyAsync(p + hb, m->w, m->nfloats * 4, hipMemcpyDeviceToHost,
+                                   m->ctx->stream));
+        SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    } else {
+        std::vector<float> tmp(m->nfloats);
+        SSM_HIP_TRY(hipMemcpyAsync(tmp.data(), m->w, m->nfloats * 4, hipMemcpyDeviceToHost,
+                                   m->ctx->stream));
+        SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+        for (size_t i = 0; i < m->nfloats; ++i) {
+            const uint16_t h = f2h(tmp[i]);
+            std::memcpy(p + hb + 2 * i, &h, 2);
+        }
+    }
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_model_load_weights(ssm_model* m, const void* buf, size_t bytes) {
+    SSM_TRY(model_enter(m));
+    const unsigned char* p = (const unsigned char*)buf;
+    auto bad = [](const char* why) { return ssm::fail(SSM_ERR_CHECKPOINT_INVALID, "%s", why); };
+    if (!p || bytes < 80 || std::memcmp(p, "SSMW", 4) != 0) return bad("bad magic");
+    uint32_t ver, dt, hb;
+    uint64_t pay;
+    std::memcpy(&ver, p + 4, 4); std::memcpy(&dt, p + 8, 4); std::memcpy(&hb, p + 12, 4);
+    std::memcpy(&pay, p + 16, 8);
+    if (ver != kVersion) return bad("unsupported version");
+    if (dt > 1) return bad("unsupported dtype");
+    int32_t f[9];
+    std::memcpy(f, p + 24, 36);
+    const Dims& d = m->dm;
+    if (f[2] != d.nl || hb != header_bytes(d.nl) || (uint64_t)hb + pay != bytes)
+        return bad("size mismatch");
+    const int32_t want[9] = {d.V, d.d, d.nl, d.N, d.K, d.expand, d.H, d.G, d.R};
+    for (int i = 0; i < 9; ++i)
+        if (f[i] != want[i]) return bad("size mismatch: checkpoint dimensions differ from model");
+    for (int l = 0; l < d.nl; ++l)
+        if (p[80 + l] != m->types[l]) return bad("size mismatch: layer types differ from model");
+    if (pay != m->nfloats * (dt ? 2 : 4)) return bad("size mismatch");
+    float eps;
+    std::memcpy(&eps, p + 60, 4);
+    if (eps > 0.f) m->dm.eps = eps;
+    if (dt == 0) {
+        SSM_HIP_TRY(hipMemcpyAsync(m->w, p + hb, m->nfloats * 4, hipMemcpyHostToDevice,
+                                   m->ctx->stream));
+        SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    } else {
+        std::vector<float> tmp(m->nfloats);
+        for (size_t i = 0; i < m->nfloats; ++i) {
+            uint16_t h;
+            std::memcpy(&h, p + hb + 2 * i, 2);
+            tmp[i] = h2f(h);
+        }
+        SSM_HIP_TRY(hipMemcpyAsync(m->w, tmp.data(), m->nfloats * 4, hipMemcpyHostToDevice,
+                                   m->ctx->stream));
+        SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    }
+    SSM_TRY(refresh_A(m));
+    SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_forward_device(ssm_model* m, const uint32_t* d_ids, int B, int L,
+                                         float* d_logits) {
+    SSM_TRY(model_enter(m));
+    SSM_REQUIRE(d_ids && d_logits && B >= 0 && L >= 0, "ssm_forward_device: bad args");
+    if (B == 0 || L == 0) return SSM_OK;
+    Ws w;
+    SSM_TRY(ensure_ws(m, B, L, false, &w));
+    SSM_TRY(trunk(m, d_ids, B, L, nullptr, w));
+    return gemm(m->ctx, B * L, m->dm.V, m->dm.d, w.nrm, m->dm.d, m->w + m->emb, d_logits,
+                m->dm.V, 0.f);
+}
+
+extern "C" ssm_status ssm_forward(ssm_model* m, const uint32_t* ids, int B, int L,
+                                  float* logits) {
+    SSM_TRY(model_enter(m));
+    SSM_REQUIRE(ids && logits && B >= 0 && L >= 0, "ssm_forward: bad args");
+    if (B == 0 || L == 0) return SSM_OK;
+    const size_t T = (size_t)B * L;
+    SSM_TRY(ensure_ids(m, T));
+    Ws w;
+    SSM_TRY(ensure_ws(m, B, L, true, &w));
+    SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, ids, T * 4, hipMemcpyHostToDevice, m->ctx->stream));
+    SSM_TRY(trunk(m, m->d_ids, B, L, nullptr, w));
+    SSM_TRY(gemm(m->ctx, (int)T, m->dm.V, m->dm.d, w.nrm, m->dm.d, m->w + m->emb, w.logits,
+                 m->dm.V, 0.f));
+    SSM_HIP_TRY(hipMemcpyAsync(logits, w.logits, T * m->dm.V * 4, hipMemcpyDeviceToHost,
+                               m->ctx->stream));
+    return check_flag(m);
+}
+
+extern "C" ssm_status ssm_mixer_forward_device(ssm_model* m, int layer, const float* d_x,
+                                               float* d_y, int B, int L) {
+    SSM_TRY(model_enter(m));
+    SSM_REQUIRE(layer >= 0 && layer < m->dm.nl && d_x && d_y && B >= 0 && L >= 0,
+                "ssm_mixer_forward_device: bad args");
+    if (B == 0 || L == 0) return SSM_OK;
+    Ws w;
+    SSM_TRY(ensure_ws(m, B, L, false, &w));
+    return mixer(m, m->layers[layer], d_x, d_y, 0.f, B, L, nullptr, nullptr, w);
+}
+
+// ------------------------------------------------------------------ state
+extern "C" ssm_status ssm_state_create(ssm_model* m, int B, ssm_state** out) {
+    SSM_REQUIRE(out, "ssm_state_create: null out");
+    *out = nullptr;
+    SSM_TRY(model_enter(m));
+    SSM_REQUIRE(B > 0, "ssm_state_create: batch must be positive");
+    const Dims& d = m->dm;
+    ssm_state* s = new ssm_state();
+    s->m = m;
+    s->B = B;
+    size_t total = 0;
+    for (int t : m->types) {
+        const size_t a = t == SSM_LAYER_MAMBA1 ? (size_t)B * d.D * d.N : (size_t)B * d.H * d.P * d.N;
+        const size_t c = (size_t)B * (t == SSM_LAYER_MAMBA1 ? d.D : d.cd) * (d.K - 1);
+        s->ssm_n.push_back(a);
+        s->conv_n.push_back(c);
+        total += al(a * 4) / 4 + al(c * 4) / 4;
+    }
+    s->floats = 0;
+    for (size_t i = 0; i < s->ssm_n.size(); ++i) s->floats += s->ssm_n[i] + s->conv_n[i];
+    hipError_t e;
+    if ((e = hipMalloc((void**)&s->buf, (total ? total : 1) * 4)) != hipSuccess ||
+        (e = hipMalloc((void**)&s->d_tok, (size_t)B * 4)) != hipSuccess ||
+        (e = hipMalloc((void**)&s->d_logits, (size_t)B * d.V * 4)) != hipSuccess) {
+        hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits);
+        delete s;
+        return ssm::from_hip(e, "ssm_state_create");
+    }
+    size_t off = 0;
+    for (size_t i = 0; i < s->ssm_n.size(); ++i) {
+        s->ssm.push_back(s->buf + off); off += al(s->ssm_n[i] * 4) / 4;
+        s->conv.push_back(s->buf + off); off += al(s->conv_n[i] * 4) / 4;
+    }
+    e = hipMemsetAsync(s->buf, 0, (total ? total : 1) * 4, m->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+    if (e != hipSuccess) {
+        hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits);
+        delete s;
+        return ssm::from_hip(e, "ssm_state_create");
+    }
+    *out = s;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_state_destroy(ssm_state* s) {
+    if (!s || s->destroyed) return SSM_OK;
+    if (!s->m->destroyed && !s->m->ctx->destroyed) {
+        hipSetDevice(s->m->ctx->device);
+        hipStreamSynchronize(s->m->ctx->stream);
+        hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits); hipFree(s->d_gen);
+    }
+    s->destroyed = true;
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_state_reset(ssm_state* s) {
+    SSM_TRY(state_enter(s));
+    for (size_t i = 0; i < s->ssm.size(); ++i) {
+        SSM_HIP_TRY(hipMemsetAsync(s->ssm[i], 0, s->ssm_n[i] * 4, s->m->ctx->stream));
+        SSM_HIP_TRY(hipMemsetAsync(s->conv[i], 0, s->conv_n[i] * 4, s->m->ctx->stream));
+    }
+    SSM_HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    return SSM_OK;
+}
+
+extern "C" size_t ssm_state_floats(ssm_state* s) { return s ? s->floats : 0; }
+
+extern "C" ssm_status ssm_state_read(ssm_state* s, float* out) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(out, "null out");
+    size_t off = 0;
+    for (size_t i = 0; i < s->ssm.size(); ++i) {
+        SSM_HIP_TRY(hipMemcpyAsync(out + off, s->ssm[i], s->ssm_n[i] * 4, hipMemcpyDeviceToHost,
+                                   s->m->ctx->stream));
+        off += s->ssm_n[i];
+        SSM_HIP_TRY(hipMemcpyAsync(out + off, s->conv[i], s->conv_n[i] * 4,
+                                   hipMemcpyDeviceToHost, s->m->ctx->stream));
+        off += s->conv_n[i];
+    }
+    SSM_HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_state_write(ssm_state* s, const float* in) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(in, "null in");
+    size_t off = 0;
+    for (size_t i = 0; i < s->ssm.size(); ++i) {
+        SSM_HIP_TRY(hipMemcpyAsync(s->ssm[i], in + off, s->ssm_n[i] * 4, hipMemcpyHostToDevice,
+                                   s->m->ctx->stream));
+        off += s->ssm_n[i];
+        SSM_HIP_TRY(hipMemcpyAsync(s->conv[i], in + off, s->conv_n[i] * 4,
+                                   hipMemcpyHostToDevice, s->m->ctx->stream));
+        off += s->conv_n[i];
+    }
+    SSM_HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_state_layer(ssm_state* s, int layer, float** ssm_p, float** conv_p) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(layer >= 0 && layer < (int)s->ssm.size(), "layer out of range");
+    if (ssm_p) *ssm_p = s->ssm[layer];
+    if (conv_p) *conv_p = s->conv[layer];
+    return SSM_OK;
+}
+
+namespace {
+
+// Prefill on device ids; leaves last-position logits in s->d_logits and argmax in d_argmax.
+ssm_status prefill_device(ssm_model* m, ssm_state* s, const uint32_t* d_ids, int L,
+                          uint32_t* d_argmax) {
+    const Dims& d = m->dm;
+    Ws w;
+    SSM_TRY(ensure_ws(m, s->B, L, false, &w));
+    SSM_TRY(trunk(m, d_ids, s->B, L, s, w));
+    SSM_TRY(ssm::launch_gather_rows(w.nrm, L, L - 1, w.last, s->B, d.d, m->ctx->stream));
+    SSM_TRY(gemm(m->ctx, s->B, d.V, d.d, w.last, d.d, m->w + m->emb, s->d_logits, d.V, 0.f));
+    if (d_argmax) SSM_TRY(ssm::launch_argmax(s->d_logits, d.V, s->B, d.V, d_argmax, m->ctx->stream));
+    return SSM_OK;
+}
+
+ssm_status finish_host(ssm_model* m, ssm_state* s, float* logits, uint32_t* argmax,
+                       const uint32_t* d_arg) {
+    hipStream_t st = m->ctx->stream;
+    if (logits)
+        SSM_HIP_TRY(hipMemcpyAsync(logits, s->d_logits, (size_t)s->B * m->dm.V * 4,
+                                   hipMemcpyDeviceToHost, st));
+    if (argmax)
+        SSM_HIP_TRY(hipMemcpyAsync(argmax, d_arg, (size_t)s->B * 4, hipMemcpyDeviceToHost, st));
+    return check_flag(m);
+}
+
+ssm_status ensure_gen(ssm_state* s, size_t n) {
+    if (n > s->gen_cap) {
+        SSM_HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
+        if (s->d_gen) SSM_HIP_TRY(hipFree(s->d_gen));
+        s->d_gen = nullptr;
+        SSM_HIP_TRY(hipMalloc((void**)&s->d_gen, n * 4));
+        s->gen_cap = n;
+    }
+    return SSM_OK;
+}
+
+}  // namespace
+
+extern "C" ssm_status ssm_prefill(ssm_model* m, ssm_state* s, const uint32_t* ids, int L,
+                                  float* last_logits, uint32_t* argmax) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(s->m == m, "state belongs to another model");
+    SSM_REQUIRE(ids && L > 0, "ssm_prefill: need at least one token");
+    const size_t T = (size_t)s->B * L;
+    SSM_TRY(ensure_ids(m, T));
+    SSM_TRY(ensure_gen(s, (size_t)s->B));
+    SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, ids, T * 4, hipMemcpyHostToDevice, m->ctx->stream));
+    SSM_TRY(prefill_device(m, s, m->d_ids, L, s->d_gen));
+    return finish_host(m, s, last_logits, argmax, s->d_gen);
+}
+
+extern "C" ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const uint32_t* d_ids,
+                                             float* d_logits, uint32_t* d_argmax) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(s->m == m && d_ids, "ssm_decode_step_device: bad args");
+    const Dims& d = m->dm;
+    Ws w;
+    SSM_TRY(ensure_ws(m, s->B, 1, false, &w));
+    SSM_TRY(trunk(m, d_ids, s->B, 1, s, w));
+    float* lg = d_logits ? d_logits : s->d_logits;
+    SSM_TRY(gemm(m->ctx, s->B, d.V, d.d, w.nrm, d.d, m->w + m->emb, lg, d.V, 0.f));
+    if (d_argmax) SSM_TRY(ssm::launch_argmax(lg, d.V, s->B, d.V, d_argmax, m->ctx->stream));
+    return SSM_OK;
+}
+
+extern "C" ssm_status ssm_decode_step(ssm_model* m, ssm_state* s, const uint32_t* ids,
+                                      float* logits, uint32_t* argmax) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(s->m == m && ids, "ssm_decode_step: bad args");
+    SSM_TRY(ensure_gen(s, (size_t)s->B));
+    SSM_HIP_TRY(hipMemcpyAsync(s->d_tok, ids, (size_t)s->B * 4, hipMemcpyHostToDevice,
+                               m->ctx->stream));
+    SSM_TRY(ssm_decode_step_device(m, s, s->d_tok, nullptr, s->d_gen));
+    return finish_host(m, s, logits, argmax, s->d_gen);
+}
+
+extern "C" ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint32_t* prompt,
+                                          int Lp, int n_new, uint32_t* out_ids) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(s->m == m && prompt && Lp > 0 && n_new >= 0 && (out_ids || n_new == 0),
+                "ssm_generate_greedy: bad args");
+    if (n_new == 0) return SSM_OK;
+    const int B = s->B;
+    const size_t T = (size_t)B * Lp;
+    SSM_TRY(ensure_ids(m, T));
+    SSM_TRY(ensure_gen(s, (size_t)n_new * B));
+    hipStream_t st = m->ctx->stream;
+    SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, prompt, T * 4, hipMemcpyHostToDevice, st));
+    SSM_TRY(prefill_device(m, s, m->d_ids, Lp, s->d_gen));
+    for (int k = 1; k < n_new; ++k)
+        SSM_TRY(ssm_decode_step_device(m, s, s->d_gen + (size_t)(k - 1) * B, nullptr,
+                                       s->d_gen + (size_t)k * B));
+    std::vector<uint32_t> tmp((size_t)n_new * B);
+    SSM_HIP_TRY(hipMemcpyAsync(tmp.data(), s->d_gen, tmp.size() * 4, hipMemcpyDeviceToHost, st));
+    SSM_TRY(check_flag(m));
+    for (int b = 0; b < B; ++b)
+        for (int k = 0; k < n_new; ++k) out_ids[(size_t)b * n_new + k] = tmp[(size_t)k * B + b];
+    return SSM_OK;
+}

@@ -1,0 +1,704 @@
+// K3-K6: Mamba-2 SSD prefill (Dao & Gu 2024, section 6) for gfx950, and K7: the one-token
+// Mamba-2 state update.
+//
+// One workgroup (4 waves) owns one (batch, head, segment) and walks the segment's chunks in
+// order with the P x N state held in MFMA accumulator registers, so the chunk-state tensor is
+// never written to HBM. Per chunk of Q = 64 steps:
+//   dt/decay  wave 0 computes dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix sum
+//             of dt' * A_h over the chunk with a 64-lane shuffle scan.
+//   staging   X^T, (X * w)^T with w_j = exp(acum_end - acum_j) dt'_j, B and B^T go to LDS as
+//             bf16 (hi, plus lo when SPLIT); each wave keeps its 16 rows of C in registers.
+//   Y_off     Y^T[p,i] = exp(acum_i) * sum_n S[p,n] C[i,n]              (MFMA, K = N)
+//   Y_diag    S^T[j,i] = sum_n B[j,n] C[i,n]; mask j <= i; * exp(acum_i - acum_j) dt'_j;
+//             Y^T[p,i] += sum_j X^T[p,j] S^T[j,i]                          (MFMA, K = N, Q)
+//   output    y[i,p] = Y^T[p,i] + D_h x[i,p]
+//   state     S = exp(acum_end) S + (X w)^T B                             (MFMA, K = Q)
+// MFMA is v_mfma_f32_16x16x32_bf16 with fp32 accumulation. SPLIT (float inputs) writes each
+// operand as hi = bf16(v), lo = bf16(v - hi) and accumulates hi*hi + hi*lo + lo*hi, which keeps
+// about 16 mantissa bits of every product.
+//
+// The internal chunk (Q = 64) is independent of the model's chunkLen: the chunked algorithm
+// is exact for any chunk length. Long single sequences are cut into segments so that
+// B*H*segments workgroups fill the chip: a state-only pass gives each segment's local final
+// state and total decay, a combine pass turns them into each segment's entering state, and
+// the full pass starts each segment from it.
+#include "common.hpp"
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int Q = 64;     // internal chunk length
+constexpr int P = 64;     // head dim handled by this kernel
+constexpr int PADB = 8;   // bf16 row padding in LDS (16 bytes) against bank conflicts
+constexpr int kTargetWG = 512;
+
+struct SsdArgs {
+    const void* x; long ldx;
+    const float* dt; long lddt;
+    const float* dt_bias; int softplus; float dt_min, dt_max;
+    const float* A;
+    const void* Bm; long ldb;
+    const void* Cm; long ldc;
+    const float* Dsk;
+    float* y; long ldy;
+    int B, L, H, G, N;
+    int nchunks, nseg, chunks_per_seg;
+    const float* h0;        // (B,H,P,N) or null
+    float* hT;              // (B,H,P,N) or null
+    float* seg_state;       // (B,H,nseg,P,N): local final state, then entering state
+    float* seg_decay;       // (B,H,nseg): sum of dt' A over the segment
+    int remap;              // XCD-aware workgroup order
+};
+
+__device__ __forceinline__ floatx4 mfma(bf16x8 a, bf16x8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float ld1(const T* p);
+template <>
+__device__ __forceinline__ float ld1<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float ld1<__bf16>(const __bf16* p) { return (float)*p; }
+
+// Load n (4 or 8) consecutive elements as floats.
+template <typename T, int n>
+__device__ __forceinline__ void ldv(const T* p, float* out) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < n; i += 4) {
+            float4 v = *reinterpret_cast<const float4*>(p + i);
+            out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
+        }
+    } else {
+        if constexpr (n == 8) {
+            bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) out[i] = (float)v[i];
+        } else {
+            bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[i] = (float)v[i];
+        }
+    }
+}
+
+__device__ __forceinline__ __bf16 hi_of(float v) { return (__bf16)v; }
+__device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v - (float)h); }
+
+template <bool SPLIT, int NN, bool FULL>
+struct Smem {
+    static constexpr int NS = SPLIT ? 2 : 1;
+    __bf16 bt[NS][NN][Q + PADB];       // B^T   (n, j)
+    __bf16 xwt[NS][P][Q + PADB];       // (X w)^T (p, j)
+    __bf16 b[FULL ? NS : 1][FULL ? Q : 1][NN + PADB];    // B (j, n)
+    __bf16 xt[FULL ? NS : 1][FULL ? P : 1][Q + PADB];    // X^T (p, j)
+    __bf16 s[FULL ? NS : 1][FULL ? P : 1][NN + PADB];    // state (p, n)
+    float dt[Q];
+    float ac[Q];
+};
+
+template <typename TIN, bool SPLIT, int NN, bool FULL>
+__global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
+    __shared__ Smem<SPLIT, NN, FULL> sm;
+    constexpr int NB = NN / 16;   // state n-blocks per wave
+    constexpr int KS = NN / 32;   // k-steps over n
+
+    int wg = blockIdx.x;
+    if (a.remap) {
+        const int per = gridDim.x / 8;
+        wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    }
+    const int seg = wg % a.nseg;
+    const int bh = wg / a.nseg;
+    const int h = bh % a.H, b = bh / a.H;
+    const int g = h / (a.H / a.G);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, q4 = lane >> 4;
+
+    const TIN* X = reinterpret_cast<const TIN*>(a.x);
+    const TIN* Bp = reinterpret_cast<const TIN*>(a.Bm) + (long)g * a.N;
+    const TIN* Cp = reinterpret_cast<const TIN*>(a.Cm) + (long)g * a.N;
+    const float Ah = a.A[h];
+    const float dtb = a.dt_bias ? a.dt_bias[h] : 0.f;
+    const float Dh = a.Dsk ? a.Dsk[h] : 0.f;
+
+    const int c_begin = seg * a.chunks_per_seg;
+    const int c_end = min(c_begin + a.chunks_per_seg, a.nchunks);
+
+    // ---- entering state -> accumulators (wave w: rows p = 16w + 4*q4 + r, cols 16nb + l16)
+    const float* init = nullptr;
+    if (FULL) {
+        if (a.nseg > 1) init = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
+        else if (a.h0) init = a.h0 + (long)bh * P * NN;
+    }
+    floatx4 S[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            S[nb][r] = init ? init[(long)(16 * w + 4 * q4 + r) * NN + 16 * nb + l16] : 0.f;
+    bool state_live = init != nullptr;
+    float decay_sum = 0.f;
+
+    auto write_state_lds = [&]() {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = S[nb][r];
+                const __bf16 hv = hi_of(v);
+                sm.s[0][16 * w + 4 * q4 + r][16 * nb + l16] = hv;
+                if constexpr (SPLIT) sm.s[SPLIT ? 1 : 0][16 * w + 4 * q4 + r][16 * nb + l16] = lo_of(v, hv);
+            }
+    };
+    if (FULL && state_live) write_state_lds();
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int t0 = c * Q;
+        const int qv = min(Q, a.L - t0);
+        const long row0 = (long)b * a.L + t0;
+
+        // ---- dt' and inclusive prefix of dt' * A over the chunk (wave 0)
+        if (w == 0) {
+            float dv = 0.f, av = 0.f;
+            if (lane < qv) {
+                dv = a.dt[(row0 + lane) * a.lddt + h] + dtb;
+                if (a.softplus) dv = ssm::softplus(dv);
+                dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
+                av = dv * Ah;
+            }
+            float s = av;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float o = __shfl_up(s, off, 64);
+                if (lane >= off) s += o;
+            }
+            sm.dt[lane] = dv;
+            sm.ac[lane] = s;
+        }
+        __syncthreads();
+        const float acend = sm.ac[Q - 1];
+        decay_sum += acend;
+
+        // ---- stage X: item (jp, pg) covers rows 2jp, 2jp+1 and p = 4pg..4pg+3
+#pragma unroll
+        for (int pass = 0; pass < (Q / 2) * (P / 4) / 256; ++pass) {
+            const int idx = pass * 256 + tid;
+            const int pg = idx % (P / 4), jp = idx / (P / 4);
+            const int j0 = 2 * jp;
+            float x0[4] = {0.f, 0.f, 0.f, 0.f}, x1[4] = {0.f, 0.f, 0.f, 0.f};
+            if (j0 < qv) ldv<TIN, 4>(X + (row0 + j0) * a.ldx + (long)h * P + 4 * pg, x0);
+            if (j0 + 1 < qv) ldv<TIN, 4>(X + (row0 + j0 + 1) * a.ldx + (long)h * P + 4 * pg, x1);
+            const float w0 = ssm::ex2((acend - sm.ac[j0]) * ssm::kLog2e) * sm.dt[j0];
+            const float w1 = ssm::ex2((acend - sm.ac[j0 + 1]) * ssm::kLog2e) * sm.dt[j0 + 1];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int p = 4 * pg + k;
+                const float u0 = x0[k] * w0, u1 = x1[k] * w1;
+                bf16x2 hw = {hi_of(u0), hi_of(u1)};
+                *reinterpret_cast<bf16x2*>(&sm.xwt[0][p][j0]) = hw;
+                if constexpr (SPLIT) {
+                    bf16x2 lw = {lo_of(u0, hw[0]), lo_of(u1, hw[1])};
+                    *reinterpret_cast<bf16x2*>(&sm.xwt[SPLIT ? 1 : 0][p][j0]) = lw;
+                }
+                if constexpr (FULL) {
+                    bf16x2 hx = {hi_of(x0[k]), hi_of(x1[k])};
+                    *reinterpret_cast<bf16x2*>(&sm.xt[0][p][j0]) = hx;
+                    if constexpr (SPLIT) {
+                        bf16x2 lx = {lo_of(x0[k], hx[0]), lo_of(x1[k], hx[1])};
+                        *reinterpret_cast<bf16x2*>(&sm.xt[SPLIT ? 1 : 0][p][j0]) = lx;
+                    }
+                }
+            }
+        }
+        // ---- stage B: item (jp, ng) covers rows 2jp, 2jp+1 and n = 8ng..8ng+7
+#pragma unroll
+        for (int pass = 0; pass < (Q / 2) * (NN / 8) / 256; ++pass) {
+            const int idx = pass * 256 + tid;
+            const int ng = idx % (NN / 8), jp = idx / (NN / 8);
+            const int j0 = 2 * jp;
+            float b0[8], b1[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) { b0[k] = 0.f; b1[k] = 0.f; }
+            if (j0 < qv) ldv<TIN, 8>(Bp + (row0 + j0) * a.ldb + 8 * ng, b0);
+            if (j0 + 1 < qv) ldv<TIN, 8>(Bp + (row0 + j0 + 1) * a.ldb + 8 * ng, b1);
+            bf16x8 h0v, h1v, l0v, l1v;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                h0v[k] = hi_of(b0[k]);
+                h1v[k] = hi_of(b1[k]);
+                l0v[k] = lo_of(b0[k], h0v[k]);
+                l1v[k] = lo_of(b1[k], h1v[k]);
+                bf16x2 ht = {h0v[k], h1v[k]};
+                *reinterpret_cast<bf16x2*>(&sm.bt[0][8 * ng + k][j0]) = ht;
+                if constexpr (SPLIT) {
+                    bf16x2 lt = {l0v[k], l1v[k]};
+                    *reinterpret_cast<bf16x2*>(&sm.bt[SPLIT ? 1 : 0][8 * ng + k][j0]) = lt;
+                }
+            }
+            if constexpr (FULL) {
+                *reinterpret_cast<bf16x8*>(&sm.b[0][j0][8 * ng]) = h0v;
+                *reinterpret_cast<bf16x8*>(&sm.b[0][j0 + 1][8 * ng]) = h1v;
+                if constexpr (SPLIT) {
+                    *reinterpret_cast<bf16x8*>(&sm.b[SPLIT ? 1 : 0][j0][8 * ng]) = l0v;
+                    *reinterpret_cast<bf16x8*>(&sm.b[SPLIT ? 1 : 0][j0 + 1][8 * ng]) = l1v;
+                }
+            }
+        }
+
+        if constexpr (FULL) {
+            // ---- C rows of this wave's strip: i = 16w + l16, k-slots n = 32ks + 8q4 + 0..7
+            const int ic = 16 * w + l16;
+            bf16x8 cfh[KS], cfl[KS];
+            {
+                float cv[8];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) cv[k] = 0.f;
+                    if (ic < qv) ldv<TIN, 8>(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, cv);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        cfh[ks][k] = hi_of(cv[k]);
+                        cfl[ks][k] = lo_of(cv[k], cfh[ks][k]);
+                    }
+                }
+            }
+            __syncthreads();   // staging done; state LDS written
+
+            const float aci = sm.ac[ic];
+            floatx4 Y[P / 16];
+#pragma unroll
+            for (int pb = 0; pb < P / 16; ++pb) Y[pb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+            // ---- Y_off = exp(acum_i) * S C^T
+            if (state_live) {
+#pragma unroll
+                for (int pb = 0; pb < P / 16; ++pb) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(
+                            &sm.s[0][16 * pb + l16][32 * ks + 8 * q4]);
+                        Y[pb] = mfma(ah, cfh[ks], Y[pb]);
+                        if constexpr (SPLIT) {
+                            const bf16x8 al = *reinterpret_cast<const bf16x8*>(
+                                &sm.s[SPLIT ? 1 : 0][16 * pb + l16][32 * ks + 8 * q4]);
+                            Y[pb] = mfma(ah, cfl[ks], Y[pb]);
+                            Y[pb] = mfma(al, cfh[ks], Y[pb]);
+                        }
+                    }
+                }
+                const float e = ssm::ex2(aci * ssm::kLog2e);
+#pragma unroll
+                for (int pb = 0; pb < P / 16; ++pb) Y[pb] *= e;
+            }
+
+            // ---- Y_diag over j-block pairs (2 x 16 rows of j per MFMA k-step)
+            for (int jb2 = 0; 2 * jb2 <= w; ++jb2) {
+                float sv[8];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int jb = 2 * jb2 + half;
+                    if (jb <= w) {
+                        floatx4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks) {
+                            const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(
+                                &sm.b[0][16 * jb + l16][32 * ks + 8 * q4]);
+                            st = mfma(bh_, cfh[ks], st);
+                            if constexpr (SPLIT) {
+                                const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
+                                    &sm.b[SPLIT ? 1 : 0][16 * jb + l16][32 * ks + 8 * q4]);
+                                st = mfma(bh_, cfl[ks], st);
+                                st = mfma(bl_, cfh[ks], st);
+                            }
+                        }
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int j = 16 * jb + 4 * q4 + r;
+                            sv[4 * half + r] =
+                                j <= ic ? st[r] * ssm::ex2((aci - sm.ac[j]) * ssm::kLog2e) * sm.dt[j]
+                                        : 0.f;
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sv[4 * half + r] = 0.f;
+                    }
+                }
+                bf16x8 sfh, sfl;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    sfh[k] = hi_of(sv[k]);
+                    sfl[k] = lo_of(sv[k], sfh[k]);
+                }
+#pragma unroll
+                for (int pb = 0; pb < P / 16; ++pb) {
+                    const int p = 16 * pb + l16;
+                    const bf16x4 x0 =
+                        *reinterpret_cast<const bf16x4*>(&sm.xt[0][p][32 * jb2 + 4 * q4]);
+                    const bf16x4 x1 =
+                        *reinterpret_cast<const bf16x4*>(&sm.xt[0][p][32 * jb2 + 16 + 4 * q4]);
+                    const bf16x8 xh = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                    Y[pb] = mfma(xh, sfh, Y[pb]);
+                    if constexpr (SPLIT) {
+                        const bf16x4 y0 = *reinterpret_cast<const bf16x4*>(
+                            &sm.xt[SPLIT ? 1 : 0][p][32 * jb2 + 4 * q4]);
+                        const bf16x4 y1 = *reinterpret_cast<const bf16x4*>(
+                            &sm.xt[SPLIT ? 1 : 0][p][32 * jb2 + 16 + 4 * q4]);
+                        const bf16x8 xl = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+                        Y[pb] = mfma(xh, sfl, Y[pb]);
+                        Y[pb] = mfma(xl, sfh, Y[pb]);
+                    }
+                }
+            }
+
+            // ---- y = Y + D x   (lane: row ic, p = 16pb + 4q4 + 0..3)
+            if (ic < qv) {
+                const long r = row0 + ic;
+#pragma unroll
+                for (int pb = 0; pb < P / 16; ++pb) {
+                    const int p0 = 16 * pb + 4 * q4;
+                    float xv[4];
+                    ldv<TIN, 4>(X + r * a.ldx + (long)h * P + p0, xv);
+                    float4 o;
+                    o.x = fmaf(Dh, xv[0], Y[pb][0]);
+                    o.y = fmaf(Dh, xv[1], Y[pb][1]);
+                    o.z = fmaf(Dh, xv[2], Y[pb][2]);
+                    o.w = fmaf(Dh, xv[3], Y[pb][3]);
+                    *reinterpret_cast<float4*>(a.y + r * a.ldy + (long)h * P + p0) = o;
+                }
+            }
+        } else {
+            __syncthreads();   // staging done
+        }
+
+        // ---- state: S = exp(acum_end) S + (X w)^T B
+        {
+            const float e = ssm::ex2(acend * ssm::kLog2e);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) S[nb] *= e;
+#pragma unroll
+            for (int ks = 0; ks < Q / 32; ++ks) {
+                const bf16x8 xh =
+                    *reinterpret_cast<const bf16x8*>(&sm.xwt[0][16 * w + l16][32 * ks + 8 * q4]);
+                bf16x8 xl;
+                if constexpr (SPLIT)
+                    xl = *reinterpret_cast<const bf16x8*>(
+                        &sm.xwt[SPLIT ? 1 : 0][16 * w + l16][32 * ks + 8 * q4]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(
+                        &sm.bt[0][16 * nb + l16][32 * ks + 8 * q4]);
+                    S[nb] = mfma(xh, bh_, S[nb]);
+                    if constexpr (SPLIT) {
+                        const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
+                            &sm.bt[SPLIT ? 1 : 0][16 * nb + l16][32 * ks + 8 * q4]);
+                        S[nb] = mfma(xh, bl_, S[nb]);
+                        S[nb] = mfma(xl, bh_, S[nb]);
+                    }
+                }
+            }
+        }
+        state_live = true;
+        __syncthreads();   // every wave is done reading this chunk's LDS
+        if (FULL && c + 1 < c_end) write_state_lds();
+    }
+
+    // ---- outputs of the state
+    float* out = nullptr;
+    if (FULL) {
+        if (a.hT && seg == a.nseg - 1) out = a.hT + (long)bh * P * NN;
+    } else {
+        out = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
+        if (tid == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
+    }
+    if (out) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out[(long)(16 * w + 4 * q4 + r) * NN + 16 * nb + l16] = S[nb][r];
+    }
+}
+
+// Segment entering states: slot[s] <- carry; carry = exp(decay[s]) carry + local[s].
+__global__ void ssd_seg_prefix(SsdArgs a, int PN) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)a.B * a.H * PN) return;
+    const int e = (int)(i % PN);
+    const long bh = i / PN;
+    float carry = a.h0 ? a.h0[bh * PN + e] : 0.f;
+    for (int s = 0; s < a.nseg; ++s) {
+        float* p = a.seg_state + (bh * a.nseg + s) * PN + e;
+        const float loc = (s + 1 < a.nseg) ? *p : 0.f;
+        *p = carry;
+        if (s + 1 < a.nseg)
+            carry = fmaf(ssm::ex2(a.seg_decay[bh * a.nseg + s] * ssm::kLog2e), carry, loc);
+    }
+}
+
+template <typename TIN, bool SPLIT, int NN>
+ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
+    const int nwg = a.B * a.H * a.nseg;
+    a.remap = (nwg % 8 == 0) ? 1 : 0;
+    if (a.nseg > 1) {
+        SsdArgs s1 = a;
+        ssd_kernel<TIN, SPLIT, NN, false><<<nwg, 256, 0, st>>>(s1);
+        ssm_status e = ssm::check_launch("ssd_state_pass");
+        if (e != SSM_OK) return e;
+        const long n = (long)a.B * a.H * P * NN;
+        ssd_seg_prefix<<<(unsigned)ssm::cdiv(n, 256), 256, 0, st>>>(a, P * NN);
+        e = ssm::check_launch("ssd_seg_prefix");
+        if (e != SSM_OK) return e;
+    }
+    ssd_kernel<TIN, SPLIT, NN, true><<<nwg, 256, 0, st>>>(a);
+    return ssm::check_launch("ssd_chunk_scan");
+}
+
+void plan(int B, int L, int H, int& nchunks, int& nseg, int& per) {
+    nchunks = (int)ssm::cdiv(L, Q);
+    const long bh = (long)B * H;
+    long s = ssm::cdiv(kTargetWG, bh > 0 ? bh : 1);
+    if (s > nchunks) s = nchunks;
+    if (s < 1) s = 1;
+    per = (int)ssm::cdiv(nchunks, s);
+    nseg = (int)ssm::cdiv(nchunks, per);
+}
+
+// ---------------------------------------------------------------- one-token update (K7)
+// Workgroup per (b, h): lanes run along n in float4 steps (N/4 lanes per row of the state),
+// rows p are spread over the remaining lanes and looped. y[p] reduces over the row's lanes.
+template <int LPR>
+__global__ __launch_bounds__(256) void m2_update_kernel(
+    const float* __restrict__ x, long ldx, const float* __restrict__ dt, long lddt,
+    const float* __restrict__ dt_bias, int softplus, float dt_min, float dt_max,
+    const float* __restrict__ A, const float* __restrict__ Bm, long ldb,
+    const float* __restrict__ Cm, long ldc, const float* __restrict__ Dsk,
+    const float* __restrict__ z, long ldz, float* __restrict__ y, long ldy,
+    float* __restrict__ hs, int H, int Pd, int G, int N) {
+    const int bh = blockIdx.x;
+    const int h = bh % H, b = bh / H, g = h / (H / G);
+    const int tid = threadIdx.x;
+    const int c4 = tid % LPR;           // float4 column
+    const int rsub = tid / LPR;         // row within a pass
+    constexpr int RPP = 256 / LPR;      // rows per pass
+    float dl = dt[(long)b * lddt + h] + (dt_bias ? dt_bias[h] : 0.f);
+    if (softplus) dl = ssm::softplus(dl);
+    dl = fminf(fmaxf(dl, dt_min), dt_max);
+    const float dA = ssm::ex2(dl * A[h] * ssm::kLog2e);
+    const float Dh = Dsk ? Dsk[h] : 0.f;
+    const float4 bv = *reinterpret_cast<const float4*>(Bm + (long)b * ldb + (long)g * N + 4 * c4);
+    const float4 cv = *reinterpret_cast<const float4*>(Cm + (long)b * ldc + (long)g * N + 4 * c4);
+    float* hb = hs + (long)bh * Pd * N;
+    for (int p = rsub; p < Pd; p += RPP) {
+        const float xp = x[(long)b * ldx + (long)h * Pd + p];
+        const float dx = dl * xp;
+        float4* hp = reinterpret_cast<float4*>(hb + (long)p * N) + c4;
+        float4 v = *hp;
+        v.x = fmaf(dA, v.x, dx * bv.x);
+        v.y = fmaf(dA, v.y, dx * bv.y);
+        v.z = fmaf(dA, v.z, dx * bv.z);
+        v.w = fmaf(dA, v.w, dx * bv.w);
+        *hp = v;
+        float acc = v.x * cv.x + v.y * cv.y + v.z * cv.z + v.w * cv.w;
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+        if (c4 == 0) {
+            acc = fmaf(Dh, xp, acc);
+            if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
+            y[(long)b * ldy + (long)h * Pd + p] = acc;
+        }
+    }
+}
+
+// Sequential SSD for shapes outside the MFMA kernel (head dim != 64 or d_state not 64/128):
+// the one-token update above run over the L steps of a (b, h) sequence with the state in
+// registers. Each thread owns RPT rows of the state (RPT <= 8) in float4 columns.
+template <typename TIN, int LPR>
+__global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, int Pd) {
+    constexpr int RPP = 256 / LPR;
+    constexpr int MAXR = 8;
+    const int bh = blockIdx.x;
+    const int h = bh % a.H, b = bh / a.H, g = h / (a.H / a.G);
+    const int tid = threadIdx.x, c4 = tid % LPR, rsub = tid / LPR;
+    const int N = a.N;
+    const bool col_ok = 4 * c4 < N;
+    const TIN* X = reinterpret_cast<const TIN*>(a.x);
+    const TIN* Bp = reinterpret_cast<const TIN*>(a.Bm) + (long)g * N;
+    const TIN* Cp = reinterpret_cast<const TIN*>(a.Cm) + (long)g * N;
+    const float Ah = a.A[h], dtb = a.dt_bias ? a.dt_bias[h] : 0.f, Dh = a.Dsk ? a.Dsk[h] : 0.f;
+    float4 st[MAXR];
+#pragma unroll
+    for (int k = 0; k < MAXR; ++k) {
+        const int p = rsub + k * RPP;
+        st[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (a.h0 && p < Pd && col_ok) {
+            const float* src = a.h0 + ((long)bh * Pd + p) * N + 4 * c4;
+            st[k] = make_float4(src[0], src[1], src[2], src[3]);
+        }
+    }
+    for (int t = 0; t < a.L; ++t) {
+        const long r = (long)b * a.L + t;
+        float dl = a.dt[r * a.lddt + h] + dtb;
+        if (a.softplus) dl = ssm::softplus(dl);
+        dl = fminf(fmaxf(dl, a.dt_min), a.dt_max);
+        const float dA = ssm::ex2(dl * Ah * ssm::kLog2e);
+        float bv[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (col_ok)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                bv[i] = ld1<TIN>(Bp + r * a.ldb + 4 * c4 + i);
+                cv[i] = ld1<TIN>(Cp + r * a.ldc + 4 * c4 + i);
+            }
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) {
+            const int p = rsub + k * RPP;
+            if (p >= Pd) break;
+            const float xp = ld1<TIN>(X + r * a.ldx + (long)h * Pd + p);
+            const float dx = dl * xp;
+            float4& v = st[k];
+            v.x = fmaf(dA, v.x, dx * bv[0]);
+            v.y = fmaf(dA, v.y, dx * bv[1]);
+            v.z = fmaf(dA, v.z, dx * bv[2]);
+            v.w = fmaf(dA, v.w, dx * bv[3]);
+            float acc = v.x * cv[0] + v.y * cv[1] + v.z * cv[2] + v.w * cv[3];
+#pragma unroll
+            for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+            if (c4 == 0) a.y[r * a.ldy + (long)h * Pd + p] = fmaf(Dh, xp, acc);
+        }
+    }
+    if (a.hT) {
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) {
+            const int p = rsub + k * RPP;
+            if (p < Pd && col_ok) {
+                float* dst = a.hT + ((long)bh * Pd + p) * N + 4 * c4;
+                dst[0] = st[k].x; dst[1] = st[k].y; dst[2] = st[k].z; dst[3] = st[k].w;
+            }
+        }
+    }
+}
+
+template <typename TIN>
+ssm_status launch_ssd_seq(SsdArgs& a, int Pd, hipStream_t st) {
+    if (a.N % 4 != 0)
+        return ssm::fail(SSM_ERR_UNSUPPORTED, "ssd: d_state %d is not a multiple of 4", a.N);
+    const int lpr = a.N / 4;
+    int L2 = 1;
+    while (L2 < lpr) L2 <<= 1;
+    if (L2 > 64 || Pd > 8 * (256 / L2))
+        return ssm::fail(SSM_ERR_UNSUPPORTED, "ssd: head dim %d with d_state %d is too large", Pd,
+                         a.N);
+    const unsigned grid = (unsigned)(a.B * a.H);
+    switch (L2) {
+        case 1: ssd_seq_kernel<TIN, 1><<<grid, 256, 0, st>>>(a, Pd); break;
+        case 2: ssd_seq_kernel<TIN, 2><<<grid, 256, 0, st>>>(a, Pd); break;
+        case 4: ssd_seq_kernel<TIN, 4><<<grid, 256, 0, st>>>(a, Pd); break;
+        case 8: ssd_seq_kernel<TIN, 8><<<grid, 256, 0, st>>>(a, Pd); break;
+        case 16: ssd_seq_kernel<TIN, 16><<<grid, 256, 0, st>>>(a, Pd); break;
+        case 32: ssd_seq_kernel<TIN, 32><<<grid, 256, 0, st>>>(a, Pd); break;
+        default: ssd_seq_kernel<TIN, 64><<<grid, 256, 0, st>>>(a, Pd); break;
+    }
+    return ssm::check_launch("ssd_seq");
+}
+
+}  // namespace
+
+extern "C" size_t ssm_ssd_workspace(int B, int L, int H, int Pd, int G, int N) {
+    (void)G;
+    if (B <= 0 || L <= 0 || H <= 0 || Pd != P || (N != 64 && N != 128)) return 0;
+    int nchunks, nseg, per;
+    plan(B, L, H, nchunks, nseg, per);
+    if (nseg <= 1) return 0;
+    return sizeof(float) * (size_t)B * H * nseg * ((size_t)Pd * N + 1);
+}
+
+extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, const float* dt,
+                                         long lddt, const float* dt_bias, int softplus,
+                                         float dt_min, float dt_max, const float* A,
+                                         const void* Bm, long ldb, const void* Cm, long ldc,
+                                         const float* Dsk, float* y, long ldy, int B, int L,
+                                         int H, int Pd, int G, int N, const float* h0,
+                                         float* hT, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+    SSM_REQUIRE(x && dt && A && Bm && Cm && y, "ssm_ssd_chunk_scan: null input");
+    SSM_REQUIRE(in_dtype == SSM_F32 || in_dtype == SSM_BF16, "ssm_ssd_chunk_scan: bad dtype");
+    SSM_REQUIRE(B >= 0 && L >= 0 && H > 0 && G > 0 && H % G == 0 && Pd > 0 && N > 0,
+                "ssm_ssd_chunk_scan: bad shape");
+    const bool mfma_path = Pd == P && (N == 64 || N == 128);
+    const long ev = in_dtype == SSM_F32 ? 4 : 8;   // vector-load element alignment
+    SSM_REQUIRE(ldx >= (long)H * Pd && ldb >= (long)G * N && ldc >= (long)G * N &&
+                    ldy >= (long)H * Pd && lddt >= H,
+                "ssm_ssd_chunk_scan: row stride below row width");
+    if (mfma_path)
+        SSM_REQUIRE(ldx % 4 == 0 && ldy % 4 == 0 && ldb % ev == 0 && ldc % ev == 0 &&
+                        (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
+                        (uintptr_t)Bm % 16 == 0 && (uintptr_t)Cm % 16 == 0,
+                    "ssm_ssd_chunk_scan: x/B/C/y rows must be 16-byte aligned");
+    if (B == 0) return SSM_OK;
+    if (L == 0) {
+        if (hT) {
+            const size_t bytes = sizeof(float) * (size_t)B * H * P * N;
+            if (h0) SSM_HIP_TRY(hipMemcpyAsync(hT, h0, bytes, hipMemcpyDeviceToDevice,
+                                               (hipStream_t)stream));
+            else SSM_HIP_TRY(hipMemsetAsync(hT, 0, bytes, (hipStream_t)stream));
+        }
+        return SSM_OK;
+    }
+    SsdArgs a{};
+    a.x = x; a.ldx = ldx; a.dt = dt; a.lddt = lddt; a.dt_bias = dt_bias; a.softplus = softplus;
+    a.dt_min = dt_min; a.dt_max = dt_max; a.A = A; a.Bm = Bm; a.ldb = ldb; a.Cm = Cm;
+    a.ldc = ldc; a.Dsk = Dsk; a.y = y; a.ldy = ldy; a.B = B; a.L = L; a.H = H; a.G = G; a.N = N;
+    a.h0 = h0; a.hT = hT;
+    hipStream_t st = (hipStream_t)stream;
+    if (!mfma_path)
+        return in_dtype == SSM_F32 ? launch_ssd_seq<float>(a, Pd, st)
+                                   : launch_ssd_seq<__bf16>(a, Pd, st);
+    plan(B, L, H, a.nchunks, a.nseg, a.chunks_per_seg);
+    if (a.nseg > 1) {
+        const size_t need = ssm_ssd_workspace(B, L, H, Pd, G, N);
+        SSM_REQUIRE(workspace && workspace_bytes >= need,
+                    "ssm_ssd_chunk_scan: workspace of %zu bytes needed", need);
+        a.seg_state = (float*)workspace;
+        a.seg_decay = a.seg_state + (size_t)B * H * a.nseg * P * N;
+    }
+    if (in_dtype == SSM_F32)
+        return N == 128 ? launch_ssd<float, true, 128>(a, st) : launch_ssd<float, true, 64>(a, st);
+    return N == 128 ? launch_ssd<__bf16, false, 128>(a, st) : launch_ssd<__bf16, false, 64>(a, st);
+}
+
+extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float* dt, long lddt,
+                                          const float* dt_bias, int softplus, float dt_min,
+                                          float dt_max, const float* A, const float* Bm,
+                                          long ldb, const float* Cm, long ldc, const float* Dsk,
+                                          const float* z, long ldz, float* y, long ldy, float* h,
+                                          int B, int H, int Pd, int G, int N, void* stream) {
+    SSM_REQUIRE(x && dt && A && Bm && Cm && y && h, "ssm_m2_state_update: null input");
+    SSM_REQUIRE(B >= 0 && H > 0 && G > 0 && H % G == 0 && Pd > 0, "ssm_m2_state_update: bad shape");
+    if (!(N == 8 || N == 16 || N == 32 || N == 64 || N == 128 || N == 256))
+        return ssm::fail(SSM_ERR_UNSUPPORTED, "ssm_m2_state_update: d_state %d not in {8..256}", N);
+    SSM_REQUIRE(ldb % 4 == 0 && ldc % 4 == 0 && (uintptr_t)Bm % 16 == 0 &&
+                    (uintptr_t)Cm % 16 == 0 && (uintptr_t)h % 16 == 0,
+                "ssm_m2_state_update: B/C/state must be 16-byte aligned");
+    if (B == 0) return SSM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = (unsigned)(B * H);
+#define M2U(LPR)                                                                               \
+    m2_update_kernel<LPR><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus, dt_min,   \
+                                                dt_max, A, Bm, ldb, Cm, ldc, Dsk, z, ldz, y,   \
+                                                ldy, h, H, Pd, G, N)
+    switch (N / 4) {
+        case 2: M2U(2); break;
+        case 4: M2U(4); break;
+        case 8: M2U(8); break;
+        case 16: M2U(16); break;
+        case 32: M2U(32); break;
+        default: M2U(64); break;
+    }
+#undef M2U
+    return ssm::check_launch("m2_state_update");
+}

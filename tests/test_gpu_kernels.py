@@ -1,0 +1,315 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Tolerances (max |gpu - oracle| / max(1, max |oracle|)):
+  fp32 kernels            1e-4   (north_star: max rel err <= 1e-4 fp32)
+  SSD with bf16 inputs    2e-2   (north_star: <= 2e-2 for the bf16 SSD variant); the oracle
+                                  gets the same bf16-rounded inputs as float32.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+from oracle import oracle as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from ssmjs_amd import kernels  # noqa: F401
+
+
+def K():
+    from ssmjs_amd import kernels
+    return kernels
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def err(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max()) / max(1.0, float(np.abs(b).max()))
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------------- conv1d
+
+@pytest.mark.parametrize("B,L,C,K,strided,with_state", [
+    (1, 256, 512, 4, False, False),    # config 1 shape
+    (2, 37, 96, 4, True, True),
+    (3, 5, 10, 3, False, True),        # C not a multiple of 4 -> scalar path; L < 16
+    (1, 2, 8, 4, False, True),         # L < K-1: state shift through the carried state
+])
+def test_conv1d_matches_oracle(B, L, C, K, strided, with_state):
+    case(f"conv1d B={B} L={L} C={C} K={K} strided={strided} state={with_state}")
+    r = rng(1000 + L)
+    x = r.standard_normal((B, L, 2 * C if strided else C)).astype(np.float32)
+    w = r.uniform(-0.5, 0.5, (C, K)).astype(np.float32)
+    b = r.uniform(-0.5, 0.5, C).astype(np.float32)
+    st = r.standard_normal((B, C, K - 1)).astype(np.float32) if with_state else None
+    xs = x[:, :, :C]
+    ref, ref_st = O.causal_conv1d(xs, w, b, state_in=st, return_state=True)
+    xd = dev(x)
+    sd = dev(st) if with_state else None
+    sout = dev(np.zeros((B, C, K - 1), np.float32))
+    y = K().causal_conv1d(xd[:, :, :C], dev(w), dev(b), True, sd, sout)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(sout), ref_st) <= F32_TOL
+
+
+def test_conv1d_state_in_place():
+    case("conv1d state_out aliasing state_in")
+    r = rng(5)
+    B, L, C, Kk = 2, 9, 64, 4
+    x = r.standard_normal((B, L, C)).astype(np.float32)
+    w = r.uniform(-0.5, 0.5, (C, Kk)).astype(np.float32)
+    st = r.standard_normal((B, C, Kk - 1)).astype(np.float32)
+    ref, ref_st = O.causal_conv1d(x, w, None, state_in=st, return_state=True)
+    sd = dev(st)
+    y = K().causal_conv1d(dev(x), dev(w), None, True, sd, sd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(sd), ref_st) <= F32_TOL
+
+
+def test_conv1d_update_matches_oracle():
+    case("conv1d_update")
+    r = rng(6)
+    B, C, Kk = 5, 200, 4
+    x = r.standard_normal((B, C)).astype(np.float32)
+    w = r.uniform(-0.5, 0.5, (C, Kk)).astype(np.float32)
+    b = r.uniform(-0.5, 0.5, C).astype(np.float32)
+    st = r.standard_normal((B, C, Kk - 1)).astype(np.float32)
+    ref, ref_st = O.conv_update(x, w, b, st)
+    sd = dev(st)
+    y = K().conv1d_update(dev(x), dev(w), dev(b), sd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(sd), ref_st) <= F32_TOL
+
+
+# ------------------------------------------------------------------------- Mamba-1 scan
+
+def _scan_inputs(r, B, L, D, N, s4d=False):
+    u = r.standard_normal((B, L, D)).astype(np.float32)
+    z = r.standard_normal((B, L, D)).astype(np.float32)
+    Bm = r.standard_normal((B, L, N)).astype(np.float32)
+    Cm = r.standard_normal((B, L, N)).astype(np.float32)
+    dt = (0.5 * r.standard_normal((B, L, D)) - 1.0).astype(np.float32)
+    if s4d:
+        A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
+    else:
+        A = -np.exp(0.5 * r.standard_normal((D, N))).astype(np.float32)
+    return u, z, Bm, Cm, dt, A
+
+
+def test_scan_config1():
+    """Config 1: B=1, L=256, D=512, N=16, A=-[1..16], D=1, dt=softplus(0.5 N(0,1) - 1)."""
+    case("selective_scan config1")
+    r = rng(1001)
+    u, z, Bm, Cm, dt, A = _scan_inputs(r, 1, 256, 512, 16, s4d=True)
+    Dk = np.ones(512, np.float32)
+    ref, hT = O.selective_scan(u, dt, A, Bm, Cm, Dk, z, None, True, return_state=True)
+    hd = torch.zeros(1, 512, 16, device="cuda")
+    y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), None, True,
+                           None, hd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), hT) <= F32_TOL
+
+
+@pytest.mark.parametrize("B,L,D,N,h0", [(2, 300, 100, 8, True), (3, 1, 64, 16, True),
+                                        (1, 97, 130, 32, False), (2, 64, 64, 64, True)])
+def test_scan_shapes(B, L, D, N, h0):
+    case(f"selective_scan B={B} L={L} D={D} N={N} h0={h0}")
+    r = rng(2000 + D)
+    u, z, Bm, Cm, dt, A = _scan_inputs(r, B, L, D, N)
+    Dk = r.standard_normal(D).astype(np.float32)
+    db = (0.1 * r.standard_normal(D)).astype(np.float32)
+    h0a = (0.3 * r.standard_normal((B, D, N))).astype(np.float32) if h0 else None
+    ref, hT = O.selective_scan(u, dt, A, Bm, Cm, Dk, z, db, True, h0=h0a, return_state=True)
+    hd = torch.zeros(B, D, N, device="cuda")
+    y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), dev(db),
+                           True, dev(h0a) if h0 else None, hd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), hT) <= F32_TOL
+
+
+def test_scan_strided_views():
+    """B, C and dt as column slices of one (B,L,R+2N) buffer, z as a slice of xz."""
+    case("selective_scan strided")
+    r = rng(3)
+    B, L, D, N, R = 2, 70, 96, 16, 6
+    u, z, _, _, dt, A = _scan_inputs(r, B, L, D, N)
+    dbl = r.standard_normal((B, L, R + 2 * N)).astype(np.float32)
+    xz = np.concatenate([u, z], axis=2)
+    ref = O.selective_scan(u, dt, A, dbl[:, :, R:R + N], dbl[:, :, R + N:], None, z)
+    dd, xzd = dev(dbl), dev(xz)
+    y = K().selective_scan(xzd[:, :, :D], dev(dt), dev(A), dd[:, :, R:R + N], dd[:, :, R + N:],
+                           None, xzd[:, :, D:])
+    assert err(host(y), ref) <= F32_TOL
+
+
+def test_m1_state_update():
+    case("m1_state_update")
+    r = rng(8)
+    B, D, N = 4, 300, 16
+    h0 = r.standard_normal((B, D, N)).astype(np.float32)
+    x, dt, z = (r.standard_normal((B, D)).astype(np.float32) for _ in range(3))
+    Bm, Cm = (r.standard_normal((B, N)).astype(np.float32) for _ in range(2))
+    A = -np.exp(0.3 * r.standard_normal((D, N))).astype(np.float32)
+    Dk, db = r.standard_normal(D).astype(np.float32), r.standard_normal(D).astype(np.float32)
+    ref, href = O.m1_state_update(x, dt, A, Bm, Cm, Dk, z, db, h0)
+    hd = dev(h0)
+    y = K().m1_state_update(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), dev(db), hd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), href) <= F32_TOL
+
+
+# ------------------------------------------------------------------------- Mamba-2 SSD
+
+def _ssd_inputs(r, B, L, H, P, G, N, bc_scale=1.0):
+    x = r.standard_normal((B, L, H, P)).astype(np.float32)
+    dt = (r.standard_normal((B, L, H)) - 3.0).astype(np.float32)   # config 3: softplus(N(0,1)-3)
+    A = -r.uniform(1.0, 16.0, H).astype(np.float32)                 # A_log ~ log U(1,16)
+    Bm = (bc_scale * r.standard_normal((B, L, G, N))).astype(np.float32)
+    Cm = (bc_scale * r.standard_normal((B, L, G, N))).astype(np.float32)
+    Dk = r.standard_normal(H).astype(np.float32)
+    return x, dt, A, Bm, Cm, Dk
+
+
+def _bf(a):
+    return torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("B,L,H,G,N,h0,dtype", [
+    (2, 200, 4, 1, 128, True, "f32"),
+    (1, 64, 2, 2, 64, False, "f32"),
+    (2, 131, 3, 1, 64, True, "bf16"),
+    (2, 256, 4, 1, 128, False, "bf16"),
+    (1, 5, 2, 1, 128, True, "f32"),
+])
+def test_ssd_matches_oracle(B, L, H, G, N, h0, dtype):
+    case(f"ssd B={B} L={L} H={H} G={G} N={N} h0={h0} {dtype}")
+    r = rng(3000 + L)
+    P = 64
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
+    db = (0.1 * r.standard_normal(H)).astype(np.float32)
+    h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32) if h0 else None
+    tdt = torch.float32
+    if dtype == "bf16":
+        x, Bm, Cm = _bf(x), _bf(Bm), _bf(Cm)
+        tdt = torch.bfloat16
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, dt_bias=db, h0=h0a, return_state=True)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x, tdt), dev(dt), dev(A), dev(Bm, tdt), dev(Cm, tdt), dev(Dk),
+                           dev(db), True, h0=dev(h0a) if h0 else None, hT=hd)
+    tol = F32_TOL if dtype == "f32" else BF16_TOL
+    e1, e2 = err(host(y), ref), err(host(hd), hT)
+    print(f"  y err {e1:.2e}  state err {e2:.2e}")
+    assert e1 <= tol
+    assert e2 <= tol
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ssd_long_sequence_segments(dtype):
+    """B*H small -> the sequence is cut into segments (state pass + combine + full pass)."""
+    case(f"ssd segmented {dtype}")
+    r = rng(4000)
+    B, L, H, G, N, P = 1, 64 * 40 + 17, 2, 1, 128, 64
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N, bc_scale=128 ** -0.25)
+    h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32)
+    tdt = torch.float32
+    if dtype == "bf16":
+        x, Bm, Cm = _bf(x), _bf(Bm), _bf(Cm)
+        tdt = torch.bfloat16
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, h0=h0a, return_state=True)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x, tdt), dev(dt), dev(A), dev(Bm, tdt), dev(Cm, tdt), dev(Dk),
+                           None, True, h0=dev(h0a), hT=hd)
+    tol = F32_TOL if dtype == "f32" else BF16_TOL
+    e1, e2 = err(host(y), ref), err(host(hd), hT)
+    print(f"  y err {e1:.2e}  state err {e2:.2e}")
+    assert e1 <= tol and e2 <= tol
+
+
+def test_ssd_sequential_fallback_shapes():
+    """head dim 16, d_state 16 (outside the MFMA kernel) -> sequential kernel."""
+    case("ssd fallback P=16 N=16")
+    r = rng(11)
+    B, L, H, G, N, P = 2, 45, 4, 1, 16, 16
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
+    h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32)
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, h0=h0a, return_state=True)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), None, True,
+                           h0=dev(h0a), hT=hd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), hT) <= F32_TOL
+
+
+def test_ssd_chunk_equals_decode_steps():
+    """Final state of a prefill == state reached by one-token updates (state passing)."""
+    case("ssd prefill vs m2 updates")
+    r = rng(12)
+    B, L, H, G, N, P = 2, 70, 2, 1, 128, 64
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    yp = K().ssd_chunk_scan(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), None, True, hT=hd)
+    hs = torch.zeros(B, H, P, N, device="cuda")
+    ys = []
+    for t in range(L):
+        ys.append(K().m2_state_update(dev(x[:, t]), dev(dt[:, t]), dev(A), dev(Bm[:, t]),
+                                      dev(Cm[:, t]), dev(Dk), None, hs))
+    ys = torch.stack(ys, 1)
+    assert err(host(ys), host(yp)) <= F32_TOL
+    assert err(host(hs), host(hd)) <= F32_TOL
+
+
+def test_m2_state_update():
+    case("m2_state_update")
+    r = rng(13)
+    B, H, P, G, N = 3, 8, 64, 2, 128
+    h0 = r.standard_normal((B, H, P, N)).astype(np.float32)
+    x, z = r.standard_normal((B, H, P)).astype(np.float32), r.standard_normal((B, H, P)).astype(np.float32)
+    dt = r.standard_normal((B, H)).astype(np.float32)
+    Bm, Cm = (r.standard_normal((B, G, N)).astype(np.float32) for _ in range(2))
+    A = -r.uniform(1, 16, H).astype(np.float32)
+    Dk, db = r.standard_normal(H).astype(np.float32), r.standard_normal(H).astype(np.float32)
+    ref, href = O.m2_state_update(x, dt, A, Bm, Cm, Dk, db, h0, z=z)
+    hd = dev(h0)
+    y = K().m2_state_update(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(db), hd, z=dev(z))
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), href) <= F32_TOL
+
+
+# ------------------------------------------------------------------------- norms
+
+def test_rmsnorm_and_gated():
+    case("rmsnorm / gated rmsnorm")
+    r = rng(14)
+    x, z = r.standard_normal((7, 300)).astype(np.float32), r.standard_normal((7, 300)).astype(np.float32)
+    w = r.uniform(0.5, 1.5, 300).astype(np.float32)
+    assert err(host(K().rmsnorm(dev(x), dev(w))), O.rmsnorm(x, w)) <= F32_TOL
+    for g in (1, 3):
+        ref = O.gated_rmsnorm(x, z, w, groups=g)
+        assert err(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=g)), ref) <= F32_TOL

@@ -1,0 +1,171 @@
+"""GPU parity of the model-level C ABI (forward / prefill / decode / greedy generate) against
+the CPU oracle and the HF golden fixtures, plus its error contract.
+
+Greedy ids are compared bit-exactly. The models used for greedy runs scale the embedding so
+that the oracle's top-1/top-2 logit margin stays far above the fp32 summation-order noise;
+each test asserts that minimum margin, so a pass is not luck on near-ties.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+from oracle import oracle as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+F32_TOL = 2e-4
+
+
+@pytest.fixture(scope="module")
+def device():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from ssmjs_amd import backend
+    d = backend.Device(0)
+    yield d
+    d.destroy()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def err(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max()) / max(1.0, float(np.abs(b).max()))
+
+
+def cfg_of(dims):
+    return {"vocabSize": dims.vocab, "dModel": dims.d_model, "numLayers": dims.n_layers,
+            "dState": dims.d_state, "dConv": dims.d_conv, "expand": dims.expand,
+            "nHeads": dims.n_heads, "nGroups": dims.n_groups, "dtRank": dims.dt_rank,
+            "layers": [{"type": t} for t in dims.layers]}
+
+
+@pytest.mark.parametrize("kind", ["mamba1", "mamba2"])
+def test_hf_fixture_logits(device, golden, kind):
+    case(f"hf fixture {kind}")
+    from ssmjs_amd import backend, checkpoint
+    g = golden[f"hf_model_{kind}"]
+    blob = g["blob"].tobytes()
+    dims, _ = checkpoint.unpack(blob)
+    m = backend.Model(device, cfg_of(dims))
+    m.load_weights(blob)
+    out = m.forward(g["ids"])
+    assert err(out, g["logits"]) <= F32_TOL
+    assert err(out, O.Model(blob).forward(g["ids"])) <= F32_TOL
+    m.destroy()
+
+
+def _model(device, layers, d=128, N=16, H=4, V=512, seed=7, emb_scale=40.0):
+    """Random-init GPU model; embedding scaled up for wide greedy margins. Returns (model, blob)."""
+    from ssmjs_amd import backend, checkpoint
+    cfg = {"vocabSize": V, "dModel": d, "numLayers": len(layers), "dState": N, "dConv": 4,
+           "expand": 2, "nHeads": H, "nGroups": 1, "layers": [{"type": t} for t in layers]}
+    m = backend.Model(device, cfg, seed=seed)
+    dims, T = checkpoint.unpack(m.export_weights())
+    T["embedding"] = T["embedding"] * emb_scale
+    blob = checkpoint.pack(dims, T)
+    m.load_weights(blob)
+    return m, blob
+
+
+@pytest.mark.parametrize("layers,N,H", [(["mamba1", "mamba1"], 16, 4),
+                                        (["mamba2", "mamba2"], 128, 4),
+                                        (["mamba1", "mamba2"], 64, 4)])
+def test_forward_matches_oracle(device, layers, N, H):
+    case(f"forward {layers} N={N}")
+    m, blob = _model(device, layers, N=N, H=H)
+    ids = np.random.default_rng(1).integers(0, 512, (2, 150)).astype(np.uint32)
+    out = m.forward(ids)
+    ref = O.Model(blob).forward(ids)
+    e = err(out, ref)
+    print(f"  logits err {e:.2e}")
+    assert e <= F32_TOL
+    m.destroy()
+
+
+@pytest.mark.parametrize("layers,N", [(["mamba1", "mamba1"], 16), (["mamba2", "mamba2"], 128)])
+def test_prefill_decode_state_matches_oracle(device, layers, N):
+    case(f"prefill/decode state {layers}")
+    m, blob = _model(device, layers, N=N)
+    om = O.Model(blob)
+    ids = np.random.default_rng(2).integers(0, 512, (3, 40)).astype(np.uint32)
+    st = m.new_state(3)
+    ost = om.new_state(3)
+    lg, _ = st.prefill(ids[:, :33])
+    assert err(lg, ost.prefill(ids[:, :33])) <= F32_TOL
+    assert err(st.read(), ost.read()) <= F32_TOL
+    for t in range(33, 40):
+        lg, _ = st.decode(ids[:, t])
+        assert err(lg, ost.decode(ids[:, t])) <= F32_TOL
+    assert err(st.read(), ost.read()) <= F32_TOL
+    st.destroy()
+    m.destroy()
+
+
+@pytest.mark.parametrize("layers,N", [(["mamba1"] * 4, 16), (["mamba2"] * 2, 128)])
+def test_greedy_ids_bit_exact(device, layers, N):
+    case(f"greedy {layers}")
+    m, blob = _model(device, layers, N=N)
+    prompt = np.random.default_rng(3).integers(0, 512, (4, 12)).astype(np.uint32)
+    st = m.new_state(4)
+    got = st.generate_greedy(prompt, 24)
+    ref, margins = O.greedy(O.Model(blob), prompt, 24)
+    print(f"  min top1-top2 margin {margins.min():.3e}")
+    assert margins.min() > 1e-3, "model too close to a tie for a bit-exact check"
+    np.testing.assert_array_equal(got, ref)
+    st.destroy()
+    m.destroy()
+
+
+def test_greedy_equals_reprefill(device):
+    """generate() (recurrent) == tokenStream semantics (full re-prefill each step,
+    src/session/streaming.ts:30-45) for topK = 1."""
+    case("greedy vs re-prefill")
+    m, _ = _model(device, ["mamba2", "mamba1"], N=64)
+    ids = [5, 17, 99]
+    st = m.new_state(1)
+    fast = st.generate_greedy(np.array([ids], np.uint32), 8)[0].tolist()
+    slow = list(ids)
+    for _ in range(8):
+        lg = m.forward(np.array([slow], np.uint32))[0, -1]
+        slow.append(int(np.argmax(lg)))
+    assert fast == slow[len(ids):]
+    m.destroy()
+
+
+def test_checkpoint_errors(device):
+    case("checkpoint errors")
+    from ssmjs_amd import _lib
+    m, blob = _model(device, ["mamba1"])
+    with pytest.raises(_lib.SsmError) as e:
+        m.load_weights(b"XXXX" + blob[4:])
+    assert e.value.code == "CHECKPOINT_INVALID"
+    with pytest.raises(_lib.SsmError) as e:
+        m.load_weights(blob[:-8])
+    assert e.value.code == "CHECKPOINT_INVALID"
+    f16 = m.export_weights(f16=True)
+    m.load_weights(f16)            # f16 images load (values rounded to half)
+    m.load_weights(blob)
+    with pytest.raises(_lib.SsmError):
+        m.forward(np.array([[600]], np.uint32))   # id >= vocab
+    h = m.handle
+    m.destroy()
+    ids = np.zeros((1, 1), np.uint32)
+    out = np.zeros((1, 1, 512), np.float32)
+    with pytest.raises(_lib.SsmError) as e:
+        _lib.call("ssm_forward", h, ids.ctypes.data, 1, 1, out.ctypes.data)
+    assert e.value.code == "SESSION_DESTROYED"
+
+
+def test_unsupported_layer_types(device):
+    case("unsupported layers")
+    from ssmjs_amd import _lib, backend
+    for t in ("attention", "mamba3"):
+        cfg = {"vocabSize": 10, "dModel": 16, "numLayers": 1, "dState": 8, "dConv": 4,
+               "expand": 2, "nHeads": 4, "layers": [{"type": t}]}
+        with pytest.raises(_lib.SsmError):
+            backend.Model(device, cfg)
