@@ -53,4 +53,19 @@ __device__ __forceinline__ float softplus(float x) {
 
 __device__ __forceinline__ float silu(float z) { return z / (1.f + expf(-z)); }
 
+// softplus on the hardware exp/log (v_exp_f32 / v_log_f32). Below -8 it returns e^x, whose
+// relative distance from log1p(e^x) is under e^x / 2 < 1.7e-4 of a value < 3.4e-4, i.e. an
+// absolute error below 6e-8; above 20 it returns x. In between log(1 + e^x) has
+// 1 + e^x >= 1.0003, so no cancellation.
+__device__ __forceinline__ float softplus_fast(float x) {
+    if (x > 20.f) return x;
+    const float e = __expf(x);
+    return x < -8.f ? e : __logf(1.f + e);
+}
+
+// z * sigmoid(z) with v_exp_f32 and v_rcp_f32 (about 1 ulp each).
+__device__ __forceinline__ float silu_fast(float z) {
+    return z * __builtin_amdgcn_rcpf(1.f + __expf(-z));
+}
+
 }  // namespace ssm

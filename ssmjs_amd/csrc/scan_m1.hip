@@ -2,16 +2,18 @@
 // decode update.
 //
 // Work split: one lane per channel d (64 adjacent channels per wave, so u/dt/z/y rows are
-// read and written as 256-byte runs) holding all N state entries in registers. B_t and C_t
-// are the same for every channel, so their loads are wave-uniform and the compiler issues
-// them as scalar loads. Time is cut into NC chunks so that B*D/64*NC waves fill the chip:
+// read and written as 256-byte runs) holding all N state entries in registers (N is a
+// template constant, so the state loop is straight-line code). B_t and C_t are the same for
+// every channel: their addresses are wave-uniform and the pointers are read-only restrict
+// parameters, so they are fetched with scalar loads into SGPRs. Time is cut into NC chunks
+// so that B*D/64*NC waves fill the chip:
 //   pass A  scan_chunk_state : each chunk from a zero state -> chunk-end state + sum(dt')
 //   pass B  scan_chunk_prefix: per (b,n,d) sequential combine over chunks -> state entering
 //                               each chunk (h_in[c] = exp(A*sum_dt[c-1]) h_in[c-1] + hend[c-1]),
 //                               final state
 //   pass C  scan_chunk_output: re-run each chunk from its entering state, emit y with the D
 //                               skip and SiLU(z) gate.
-// exp(dt A) is computed as exp2(dt * (A log2 e)) with A pre-scaled once per lane.
+// exp(dt A) is exp2(dt * (A log2 e)) with A pre-scaled once per lane (one v_exp_f32 each).
 #include "common.hpp"
 
 namespace {
@@ -20,111 +22,130 @@ constexpr int kWave = 64;
 constexpr int kMinChunk = 16;
 constexpr int kTargetWaves = 4096;
 
-struct ScanArgs {
-    const float* u; long ldu;
-    const float* dt; long lddt;
-    const float* dt_bias; int softplus;
-    const float* A;
-    const float* Bm; long ldb;
-    const float* Cm; long ldc;
-    const float* Dsk;
-    const float* z; long ldz;
-    float* y; long ldy;
-    int B, L, D, N;
-    int T;        // chunk length
-    int NC;       // number of chunks
-    float* hc;    // (B, NC, N, D): chunk-end state (pass A), then state entering chunk (pass B)
-    float* sdt;   // (B, NC, D): sum of dt' over the chunk
-    const float* h0;
-    float* hT;
-};
-
-__device__ __forceinline__ float delta_at(const ScanArgs& a, long r, int d, float bias) {
-    float v = a.dt[r * a.lddt + d] + bias;
-    return a.softplus ? ssm::softplus(v) : v;
+__device__ __forceinline__ float delta_of(float raw, float bias, int softplus) {
+    const float v = raw + bias;
+    return softplus ? ssm::softplus_fast(v) : v;
 }
 
-template <int NS>
-__global__ __launch_bounds__(kWave) void scan_chunk_state(ScanArgs a) {
+// N: state size the kernel is compiled for; Nr: runtime size (<= N). Entries n >= Nr get
+// A = 0 and B = C = 0 (clamped loads times a zero mask), so they stay exactly zero and add
+// nothing to y.
+template <int N, bool EXACT>
+__global__ __launch_bounds__(kWave) void scan_chunk_state(
+    const float* __restrict__ u, long ldu, const float* __restrict__ dt, long lddt,
+    const float* __restrict__ dt_bias, int softplus, const float* __restrict__ A,
+    const float* __restrict__ Bm, long ldb, int L, int D, int Nr, int T, int NC,
+    float* __restrict__ hc, float* __restrict__ sdt_out) {
     const int d = blockIdx.x * kWave + threadIdx.x;
     const int c = blockIdx.y, b = blockIdx.z;
-    if (d >= a.D) return;
-    float A2[NS], h[NS];
+    if (d >= D) return;
+    if (EXACT) Nr = N;
+    float A2[N], h[N], msk[N];
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-        A2[n] = n < a.N ? a.A[(long)d * a.N + n] * ssm::kLog2e : 0.f;
+    for (int n = 0; n < N; ++n) {
+        const int nn = EXACT ? n : (n < Nr ? n : Nr - 1);
+        msk[n] = (EXACT || n < Nr) ? 1.f : 0.f;
+        A2[n] = A[(long)d * Nr + nn] * ssm::kLog2e * msk[n];
         h[n] = 0.f;
     }
-    const float bias = a.dt_bias ? a.dt_bias[d] : 0.f;
-    const int t0 = c * a.T, t1 = min(t0 + a.T, a.L);
+    const float bias = dt_bias ? dt_bias[d] : 0.f;
+    const int t0 = c * T, t1 = min(t0 + T, L);
     float sdt = 0.f;
-    for (int t = t0; t < t1; ++t) {
-        const long r = (long)b * a.L + t;
-        const float dl = delta_at(a, r, d, bias);
-        const float du = dl * a.u[r * a.ldu + d];
+    // software pipeline: the next step's dt and u are in flight while this step computes
+    long r = (long)b * L + t0;
+    float dt_n = dt[r * lddt + d], u_n = u[r * ldu + d];
+    for (int t = t0; t < t1; ++t, ++r) {
+        const float dtc = dt_n, uc = u_n;
+        if (t + 1 < t1) {
+            dt_n = dt[(r + 1) * lddt + d];
+            u_n = u[(r + 1) * ldu + d];
+        }
+        const float dl = delta_of(dtc, bias, softplus);
+        const float du = dl * uc;
         sdt += dl;
-        const float* Br = a.Bm + r * a.ldb;
+        const float* Br = Bm + r * ldb;
 #pragma unroll
-        for (int n = 0; n < NS; ++n)
-            if (n < a.N) h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * Br[n]);
+        for (int n = 0; n < N; ++n) {
+            const float bn = EXACT ? Br[n] : Br[n < Nr ? n : Nr - 1] * msk[n];
+            h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bn);
+        }
     }
-    float* hc = a.hc + (((long)b * a.NC + c) * a.N) * a.D + d;
+    float* hp = hc + (((long)b * NC + c) * Nr) * D + d;
 #pragma unroll
-    for (int n = 0; n < NS; ++n)
-        if (n < a.N) hc[(long)n * a.D] = h[n];
-    a.sdt[((long)b * a.NC + c) * a.D + d] = sdt;
+    for (int n = 0; n < N; ++n)
+        if (n < Nr) hp[(long)n * D] = h[n];
+    sdt_out[((long)b * NC + c) * D + d] = sdt;
 }
 
 // One thread per (b, n, d); d fastest so the chunk-state rows are read coalesced.
-__global__ void scan_chunk_prefix(ScanArgs a) {
+__global__ void scan_chunk_prefix(const float* __restrict__ A, int L, int D, int N, int NC,
+                                  long total, float* __restrict__ hc,
+                                  const float* __restrict__ sdt, const float* __restrict__ h0,
+                                  float* __restrict__ hT) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)a.B * a.N * a.D) return;
-    const int d = (int)(i % a.D);
-    const int n = (int)((i / a.D) % a.N);
-    const int b = (int)(i / ((long)a.D * a.N));
-    const float A2 = a.A[(long)d * a.N + n] * ssm::kLog2e;
-    float carry = a.h0 ? a.h0[((long)b * a.D + d) * a.N + n] : 0.f;
-    for (int c = 0; c < a.NC; ++c) {
-        float* p = a.hc + (((long)b * a.NC + c) * a.N + n) * a.D + d;
+    if (i >= total) return;
+    const int d = (int)(i % D);
+    const int n = (int)((i / D) % N);
+    const int b = (int)(i / ((long)D * N));
+    const float A2 = A[(long)d * N + n] * ssm::kLog2e;
+    float carry = h0 ? h0[((long)b * D + d) * N + n] : 0.f;
+    for (int c = 0; c < NC; ++c) {
+        float* p = hc + (((long)b * NC + c) * N + n) * D + d;
         const float hend = *p;
         *p = carry;
-        carry = fmaf(ssm::ex2(A2 * a.sdt[((long)b * a.NC + c) * a.D + d]), carry, hend);
+        carry = fmaf(ssm::ex2(A2 * sdt[((long)b * NC + c) * D + d]), carry, hend);
     }
-    if (a.hT) a.hT[((long)b * a.D + d) * a.N + n] = carry;
+    if (hT) hT[((long)b * D + d) * N + n] = carry;
 }
 
-template <int NS>
-__global__ __launch_bounds__(kWave) void scan_chunk_output(ScanArgs a) {
+template <int N, bool EXACT>
+__global__ __launch_bounds__(kWave) void scan_chunk_output(
+    const float* __restrict__ u, long ldu, const float* __restrict__ dt, long lddt,
+    const float* __restrict__ dt_bias, int softplus, const float* __restrict__ A,
+    const float* __restrict__ Bm, long ldb, const float* __restrict__ Cm, long ldc,
+    const float* __restrict__ Dsk, const float* __restrict__ z, long ldz, float* __restrict__ y,
+    long ldy, int L, int D, int Nr, int T, int NC, const float* __restrict__ hc) {
     const int d = blockIdx.x * kWave + threadIdx.x;
     const int c = blockIdx.y, b = blockIdx.z;
-    if (d >= a.D) return;
-    float A2[NS], h[NS];
-    const float* hc = a.hc + (((long)b * a.NC + c) * a.N) * a.D + d;
+    if (d >= D) return;
+    if (EXACT) Nr = N;
+    float A2[N], h[N], msk[N];
+    const float* hp = hc + (((long)b * NC + c) * Nr) * D + d;
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-        A2[n] = n < a.N ? a.A[(long)d * a.N + n] * ssm::kLog2e : 0.f;
-        h[n] = n < a.N ? hc[(long)n * a.D] : 0.f;
+    for (int n = 0; n < N; ++n) {
+        const int nn = EXACT ? n : (n < Nr ? n : Nr - 1);
+        msk[n] = (EXACT || n < Nr) ? 1.f : 0.f;
+        A2[n] = A[(long)d * Nr + nn] * ssm::kLog2e * msk[n];
+        h[n] = hp[(long)nn * D] * msk[n];
     }
-    const float bias = a.dt_bias ? a.dt_bias[d] : 0.f;
-    const float Dd = a.Dsk ? a.Dsk[d] : 0.f;
-    const int t0 = c * a.T, t1 = min(t0 + a.T, a.L);
-    for (int t = t0; t < t1; ++t) {
-        const long r = (long)b * a.L + t;
-        const float dl = delta_at(a, r, d, bias);
-        const float uu = a.u[r * a.ldu + d];
+    const float bias = dt_bias ? dt_bias[d] : 0.f;
+    const float Dd = Dsk ? Dsk[d] : 0.f;
+    const int t0 = c * T, t1 = min(t0 + T, L);
+    long r = (long)b * L + t0;
+    float dt_n = dt[r * lddt + d], u_n = u[r * ldu + d], z_n = z ? z[r * ldz + d] : 0.f;
+    for (int t = t0; t < t1; ++t, ++r) {
+        const float dtc = dt_n, uu = u_n, zc = z_n;
+        if (t + 1 < t1) {
+            dt_n = dt[(r + 1) * lddt + d];
+            u_n = u[(r + 1) * ldu + d];
+            if (z) z_n = z[(r + 1) * ldz + d];
+        }
+        const float dl = delta_of(dtc, bias, softplus);
         const float du = dl * uu;
-        const float* Br = a.Bm + r * a.ldb;
-        const float* Cr = a.Cm + r * a.ldc;
+        const float* Br = Bm + r * ldb;
+        const float* Cr = Cm + r * ldc;
         float acc = 0.f;
 #pragma unroll
-        for (int n = 0; n < NS; ++n)
-            if (n < a.N) {
-                h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * Br[n]);
-                acc = fmaf(h[n], Cr[n], acc);
-            }
+        for (int n = 0; n < N; ++n) {
+            const int nn = EXACT ? n : (n < Nr ? n : Nr - 1);
+            const float bn = EXACT ? Br[n] : Br[nn] * msk[n];
+            const float cn = EXACT ? Cr[n] : Cr[nn] * msk[n];
+            h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bn);
+            acc = fmaf(h[n], cn, acc);
+        }
         acc = fmaf(Dd, uu, acc);
-        if (a.z) acc *= ssm::silu(a.z[r * a.ldz + d]);
-        a.y[r * a.ldy + d] = acc;
+        if (z) acc *= ssm::silu_fast(zc);
+        y[r * ldy + d] = acc;
     }
 }
 
@@ -136,17 +157,40 @@ int pick_chunk(int B, int L, int D) {
     return (int)T;
 }
 
-template <int NS>
-void launch_all(ScanArgs& a, hipStream_t st) {
+struct ScanArgs {
+    const float* u; long ldu;
+    const float* dt; long lddt;
+    const float* dt_bias; int softplus;
+    const float* A;
+    const float* Bm; long ldb;
+    const float* Cm; long ldc;
+    const float* Dsk;
+    const float* z; long ldz;
+    float* y; long ldy;
+    int B, L, D, N, T, NC;
+    float* hc;
+    float* sdt;
+    const float* h0;
+    float* hT;
+};
+
+template <int N, bool EXACT>
+void launch_all(const ScanArgs& a, hipStream_t st) {
     dim3 grid((unsigned)ssm::cdiv(a.D, kWave), (unsigned)a.NC, (unsigned)a.B);
-    scan_chunk_state<NS><<<grid, kWave, 0, st>>>(a);
+    scan_chunk_state<N, EXACT><<<grid, kWave, 0, st>>>(a.u, a.ldu, a.dt, a.lddt, a.dt_bias, a.softplus,
+                                                a.A, a.Bm, a.ldb, a.L, a.D, a.N, a.T, a.NC, a.hc,
+                                                a.sdt);
     const long nthr = (long)a.B * a.N * a.D;
-    scan_chunk_prefix<<<(unsigned)ssm::cdiv(nthr, 256), 256, 0, st>>>(a);
-    scan_chunk_output<NS><<<grid, kWave, 0, st>>>(a);
+    scan_chunk_prefix<<<(unsigned)ssm::cdiv(nthr, 256), 256, 0, st>>>(
+        a.A, a.L, a.D, a.N, a.NC, nthr, a.hc, a.sdt, a.h0, a.hT);
+    scan_chunk_output<N, EXACT><<<grid, kWave, 0, st>>>(a.u, a.ldu, a.dt, a.lddt, a.dt_bias,
+                                                 a.softplus, a.A, a.Bm, a.ldb, a.Cm, a.ldc,
+                                                 a.Dsk, a.z, a.ldz, a.y, a.ldy, a.L, a.D, a.N,
+                                                 a.T, a.NC, a.hc);
 }
 
 // One-token update: one thread per (b, d) with the N state entries in registers.
-template <int NS>
+template <int N>
 __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
                                  const float* __restrict__ dt, long lddt,
                                  const float* __restrict__ dt_bias, int softplus,
@@ -154,26 +198,25 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
                                  long ldb, const float* __restrict__ Cm, long ldc,
                                  const float* __restrict__ Dsk, const float* __restrict__ z,
                                  long ldz, float* __restrict__ y, long ldy,
-                                 float* __restrict__ h, int B, int D, int N) {
+                                 float* __restrict__ h, int B, int D, int Nr) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)B * D) return;
     const int b = (int)(i / D), d = (int)(i % D);
-    float dl = dt[(long)b * lddt + d] + (dt_bias ? dt_bias[d] : 0.f);
-    if (softplus) dl = ssm::softplus(dl);
+    const float dl = delta_of(dt[(long)b * lddt + d], dt_bias ? dt_bias[d] : 0.f, softplus);
     const float xx = x[(long)b * ldx + d];
     const float du = dl * xx;
-    float* hp = h + i * N;
+    float* hp = h + i * Nr;
     float acc = 0.f;
 #pragma unroll
-    for (int n = 0; n < NS; ++n)
-        if (n < N) {
-            const float v = fmaf(ssm::ex2(dl * A[(long)d * N + n] * ssm::kLog2e), hp[n],
+    for (int n = 0; n < N; ++n)
+        if (n < Nr) {
+            const float v = fmaf(ssm::ex2(dl * A[(long)d * Nr + n] * ssm::kLog2e), hp[n],
                                  du * Bm[(long)b * ldb + n]);
             hp[n] = v;
             acc = fmaf(v, Cm[(long)b * ldc + n], acc);
         }
     if (Dsk) acc = fmaf(Dsk[d], xx, acc);
-    if (z) acc *= ssm::silu(z[(long)b * ldz + d]);
+    if (z) acc *= ssm::silu_fast(z[(long)b * ldz + d]);
     y[(long)b * ldy + d] = acc;
 }
 
@@ -222,10 +265,18 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
     a.sdt = a.hc + (size_t)B * a.NC * N * D;
     a.h0 = h0; a.hT = hT;
     hipStream_t st = (hipStream_t)stream;
-    if (N <= 8) launch_all<8>(a, st);
-    else if (N <= 16) launch_all<16>(a, st);
-    else if (N <= 32) launch_all<32>(a, st);
-    else launch_all<64>(a, st);
+    switch (N) {
+        case 4: launch_all<4, true>(a, st); break;
+        case 8: launch_all<8, true>(a, st); break;
+        case 16: launch_all<16, true>(a, st); break;
+        case 32: launch_all<32, true>(a, st); break;
+        case 64: launch_all<64, true>(a, st); break;
+        default:
+            if (N < 8) launch_all<8, false>(a, st);
+            else if (N < 16) launch_all<16, false>(a, st);
+            else if (N < 32) launch_all<32, false>(a, st);
+            else launch_all<64, false>(a, st);
+    }
     return ssm::check_launch("selective_scan");
 }
 

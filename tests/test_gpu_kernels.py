@@ -56,24 +56,24 @@ def rng(seed):
 
 # ------------------------------------------------------------------------- conv1d
 
-@pytest.mark.parametrize("B,L,C,K,strided,with_state", [
+@pytest.mark.parametrize("B,L,C,Kw,strided,with_state", [
     (1, 256, 512, 4, False, False),    # config 1 shape
     (2, 37, 96, 4, True, True),
     (3, 5, 10, 3, False, True),        # C not a multiple of 4 -> scalar path; L < 16
     (1, 2, 8, 4, False, True),         # L < K-1: state shift through the carried state
 ])
-def test_conv1d_matches_oracle(B, L, C, K, strided, with_state):
-    case(f"conv1d B={B} L={L} C={C} K={K} strided={strided} state={with_state}")
+def test_conv1d_matches_oracle(B, L, C, Kw, strided, with_state):
+    case(f"conv1d B={B} L={L} C={C} K={Kw} strided={strided} state={with_state}")
     r = rng(1000 + L)
     x = r.standard_normal((B, L, 2 * C if strided else C)).astype(np.float32)
-    w = r.uniform(-0.5, 0.5, (C, K)).astype(np.float32)
+    w = r.uniform(-0.5, 0.5, (C, Kw)).astype(np.float32)
     b = r.uniform(-0.5, 0.5, C).astype(np.float32)
-    st = r.standard_normal((B, C, K - 1)).astype(np.float32) if with_state else None
+    st = r.standard_normal((B, C, Kw - 1)).astype(np.float32) if with_state else None
     xs = x[:, :, :C]
     ref, ref_st = O.causal_conv1d(xs, w, b, state_in=st, return_state=True)
     xd = dev(x)
     sd = dev(st) if with_state else None
-    sout = dev(np.zeros((B, C, K - 1), np.float32))
+    sout = dev(np.zeros((B, C, Kw - 1), np.float32))
     y = K().causal_conv1d(xd[:, :, :C], dev(w), dev(b), True, sd, sout)
     assert err(host(y), ref) <= F32_TOL
     assert err(host(sout), ref_st) <= F32_TOL
