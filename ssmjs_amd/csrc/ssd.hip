@@ -22,6 +22,9 @@
 // B*H*segments workgroups fill the chip: a state-only pass gives each segment's local final
 // state and total decay, a combine pass turns them into each segment's entering state, and
 // the full pass starts each segment from it.
+#include <algorithm>
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -90,23 +93,75 @@ __device__ __forceinline__ void ldv(const T* p, float* out) {
 __device__ __forceinline__ __bf16 hi_of(float v) { return (__bf16)v; }
 __device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v - (float)h); }
 
+// LDS tiles, all in natural row-major layout (rows = time steps j, or p for the state). The
+// operands an MFMA needs with K = j (X^T, (X w)^T, B^T) are read with ds_read_b64_tr_b16:
+// inside each 16-lane group, lane 4a+b receives element b of the 8-byte chunks addressed by
+// lanes a, a+4, a+8, a+12. If lane m points at row j0 + m/4, column base + 4 (m % 4), lane L
+// receives M[j0 .. j0+3][base + L]: four K-consecutive values of column base + L.
+// Row pitches (in 4-byte banks of the 64-bank LDS): X 36, B 72 (N=128) / 40 (N=64), state
+// 68 / 36, so both the transposed reads (4 rows x 32 bytes) and the b128 row reads of a phase
+// land on distinct banks.
 template <bool SPLIT, int NN, bool FULL>
 struct Smem {
     static constexpr int NS = SPLIT ? 2 : 1;
-    __bf16 bt[NS][NN][Q + PADB];       // B^T   (n, j)
-    __bf16 xwt[NS][P][Q + PADB];       // (X w)^T (p, j)
-    __bf16 b[FULL ? NS : 1][FULL ? Q : 1][NN + PADB];    // B (j, n)
-    __bf16 xt[FULL ? NS : 1][FULL ? P : 1][Q + PADB];    // X^T (p, j)
-    __bf16 s[FULL ? NS : 1][FULL ? P : 1][NN + PADB];    // state (p, n)
+    static constexpr int XP = P + 8;                   // X / Xw row pitch (bf16)
+    static constexpr int BP = NN + 16;                 // B row pitch
+    static constexpr int SP = NN + 8;                  // state row pitch
+    __bf16 xw[NS][Q][XP];                              // X * w_j   (j, p)
+    __bf16 b[NS][Q][BP];                               // B         (j, n)
+    __bf16 x[FULL ? NS : 1][FULL ? Q : 1][XP];         // X         (j, p)
+    __bf16 s[FULL ? NS : 1][FULL ? P : 1][SP];         // state     (p, n)
     float dt[Q];
     float ac[Q];
 };
 
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// Transposed read: see Smem. `row0` is j0 for this lane's 16-lane group, `col0` the first of
+// the 16 columns; returns M[j0..j0+3][col0 + (lane % 16)].
+template <int PITCH>
+__device__ __forceinline__ bf16x4 tr_read(const __bf16* base, int row0, int col0, int l16) {
+    const __bf16* p = base + (row0 + (l16 >> 2)) * PITCH + col0 + 4 * (l16 & 3);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
+
+__device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Per-thread raw prefetch of one chunk: X rows t/16 + 16k (4 elements at 4 (t % 16)), B rows
+// t/(NN/8) + (256/(NN/8)) k (8 elements at 8 (t % (NN/8))), C fragments, dt.
+template <typename TIN, int NN, bool PRE_C>
+struct Raw {
+    static constexpr int KS = NN / 32;
+    static constexpr int BL = NN / 8;          // lanes per B row
+    static constexpr int BR = 256 / BL;        // B rows per pass
+    static constexpr int BPASS = Q / BR;
+    using v4 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x4>::type;
+    using v8 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x8>::type;
+    static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // v8 units per 8 elements
+    v4 x[4];
+    v8 b[BPASS][V8N];
+    v8 c[PRE_C ? KS : 1][V8N];
+    float dt;
+};
+
+template <typename V>
+__device__ __forceinline__ V vzero() {
+    V v;
+    __builtin_memset(&v, 0, sizeof v);
+    return v;
+}
+
 template <typename TIN, bool SPLIT, int NN, bool FULL>
 __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     __shared__ Smem<SPLIT, NN, FULL> sm;
+    using SM = Smem<SPLIT, NN, FULL>;
     constexpr int NB = NN / 16;   // state n-blocks per wave
     constexpr int KS = NN / 32;   // k-steps over n
+    constexpr bool PRE_C = FULL && sizeof(TIN) == 2;
+    using RW = Raw<TIN, NN, PRE_C>;
+    constexpr int L1 = SPLIT ? 1 : 0;   // index of the lo copy (aliases hi when unused)
 
     int wg = blockIdx.x;
     if (a.remap) {
@@ -119,8 +174,11 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     const int g = h / (a.H / a.G);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, q4 = lane >> 4;
+    const int ic = 16 * w + l16;        // this lane's output row in the chunk
+    const int xr = tid >> 4, xc = 4 * (tid & 15);              // X staging row / column
+    const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);      // B staging row / column
 
-    const TIN* X = reinterpret_cast<const TIN*>(a.x);
+    const TIN* X = reinterpret_cast<const TIN*>(a.x) + (long)h * P;
     const TIN* Bp = reinterpret_cast<const TIN*>(a.Bm) + (long)g * a.N;
     const TIN* Cp = reinterpret_cast<const TIN*>(a.Cm) + (long)g * a.N;
     const float Ah = a.A[h];
@@ -129,6 +187,49 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
 
     const int c_begin = seg * a.chunks_per_seg;
     const int c_end = min(c_begin + a.chunks_per_seg, a.nchunks);
+
+    RW raw;
+    auto ld4 = [&](const TIN* p) -> typename RW::v4 { return *reinterpret_cast<const typename RW::v4*>(p); };
+    auto ld8 = [&](const TIN* p, typename RW::v8* out) {
+#pragma unroll
+        for (int u = 0; u < RW::V8N; ++u) out[u] = *reinterpret_cast<const typename RW::v8*>(p + 4 * u);
+    };
+    // rows past the sequence end are never read: their slots are zero (uniform branch on
+    // the chunk being partial, so full chunks carry no per-row guards)
+    auto load_raw = [&](int c) {
+        const int qv = min(Q, a.L - c * Q);
+        const long row0 = (long)b * a.L + (long)c * Q;
+        if (qv == Q) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) raw.x[k] = ld4(X + (row0 + xr + 16 * k) * a.ldx + xc);
+#pragma unroll
+            for (int k = 0; k < RW::BPASS; ++k) ld8(Bp + (row0 + br + RW::BR * k) * a.ldb + bc, raw.b[k]);
+            if constexpr (PRE_C)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) ld8(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, raw.c[ks]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                raw.x[k] = xr + 16 * k < qv ? ld4(X + (row0 + xr + 16 * k) * a.ldx + xc)
+                                            : vzero<typename RW::v4>();
+#pragma unroll
+            for (int k = 0; k < RW::BPASS; ++k) {
+                if (br + RW::BR * k < qv) ld8(Bp + (row0 + br + RW::BR * k) * a.ldb + bc, raw.b[k]);
+                else
+#pragma unroll
+                    for (int u = 0; u < RW::V8N; ++u) raw.b[k][u] = vzero<typename RW::v8>();
+            }
+            if constexpr (PRE_C)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    if (ic < qv) ld8(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, raw.c[ks]);
+                    else
+#pragma unroll
+                        for (int u = 0; u < RW::V8N; ++u) raw.c[ks][u] = vzero<typename RW::v8>();
+                }
+        }
+        raw.dt = lane < qv ? a.dt[(row0 + lane) * a.lddt + h] : 0.f;
+    };
 
     // ---- entering state -> accumulators (wave w: rows p = 16w + 4*q4 + r, cols 16nb + l16)
     const float* init = nullptr;
@@ -153,124 +254,130 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                 const float v = S[nb][r];
                 const __bf16 hv = hi_of(v);
                 sm.s[0][16 * w + 4 * q4 + r][16 * nb + l16] = hv;
-                if constexpr (SPLIT) sm.s[SPLIT ? 1 : 0][16 * w + 4 * q4 + r][16 * nb + l16] = lo_of(v, hv);
+                if constexpr (SPLIT) sm.s[L1][16 * w + 4 * q4 + r][16 * nb + l16] = lo_of(v, hv);
             }
     };
     if (FULL && state_live) write_state_lds();
+    if (c_begin < c_end) load_raw(c_begin);
 
     for (int c = c_begin; c < c_end; ++c) {
         const int t0 = c * Q;
         const int qv = min(Q, a.L - t0);
         const long row0 = (long)b * a.L + t0;
 
-        // ---- dt' and inclusive prefix of dt' * A over the chunk (wave 0)
-        if (w == 0) {
-            float dv = 0.f, av = 0.f;
-            if (lane < qv) {
-                dv = a.dt[(row0 + lane) * a.lddt + h] + dtb;
-                if (a.softplus) dv = ssm::softplus(dv);
-                dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
-                av = dv * Ah;
-            }
-            float s = av;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float o = __shfl_up(s, off, 64);
-                if (lane >= off) s += o;
-            }
-            sm.dt[lane] = dv;
-            sm.ac[lane] = s;
+        // ---- dt' and the inclusive prefix of dt' * A (every wave; lane = time step)
+        float dv = 0.f, av = 0.f;
+        if (lane < qv) {
+            dv = raw.dt + dtb;
+            if (a.softplus) dv = ssm::softplus_fast(dv);
+            dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
+            av = dv * Ah;
         }
-        __syncthreads();
-        const float acend = sm.ac[Q - 1];
+        float sc = av;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float o = __shfl_up(sc, off, 64);
+            if (lane >= off) sc += o;
+        }
+        const float acend = __shfl(sc, 63, 64);
         decay_sum += acend;
+        if (w == 0) {
+            sm.dt[lane] = dv;
+            sm.ac[lane] = sc;
+        }
+        const float wl = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
 
-        // ---- stage X: item (jp, pg) covers rows 2jp, 2jp+1 and p = 4pg..4pg+3
+        // ---- stage X, X w and B (row-major copies)
 #pragma unroll
-        for (int pass = 0; pass < (Q / 2) * (P / 4) / 256; ++pass) {
-            const int idx = pass * 256 + tid;
-            const int pg = idx % (P / 4), jp = idx / (P / 4);
-            const int j0 = 2 * jp;
-            float x0[4] = {0.f, 0.f, 0.f, 0.f}, x1[4] = {0.f, 0.f, 0.f, 0.f};
-            if (j0 < qv) ldv<TIN, 4>(X + (row0 + j0) * a.ldx + (long)h * P + 4 * pg, x0);
-            if (j0 + 1 < qv) ldv<TIN, 4>(X + (row0 + j0 + 1) * a.ldx + (long)h * P + 4 * pg, x1);
-            const float w0 = ssm::ex2((acend - sm.ac[j0]) * ssm::kLog2e) * sm.dt[j0];
-            const float w1 = ssm::ex2((acend - sm.ac[j0 + 1]) * ssm::kLog2e) * sm.dt[j0 + 1];
+        for (int k = 0; k < 4; ++k) {
+            const int j = xr + 16 * k;
+            const float wj = __shfl(wl, j, 64);
+            float xv[4];
+            if constexpr (sizeof(TIN) == 4) {
+                xv[0] = raw.x[k].x; xv[1] = raw.x[k].y; xv[2] = raw.x[k].z; xv[3] = raw.x[k].w;
+            } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int p = 4 * pg + k;
-                const float u0 = x0[k] * w0, u1 = x1[k] * w1;
-                bf16x2 hw = {hi_of(u0), hi_of(u1)};
-                *reinterpret_cast<bf16x2*>(&sm.xwt[0][p][j0]) = hw;
-                if constexpr (SPLIT) {
-                    bf16x2 lw = {lo_of(u0, hw[0]), lo_of(u1, hw[1])};
-                    *reinterpret_cast<bf16x2*>(&sm.xwt[SPLIT ? 1 : 0][p][j0]) = lw;
+                for (int e = 0; e < 4; ++e) xv[e] = (float)raw.x[k][e];
+            }
+            bf16x4 wh, wlo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float u = xv[e] * wj;
+                wh[e] = hi_of(u);
+                wlo[e] = lo_of(u, wh[e]);
+            }
+            *reinterpret_cast<bf16x4*>(&sm.xw[0][j][xc]) = wh;
+            if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.xw[L1][j][xc]) = wlo;
+            if constexpr (FULL) {
+                if constexpr (sizeof(TIN) == 2) {
+                    *reinterpret_cast<bf16x4*>(&sm.x[0][j][xc]) = raw.x[k];
+                } else {
+                    bf16x4 hh, ll;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hh[e] = hi_of(xv[e]);
+                        ll[e] = lo_of(xv[e], hh[e]);
+                    }
+                    *reinterpret_cast<bf16x4*>(&sm.x[0][j][xc]) = hh;
+                    if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.x[L1][j][xc]) = ll;
                 }
-                if constexpr (FULL) {
-                    bf16x2 hx = {hi_of(x0[k]), hi_of(x1[k])};
-                    *reinterpret_cast<bf16x2*>(&sm.xt[0][p][j0]) = hx;
-                    if constexpr (SPLIT) {
-                        bf16x2 lx = {lo_of(x0[k], hx[0]), lo_of(x1[k], hx[1])};
-                        *reinterpret_cast<bf16x2*>(&sm.xt[SPLIT ? 1 : 0][p][j0]) = lx;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < RW::BPASS; ++k) {
+            const int j = br + RW::BR * k;
+            if constexpr (sizeof(TIN) == 2) {
+                *reinterpret_cast<bf16x8*>(&sm.b[0][j][bc]) = raw.b[k][0];
+            } else {
+                bf16x8 hh, ll;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float e4[4] = {raw.b[k][u].x, raw.b[k][u].y, raw.b[k][u].z, raw.b[k][u].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hh[4 * u + e] = hi_of(e4[e]);
+                        ll[4 * u + e] = lo_of(e4[e], hh[4 * u + e]);
                     }
                 }
-            }
-        }
-        // ---- stage B: item (jp, ng) covers rows 2jp, 2jp+1 and n = 8ng..8ng+7
-#pragma unroll
-        for (int pass = 0; pass < (Q / 2) * (NN / 8) / 256; ++pass) {
-            const int idx = pass * 256 + tid;
-            const int ng = idx % (NN / 8), jp = idx / (NN / 8);
-            const int j0 = 2 * jp;
-            float b0[8], b1[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) { b0[k] = 0.f; b1[k] = 0.f; }
-            if (j0 < qv) ldv<TIN, 8>(Bp + (row0 + j0) * a.ldb + 8 * ng, b0);
-            if (j0 + 1 < qv) ldv<TIN, 8>(Bp + (row0 + j0 + 1) * a.ldb + 8 * ng, b1);
-            bf16x8 h0v, h1v, l0v, l1v;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                h0v[k] = hi_of(b0[k]);
-                h1v[k] = hi_of(b1[k]);
-                l0v[k] = lo_of(b0[k], h0v[k]);
-                l1v[k] = lo_of(b1[k], h1v[k]);
-                bf16x2 ht = {h0v[k], h1v[k]};
-                *reinterpret_cast<bf16x2*>(&sm.bt[0][8 * ng + k][j0]) = ht;
-                if constexpr (SPLIT) {
-                    bf16x2 lt = {l0v[k], l1v[k]};
-                    *reinterpret_cast<bf16x2*>(&sm.bt[SPLIT ? 1 : 0][8 * ng + k][j0]) = lt;
-                }
-            }
-            if constexpr (FULL) {
-                *reinterpret_cast<bf16x8*>(&sm.b[0][j0][8 * ng]) = h0v;
-                *reinterpret_cast<bf16x8*>(&sm.b[0][j0 + 1][8 * ng]) = h1v;
-                if constexpr (SPLIT) {
-                    *reinterpret_cast<bf16x8*>(&sm.b[SPLIT ? 1 : 0][j0][8 * ng]) = l0v;
-                    *reinterpret_cast<bf16x8*>(&sm.b[SPLIT ? 1 : 0][j0 + 1][8 * ng]) = l1v;
-                }
+                *reinterpret_cast<bf16x8*>(&sm.b[0][j][bc]) = hh;
+                if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&sm.b[L1][j][bc]) = ll;
             }
         }
 
+        // ---- C rows of this wave's strip as MFMA fragments: row ic, n = 32ks + 8q4 + 0..7
+        bf16x8 cfh[FULL ? KS : 1], cfl[FULL ? KS : 1];
         if constexpr (FULL) {
-            // ---- C rows of this wave's strip: i = 16w + l16, k-slots n = 32ks + 8q4 + 0..7
-            const int ic = 16 * w + l16;
-            bf16x8 cfh[KS], cfl[KS];
-            {
-                float cv[8];
+            if constexpr (PRE_C) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) cfh[ks] = raw.c[ks][0];
+            } else {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
+                    typename RW::v8 cv[RW::V8N];
+                    if (ic < qv) ld8(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, cv);
+                    else
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) cv[k] = 0.f;
-                    if (ic < qv) ldv<TIN, 8>(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, cv);
+                        for (int u = 0; u < RW::V8N; ++u) cv[u] = vzero<typename RW::v8>();
+                    if constexpr (sizeof(TIN) == 4) {
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        cfh[ks][k] = hi_of(cv[k]);
-                        cfl[ks][k] = lo_of(cv[k], cfh[ks][k]);
+                        for (int u = 0; u < 2; ++u) {
+                            const float e4[4] = {cv[u].x, cv[u].y, cv[u].z, cv[u].w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                cfh[ks][4 * u + e] = hi_of(e4[e]);
+                                cfl[ks][4 * u + e] = lo_of(e4[e], cfh[ks][4 * u + e]);
+                            }
+                        }
                     }
                 }
             }
-            __syncthreads();   // staging done; state LDS written
+        }
+        __syncthreads();   // staging (and the state LDS copy) visible to every wave
 
+        // ---- the next chunk's raw inputs are in flight while this one computes
+        if (c + 1 < c_end) load_raw(c + 1);
+
+        if constexpr (FULL) {
             const float aci = sm.ac[ic];
             floatx4 Y[P / 16];
 #pragma unroll
@@ -287,7 +394,7 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                         Y[pb] = mfma(ah, cfh[ks], Y[pb]);
                         if constexpr (SPLIT) {
                             const bf16x8 al = *reinterpret_cast<const bf16x8*>(
-                                &sm.s[SPLIT ? 1 : 0][16 * pb + l16][32 * ks + 8 * q4]);
+                                &sm.s[L1][16 * pb + l16][32 * ks + 8 * q4]);
                             Y[pb] = mfma(ah, cfl[ks], Y[pb]);
                             Y[pb] = mfma(al, cfh[ks], Y[pb]);
                         }
@@ -313,7 +420,7 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                             st = mfma(bh_, cfh[ks], st);
                             if constexpr (SPLIT) {
                                 const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
-                                    &sm.b[SPLIT ? 1 : 0][16 * jb + l16][32 * ks + 8 * q4]);
+                                    &sm.b[L1][16 * jb + l16][32 * ks + 8 * q4]);
                                 st = mfma(bh_, cfl[ks], st);
                                 st = mfma(bl_, cfh[ks], st);
                             }
@@ -336,35 +443,36 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                     sfh[k] = hi_of(sv[k]);
                     sfl[k] = lo_of(sv[k], sfh[k]);
                 }
+                // X^T fragment: k-slots 0..3 <-> j = 32 jb2 + 4 q4 + 0..3, 4..7 <-> +16
 #pragma unroll
                 for (int pb = 0; pb < P / 16; ++pb) {
-                    const int p = 16 * pb + l16;
-                    const bf16x4 x0 =
-                        *reinterpret_cast<const bf16x4*>(&sm.xt[0][p][32 * jb2 + 4 * q4]);
-                    const bf16x4 x1 =
-                        *reinterpret_cast<const bf16x4*>(&sm.xt[0][p][32 * jb2 + 16 + 4 * q4]);
-                    const bf16x8 xh = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                    const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                          tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
                     Y[pb] = mfma(xh, sfh, Y[pb]);
                     if constexpr (SPLIT) {
-                        const bf16x4 y0 = *reinterpret_cast<const bf16x4*>(
-                            &sm.xt[SPLIT ? 1 : 0][p][32 * jb2 + 4 * q4]);
-                        const bf16x4 y1 = *reinterpret_cast<const bf16x4*>(
-                            &sm.xt[SPLIT ? 1 : 0][p][32 * jb2 + 16 + 4 * q4]);
-                        const bf16x8 xl = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+                        const bf16x8 xl = cat(tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
                         Y[pb] = mfma(xh, sfl, Y[pb]);
                         Y[pb] = mfma(xl, sfh, Y[pb]);
                     }
                 }
             }
 
-            // ---- y = Y + D x   (lane: row ic, p = 16pb + 4q4 + 0..3)
+            // ---- y = Y + D x   (lane: row ic, p = 16pb + 4q4 + 0..3; x from the LDS tile)
             if (ic < qv) {
                 const long r = row0 + ic;
 #pragma unroll
                 for (int pb = 0; pb < P / 16; ++pb) {
                     const int p0 = 16 * pb + 4 * q4;
+                    const bf16x4 xh4 = *reinterpret_cast<const bf16x4*>(&sm.x[0][ic][p0]);
                     float xv[4];
-                    ldv<TIN, 4>(X + r * a.ldx + (long)h * P + p0, xv);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) xv[k] = (float)xh4[k];
+                    if constexpr (SPLIT) {
+                        const bf16x4 xl4 = *reinterpret_cast<const bf16x4*>(&sm.x[L1][ic][p0]);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) xv[k] += (float)xl4[k];
+                    }
                     float4 o;
                     o.x = fmaf(Dh, xv[0], Y[pb][0]);
                     o.y = fmaf(Dh, xv[1], Y[pb][1]);
@@ -373,31 +481,30 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                     *reinterpret_cast<float4*>(a.y + r * a.ldy + (long)h * P + p0) = o;
                 }
             }
-        } else {
-            __syncthreads();   // staging done
         }
 
-        // ---- state: S = exp(acum_end) S + (X w)^T B
+        // ---- state: S = exp(acum_end) S + (X w)^T B   (k-slots j = 32ks + 8q4 + 0..7)
         {
             const float e = ssm::ex2(acend * ssm::kLog2e);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) S[nb] *= e;
 #pragma unroll
             for (int ks = 0; ks < Q / 32; ++ks) {
-                const bf16x8 xh =
-                    *reinterpret_cast<const bf16x8*>(&sm.xwt[0][16 * w + l16][32 * ks + 8 * q4]);
+                const int j0 = 32 * ks + 8 * q4;
+                const bf16x8 xh = cat(tr_read<SM::XP>(&sm.xw[0][0][0], j0, 16 * w, l16),
+                                      tr_read<SM::XP>(&sm.xw[0][0][0], j0 + 4, 16 * w, l16));
                 bf16x8 xl;
                 if constexpr (SPLIT)
-                    xl = *reinterpret_cast<const bf16x8*>(
-                        &sm.xwt[SPLIT ? 1 : 0][16 * w + l16][32 * ks + 8 * q4]);
+                    xl = cat(tr_read<SM::XP>(&sm.xw[L1][0][0], j0, 16 * w, l16),
+                             tr_read<SM::XP>(&sm.xw[L1][0][0], j0 + 4, 16 * w, l16));
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(
-                        &sm.bt[0][16 * nb + l16][32 * ks + 8 * q4]);
+                    const bf16x8 bh_ = cat(tr_read<SM::BP>(&sm.b[0][0][0], j0, 16 * nb, l16),
+                                           tr_read<SM::BP>(&sm.b[0][0][0], j0 + 4, 16 * nb, l16));
                     S[nb] = mfma(xh, bh_, S[nb]);
                     if constexpr (SPLIT) {
-                        const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
-                            &sm.bt[SPLIT ? 1 : 0][16 * nb + l16][32 * ks + 8 * q4]);
+                        const bf16x8 bl_ = cat(tr_read<SM::BP>(&sm.b[L1][0][0], j0, 16 * nb, l16),
+                                               tr_read<SM::BP>(&sm.b[L1][0][0], j0 + 4, 16 * nb, l16));
                         S[nb] = mfma(xh, bl_, S[nb]);
                         S[nb] = mfma(xl, bh_, S[nb]);
                     }
@@ -472,45 +579,73 @@ void plan(int B, int L, int H, int& nchunks, int& nseg, int& per) {
 // ---------------------------------------------------------------- one-token update (K7)
 // Workgroup per (b, h): lanes run along n in float4 steps (N/4 lanes per row of the state),
 // rows p are spread over the remaining lanes and looped. y[p] reduces over the row's lanes.
-template <int LPR>
+// Persistent form: a bounded grid walks the (b, h) tiles; each thread owns the same float4
+// slots of every tile it visits and prefetches the next tile's state while it updates and
+// writes back the current one, so reads and write-backs overlap across the whole kernel.
+template <int LPR, int MAXR>
 __global__ __launch_bounds__(256) void m2_update_kernel(
     const float* __restrict__ x, long ldx, const float* __restrict__ dt, long lddt,
     const float* __restrict__ dt_bias, int softplus, float dt_min, float dt_max,
     const float* __restrict__ A, const float* __restrict__ Bm, long ldb,
     const float* __restrict__ Cm, long ldc, const float* __restrict__ Dsk,
     const float* __restrict__ z, long ldz, float* __restrict__ y, long ldy,
-    float* __restrict__ hs, int H, int Pd, int G, int N) {
-    const int bh = blockIdx.x;
-    const int h = bh % H, b = bh / H, g = h / (H / G);
+    float* __restrict__ hs, int B, int H, int Pd, int G, int N) {
+    constexpr int RPP = 256 / LPR;      // rows per pass; MAXR * RPP >= Pd
     const int tid = threadIdx.x;
     const int c4 = tid % LPR;           // float4 column
-    const int rsub = tid / LPR;         // row within a pass
-    constexpr int RPP = 256 / LPR;      // rows per pass
-    float dl = dt[(long)b * lddt + h] + (dt_bias ? dt_bias[h] : 0.f);
-    if (softplus) dl = ssm::softplus(dl);
-    dl = fminf(fmaxf(dl, dt_min), dt_max);
-    const float dA = ssm::ex2(dl * A[h] * ssm::kLog2e);
-    const float Dh = Dsk ? Dsk[h] : 0.f;
-    const float4 bv = *reinterpret_cast<const float4*>(Bm + (long)b * ldb + (long)g * N + 4 * c4);
-    const float4 cv = *reinterpret_cast<const float4*>(Cm + (long)b * ldc + (long)g * N + 4 * c4);
-    float* hb = hs + (long)bh * Pd * N;
-    for (int p = rsub; p < Pd; p += RPP) {
-        const float xp = x[(long)b * ldx + (long)h * Pd + p];
-        const float dx = dl * xp;
-        float4* hp = reinterpret_cast<float4*>(hb + (long)p * N) + c4;
-        float4 v = *hp;
-        v.x = fmaf(dA, v.x, dx * bv.x);
-        v.y = fmaf(dA, v.y, dx * bv.y);
-        v.z = fmaf(dA, v.z, dx * bv.z);
-        v.w = fmaf(dA, v.w, dx * bv.w);
-        *hp = v;
-        float acc = v.x * cv.x + v.y * cv.y + v.z * cv.z + v.w * cv.w;
+    const int rsub = tid / LPR;         // first row
+    const int ntiles = B * H;
+    float4 v[MAXR];
+    auto load_tile = [&](int bh) {
+        const float* hb = hs + (long)bh * Pd * N;
 #pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
-        if (c4 == 0) {
-            acc = fmaf(Dh, xp, acc);
-            if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
-            y[(long)b * ldy + (long)h * Pd + p] = acc;
+        for (int k = 0; k < MAXR; ++k) {
+            const int p = rsub + k * RPP;
+            if (p < Pd) v[k] = *(reinterpret_cast<const float4*>(hb + (long)p * N) + c4);
+        }
+    };
+    int bh = blockIdx.x;
+    if (bh < ntiles) load_tile(bh);
+    for (; bh < ntiles; bh += gridDim.x) {
+        const int h = bh % H, b = bh / H, g = h / (H / G);
+        float dl = dt[(long)b * lddt + h] + (dt_bias ? dt_bias[h] : 0.f);
+        if (softplus) dl = ssm::softplus(dl);
+        dl = fminf(fmaxf(dl, dt_min), dt_max);
+        const float dA = ssm::ex2(dl * A[h] * ssm::kLog2e);
+        const float Dh = Dsk ? Dsk[h] : 0.f;
+        const float4 bv = *reinterpret_cast<const float4*>(Bm + (long)b * ldb + (long)g * N + 4 * c4);
+        const float4 cv = *reinterpret_cast<const float4*>(Cm + (long)b * ldc + (long)g * N + 4 * c4);
+        float xp[MAXR];
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) {
+            const int p = rsub + k * RPP;
+            xp[k] = p < Pd ? x[(long)b * ldx + (long)h * Pd + p] : 0.f;
+        }
+        float4 cur[MAXR];
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) cur[k] = v[k];
+        const int nxt = bh + gridDim.x;
+        if (nxt < ntiles) load_tile(nxt);
+        float* hb = hs + (long)bh * Pd * N;
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) {
+            const int p = rsub + k * RPP;
+            if (p >= Pd) break;
+            const float dx = dl * xp[k];
+            float4 u = cur[k];
+            u.x = fmaf(dA, u.x, dx * bv.x);
+            u.y = fmaf(dA, u.y, dx * bv.y);
+            u.z = fmaf(dA, u.z, dx * bv.z);
+            u.w = fmaf(dA, u.w, dx * bv.w);
+            *(reinterpret_cast<float4*>(hb + (long)p * N) + c4) = u;
+            float acc = u.x * cv.x + u.y * cv.y + u.z * cv.z + u.w * cv.w;
+#pragma unroll
+            for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+            if (c4 == 0) {
+                acc = fmaf(Dh, xp[k], acc);
+                if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
+                y[(long)b * ldy + (long)h * Pd + p] = acc;
+            }
         }
     }
 }
@@ -686,19 +821,29 @@ extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float*
                 "ssm_m2_state_update: B/C/state must be 16-byte aligned");
     if (B == 0) return SSM_OK;
     hipStream_t st = (hipStream_t)stream;
-    const unsigned grid = (unsigned)(B * H);
-#define M2U(LPR)                                                                               \
-    m2_update_kernel<LPR><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus, dt_min,   \
-                                                dt_max, A, Bm, ldb, Cm, ldc, Dsk, z, ldz, y,   \
-                                                ldy, h, H, Pd, G, N)
-    switch (N / 4) {
-        case 2: M2U(2); break;
-        case 4: M2U(4); break;
-        case 8: M2U(8); break;
-        case 16: M2U(16); break;
-        case 32: M2U(32); break;
-        default: M2U(64); break;
+    const int lpr = N / 4, rpp = 256 / lpr;
+    if (Pd > 16 * rpp)
+        return ssm::fail(SSM_ERR_UNSUPPORTED, "ssm_m2_state_update: head dim %d too large for "
+                         "d_state %d", Pd, N);
+    // up to 4 resident tiles per CU-slot pass; the kernel strides over the rest
+    const unsigned grid = (unsigned)std::min<long>((long)B * H, 1024);
+#define M2U(LPR, MAXR)                                                                           \
+    m2_update_kernel<LPR, MAXR><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus,       \
+                                                      dt_min, dt_max, A, Bm, ldb, Cm, ldc, Dsk,  \
+                                                      z, ldz, y, ldy, h, B, H, Pd, G, N)
+#define M2R(LPR)                                   \
+    if (Pd <= 4 * rpp) M2U(LPR, 4);                \
+    else if (Pd <= 8 * rpp) M2U(LPR, 8);           \
+    else M2U(LPR, 16);
+    switch (lpr) {
+        case 2: M2R(2); break;
+        case 4: M2R(4); break;
+        case 8: M2R(8); break;
+        case 16: M2R(16); break;
+        case 32: M2R(32); break;
+        default: M2R(64); break;
     }
+#undef M2R
 #undef M2U
     return ssm::check_launch("m2_state_update");
 }

@@ -313,3 +313,22 @@ def test_rmsnorm_and_gated():
     for g in (1, 3):
         ref = O.gated_rmsnorm(x, z, w, groups=g)
         assert err(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=g)), ref) <= F32_TOL
+
+
+def test_m2_state_update_decode_shape():
+    """Config-4 shape (64 sequences x 32 heads): more tiles than the persistent grid, so
+    every workgroup walks several (b, h) tiles."""
+    case("m2_state_update decode shape")
+    r = rng(15)
+    B, H, P, G, N = 64, 32, 64, 1, 128
+    h0 = (0.1 * r.standard_normal((B, H, P, N))).astype(np.float32)
+    x = r.standard_normal((B, H, P)).astype(np.float32)
+    dt = (r.standard_normal((B, H)) - 3).astype(np.float32)
+    Bm, Cm = (r.standard_normal((B, G, N)).astype(np.float32) for _ in range(2))
+    A = -r.uniform(1, 16, H).astype(np.float32)
+    Dk, db = r.standard_normal(H).astype(np.float32), r.standard_normal(H).astype(np.float32)
+    ref, href = O.m2_state_update(x, dt, A, Bm, Cm, Dk, db, h0)
+    hd = dev(h0)
+    y = K().m2_state_update(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(db), hd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), href) <= F32_TOL
