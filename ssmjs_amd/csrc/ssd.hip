@@ -98,21 +98,22 @@ __device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v -
 // inside each 16-lane group, lane 4a+b receives element b of the 8-byte chunks addressed by
 // lanes a, a+4, a+8, a+12. If lane m points at row j0 + m/4, column base + 4 (m % 4), lane L
 // receives M[j0 .. j0+3][base + L]: four K-consecutive values of column base + L.
-// Row pitches (in 4-byte banks of the 64-bank LDS): X 36, B 72 (N=128) / 40 (N=64), state
-// 68 / 36, so both the transposed reads (4 rows x 32 bytes) and the b128 row reads of a phase
-// land on distinct banks.
+// Row pitches (in 4-byte banks of the 64-bank LDS): X, X w and state^T 36, B 72 (N=128) /
+// 40 (N=64), so both the transposed reads (4 rows x 32 bytes) and the b128 row reads of a
+// phase land on distinct banks.
 template <bool SPLIT, int NN, bool FULL>
 struct Smem {
     static constexpr int NS = SPLIT ? 2 : 1;
     static constexpr int XP = P + 8;                   // X / Xw row pitch (bf16)
     static constexpr int BP = NN + 16;                 // B row pitch
-    static constexpr int SP = NN + 8;                  // state row pitch
-    __bf16 xw[NS][Q][XP];                              // X * w_j   (j, p)
-    __bf16 b[NS][Q][BP];                               // B         (j, n)
-    __bf16 x[FULL ? NS : 1][FULL ? Q : 1][XP];         // X         (j, p)
-    __bf16 s[FULL ? NS : 1][FULL ? P : 1][SP];         // state     (p, n)
-    float dt[Q];
-    float ac[Q];
+    // 16-byte alignment lets the compiler use ds_read_b128 / ds_write_b128 for the 8-wide
+    // bf16 rows (every pitch is a multiple of 8 elements)
+    alignas(16) __bf16 xw[NS][Q][XP];                  // X * w_j   (j, p)
+    alignas(16) __bf16 b[NS][Q][BP];                   // B         (j, n)
+    alignas(16) __bf16 x[FULL ? NS : 1][FULL ? Q : 1][XP];   // X   (j, p)
+    alignas(16) __bf16 s[FULL ? NS : 1][FULL ? NN : 1][XP];  // state^T (n, p)
+    alignas(16) float dt[Q];
+    alignas(16) float ac[Q];
 };
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -129,22 +130,41 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Per-thread raw prefetch of one chunk: X rows t/16 + 16k (4 elements at 4 (t % 16)), B rows
-// t/(NN/8) + (256/(NN/8)) k (8 elements at 8 (t % (NN/8))), C fragments, dt.
+// Per-thread raw prefetch of one chunk: X row j = lane, columns 16w..16w+15 (so the lane that
+// owns time step j also owns its weight w_j); B rows t/(NN/8) + (256/(NN/8)) k, 8 elements at
+// 8 (t % (NN/8)); the C fragments of the wave's strip; dt of time step lane.
 template <typename TIN, int NN, bool PRE_C>
 struct Raw {
     static constexpr int KS = NN / 32;
     static constexpr int BL = NN / 8;          // lanes per B row
     static constexpr int BR = 256 / BL;        // B rows per pass
     static constexpr int BPASS = Q / BR;
-    using v4 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x4>::type;
     using v8 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x8>::type;
     static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // v8 units per 8 elements
-    v4 x[4];
+    v8 x[2][V8N];
     v8 b[BPASS][V8N];
     v8 c[PRE_C ? KS : 1][V8N];
     float dt;
 };
+
+// Inclusive prefix sum over the 64 lanes with DPP (row_shr inside rows of 16, then
+// row_bcast:15 / row_bcast:31 across rows); no LDS traffic.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float add_dpp(float x) {
+    const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xf,
+                                              true);
+    return x + __builtin_bit_cast(float, y);
+}
+
+__device__ __forceinline__ float wave_prefix_sum(float v) {
+    v = add_dpp<0x111, 0xf>(v);   // row_shr:1
+    v = add_dpp<0x112, 0xf>(v);   // row_shr:2
+    v = add_dpp<0x114, 0xf>(v);   // row_shr:4
+    v = add_dpp<0x118, 0xf>(v);   // row_shr:8
+    v = add_dpp<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v = add_dpp<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return v;
+}
 
 template <typename V>
 __device__ __forceinline__ V vzero() {
@@ -155,7 +175,7 @@ __device__ __forceinline__ V vzero() {
 
 template <typename TIN, bool SPLIT, int NN, bool FULL>
 __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
-    __shared__ Smem<SPLIT, NN, FULL> sm;
+    __shared__ __attribute__((aligned(16))) Smem<SPLIT, NN, FULL> sm;
     using SM = Smem<SPLIT, NN, FULL>;
     constexpr int NB = NN / 16;   // state n-blocks per wave
     constexpr int KS = NN / 32;   // k-steps over n
@@ -175,12 +195,8 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, q4 = lane >> 4;
     const int ic = 16 * w + l16;        // this lane's output row in the chunk
-    const int xr = tid >> 4, xc = 4 * (tid & 15);              // X staging row / column
     const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);      // B staging row / column
 
-    const TIN* X = reinterpret_cast<const TIN*>(a.x) + (long)h * P;
-    const TIN* Bp = reinterpret_cast<const TIN*>(a.Bm) + (long)g * a.N;
-    const TIN* Cp = reinterpret_cast<const TIN*>(a.Cm) + (long)g * a.N;
     const float Ah = a.A[h];
     const float dtb = a.dt_bias ? a.dt_bias[h] : 0.f;
     const float Dh = a.Dsk ? a.Dsk[h] : 0.f;
@@ -188,47 +204,58 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     const int c_begin = seg * a.chunks_per_seg;
     const int c_end = min(c_begin + a.chunks_per_seg, a.nchunks);
 
+    // Per-thread global pointers at chunk c_begin, advanced by one chunk per iteration.
+    const long rbase = (long)b * a.L + (long)c_begin * Q;
+    const TIN* xg = reinterpret_cast<const TIN*>(a.x) + (rbase + lane) * a.ldx + (long)h * P + 16 * w;
+    const TIN* bg = reinterpret_cast<const TIN*>(a.Bm) + (rbase + br) * a.ldb + (long)g * a.N + bc;
+    const TIN* cg = reinterpret_cast<const TIN*>(a.Cm) + (rbase + ic) * a.ldc + (long)g * a.N + 8 * q4;
+    const float* dtg = a.dt + (rbase + lane) * a.lddt + h;
+    const long xstep = (long)Q * a.ldx, bstep = (long)Q * a.ldb, cstep = (long)Q * a.ldc,
+               dstep = (long)Q * a.lddt;
+
     RW raw;
-    auto ld4 = [&](const TIN* p) -> typename RW::v4 { return *reinterpret_cast<const typename RW::v4*>(p); };
     auto ld8 = [&](const TIN* p, typename RW::v8* out) {
 #pragma unroll
         for (int u = 0; u < RW::V8N; ++u) out[u] = *reinterpret_cast<const typename RW::v8*>(p + 4 * u);
     };
+    auto z8 = [&](typename RW::v8* out) {
+#pragma unroll
+        for (int u = 0; u < RW::V8N; ++u) out[u] = vzero<typename RW::v8>();
+    };
     // rows past the sequence end are never read: their slots are zero (uniform branch on
     // the chunk being partial, so full chunks carry no per-row guards)
+    // xg / bg / cg / dtg always point at the chunk load_raw reads next
     auto load_raw = [&](int c) {
         const int qv = min(Q, a.L - c * Q);
-        const long row0 = (long)b * a.L + (long)c * Q;
+        const TIN* xp = xg;
+        const TIN* bp = bg;
+        const TIN* cp = cg;
         if (qv == Q) {
+            ld8(xp, raw.x[0]);
+            ld8(xp + 8, raw.x[1]);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) raw.x[k] = ld4(X + (row0 + xr + 16 * k) * a.ldx + xc);
-#pragma unroll
-            for (int k = 0; k < RW::BPASS; ++k) ld8(Bp + (row0 + br + RW::BR * k) * a.ldb + bc, raw.b[k]);
+            for (int k = 0; k < RW::BPASS; ++k) ld8(bp + (long)RW::BR * k * a.ldb, raw.b[k]);
             if constexpr (PRE_C)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) ld8(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, raw.c[ks]);
+                for (int ks = 0; ks < KS; ++ks) ld8(cp + 32 * ks, raw.c[ks]);
+            raw.dt = *dtg;
         } else {
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                raw.x[k] = xr + 16 * k < qv ? ld4(X + (row0 + xr + 16 * k) * a.ldx + xc)
-                                            : vzero<typename RW::v4>();
+            if (lane < qv) { ld8(xp, raw.x[0]); ld8(xp + 8, raw.x[1]); }
+            else { z8(raw.x[0]); z8(raw.x[1]); }
 #pragma unroll
             for (int k = 0; k < RW::BPASS; ++k) {
-                if (br + RW::BR * k < qv) ld8(Bp + (row0 + br + RW::BR * k) * a.ldb + bc, raw.b[k]);
-                else
-#pragma unroll
-                    for (int u = 0; u < RW::V8N; ++u) raw.b[k][u] = vzero<typename RW::v8>();
+                if (br + RW::BR * k < qv) ld8(bp + (long)RW::BR * k * a.ldb, raw.b[k]);
+                else z8(raw.b[k]);
             }
             if constexpr (PRE_C)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    if (ic < qv) ld8(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, raw.c[ks]);
-                    else
-#pragma unroll
-                        for (int u = 0; u < RW::V8N; ++u) raw.c[ks][u] = vzero<typename RW::v8>();
+                    if (ic < qv) ld8(cp + 32 * ks, raw.c[ks]);
+                    else z8(raw.c[ks]);
                 }
+            raw.dt = lane < qv ? *dtg : 0.f;
         }
-        raw.dt = lane < qv ? a.dt[(row0 + lane) * a.lddt + h] : 0.f;
+        xg += xstep; bg += bstep; cg += cstep; dtg += dstep;
     };
 
     // ---- entering state -> accumulators (wave w: rows p = 16w + 4*q4 + r, cols 16nb + l16)
@@ -246,16 +273,20 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     bool state_live = init != nullptr;
     float decay_sum = 0.f;
 
+    // The accumulators hold S[p = 16w + 4q4 + r][n = 16nb + l16] for r = 0..3: four
+    // consecutive p of one n, i.e. one 8-byte run of the state^T tile.
     auto write_state_lds = [&]() {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb) {
+            bf16x4 hv, lv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float v = S[nb][r];
-                const __bf16 hv = hi_of(v);
-                sm.s[0][16 * w + 4 * q4 + r][16 * nb + l16] = hv;
-                if constexpr (SPLIT) sm.s[L1][16 * w + 4 * q4 + r][16 * nb + l16] = lo_of(v, hv);
+                hv[r] = hi_of(S[nb][r]);
+                lv[r] = lo_of(S[nb][r], hv[r]);
             }
+            *reinterpret_cast<bf16x4*>(&sm.s[0][16 * nb + l16][16 * w + 4 * q4]) = hv;
+            if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.s[L1][16 * nb + l16][16 * w + 4 * q4]) = lv;
+        }
     };
     if (FULL && state_live) write_state_lds();
     if (c_begin < c_end) load_raw(c_begin);
@@ -273,13 +304,9 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
             dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
             av = dv * Ah;
         }
-        float sc = av;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float o = __shfl_up(sc, off, 64);
-            if (lane >= off) sc += o;
-        }
-        const float acend = __shfl(sc, 63, 64);
+        const float sc = wave_prefix_sum(av);
+        const float acend = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
         decay_sum += acend;
         if (w == 0) {
             sm.dt[lane] = dv;
@@ -287,39 +314,42 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
         }
         const float wl = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
 
-        // ---- stage X, X w and B (row-major copies)
+        // ---- stage X and X w: lane = row j, columns 16w..16w+15 (two 8-wide halves)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int j = xr + 16 * k;
-            const float wj = __shfl(wl, j, 64);
-            float xv[4];
+        for (int hlf = 0; hlf < 2; ++hlf) {
+            float xv[8];
             if constexpr (sizeof(TIN) == 4) {
-                xv[0] = raw.x[k].x; xv[1] = raw.x[k].y; xv[2] = raw.x[k].z; xv[3] = raw.x[k].w;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    xv[4 * u] = raw.x[hlf][u].x; xv[4 * u + 1] = raw.x[hlf][u].y;
+                    xv[4 * u + 2] = raw.x[hlf][u].z; xv[4 * u + 3] = raw.x[hlf][u].w;
+                }
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) xv[e] = (float)raw.x[k][e];
+                for (int e = 0; e < 8; ++e) xv[e] = (float)raw.x[hlf][0][e];
             }
-            bf16x4 wh, wlo;
+            const int col = 16 * w + 8 * hlf;
+            bf16x8 wh, wlo;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float u = xv[e] * wj;
+            for (int e = 0; e < 8; ++e) {
+                const float u = xv[e] * wl;
                 wh[e] = hi_of(u);
                 wlo[e] = lo_of(u, wh[e]);
             }
-            *reinterpret_cast<bf16x4*>(&sm.xw[0][j][xc]) = wh;
-            if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.xw[L1][j][xc]) = wlo;
+            *reinterpret_cast<bf16x8*>(&sm.xw[0][lane][col]) = wh;
+            if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&sm.xw[L1][lane][col]) = wlo;
             if constexpr (FULL) {
                 if constexpr (sizeof(TIN) == 2) {
-                    *reinterpret_cast<bf16x4*>(&sm.x[0][j][xc]) = raw.x[k];
+                    *reinterpret_cast<bf16x8*>(&sm.x[0][lane][col]) = raw.x[hlf][0];
                 } else {
-                    bf16x4 hh, ll;
+                    bf16x8 hh, ll;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
+                    for (int e = 0; e < 8; ++e) {
                         hh[e] = hi_of(xv[e]);
                         ll[e] = lo_of(xv[e], hh[e]);
                     }
-                    *reinterpret_cast<bf16x4*>(&sm.x[0][j][xc]) = hh;
-                    if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.x[L1][j][xc]) = ll;
+                    *reinterpret_cast<bf16x8*>(&sm.x[0][lane][col]) = hh;
+                    if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&sm.x[L1][lane][col]) = ll;
                 }
             }
         }
@@ -351,13 +381,12 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) cfh[ks] = raw.c[ks][0];
             } else {
+                const TIN* cp = cg - cstep;   // load_raw(c) already advanced cg past chunk c
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     typename RW::v8 cv[RW::V8N];
-                    if (ic < qv) ld8(Cp + (row0 + ic) * a.ldc + 32 * ks + 8 * q4, cv);
-                    else
-#pragma unroll
-                        for (int u = 0; u < RW::V8N; ++u) cv[u] = vzero<typename RW::v8>();
+                    if (ic < qv) ld8(cp + 32 * ks, cv);
+                    else z8(cv);
                     if constexpr (sizeof(TIN) == 4) {
 #pragma unroll
                         for (int u = 0; u < 2; ++u) {
@@ -389,12 +418,14 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                 for (int pb = 0; pb < P / 16; ++pb) {
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks) {
-                        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(
-                            &sm.s[0][16 * pb + l16][32 * ks + 8 * q4]);
+                        // S[p = 16pb + l16][n = 32ks + 8q4 + 0..7] from the state^T tile
+                        const int n0 = 32 * ks + 8 * q4;
+                        const bf16x8 ah = cat(tr_read<SM::XP>(&sm.s[0][0][0], n0, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.s[0][0][0], n0 + 4, 16 * pb, l16));
                         Y[pb] = mfma(ah, cfh[ks], Y[pb]);
                         if constexpr (SPLIT) {
-                            const bf16x8 al = *reinterpret_cast<const bf16x8*>(
-                                &sm.s[L1][16 * pb + l16][32 * ks + 8 * q4]);
+                            const bf16x8 al = cat(tr_read<SM::XP>(&sm.s[L1][0][0], n0, 16 * pb, l16),
+                                                  tr_read<SM::XP>(&sm.s[L1][0][0], n0 + 4, 16 * pb, l16));
                             Y[pb] = mfma(ah, cfl[ks], Y[pb]);
                             Y[pb] = mfma(al, cfh[ks], Y[pb]);
                         }
