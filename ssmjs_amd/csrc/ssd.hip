@@ -11,7 +11,7 @@
 //   Y_off     Y^T[p,i] = exp(acum_i) * sum_n S[p,n] C[i,n]              (MFMA, K = N)
 //   Y_diag    S^T[j,i] = sum_n B[j,n] C[i,n]; mask j <= i; * exp(acum_i - acum_j) dt'_j;
 //             Y^T[p,i] += sum_j X^T[p,j] S^T[j,i]                          (MFMA, K = N, Q)
-//   output    y[i,p] = Y^T[p,i] + D_h x[i,p]
+//             with D_h added on the diagonal j == i, so Y^T is y^T
 //   state     S = exp(acum_end) S + (X w)^T B                             (MFMA, K = Q)
 // MFMA is v_mfma_f32_16x16x32_bf16 with fp32 accumulation. SPLIT (float inputs) writes each
 // operand as hi = bf16(v), lo = bf16(v - hi) and accumulates hi*hi + hi*lo + lo*hi, which keeps
@@ -132,20 +132,45 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
 
 // Per-thread raw prefetch of one chunk: X row j = lane, columns 16w..16w+15 (so the lane that
 // owns time step j also owns its weight w_j); B rows t/(NN/8) + (256/(NN/8)) k, 8 elements at
-// 8 (t % (NN/8)); the C fragments of the wave's strip; dt of time step lane.
-template <typename TIN, int NN, bool PRE_C>
+// 8 (t % (NN/8)); dt of time step lane. The C fragments of the wave's strip are prefetched
+// separately (they are still in use when the X / B prefetch is issued).
+template <typename TIN, int NN>
 struct Raw {
     static constexpr int KS = NN / 32;
     static constexpr int BL = NN / 8;          // lanes per B row
     static constexpr int BR = 256 / BL;        // B rows per pass
     static constexpr int BPASS = Q / BR;
     using v8 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x8>::type;
-    static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // v8 units per 8 elements
+    static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // 16-byte units per 8 elements
     v8 x[2][V8N];
     v8 b[BPASS][V8N];
-    v8 c[PRE_C ? KS : 1][V8N];
     float dt;
 };
+
+// Range-checked buffer access (raw buffer, stride 0, dword 3 = 0x00020000 on gfx9): a lane
+// whose byte offset lies at or past num_records reads zeros and its stores are dropped.
+// Every chunk gets descriptors whose num_records ends with its last valid time step, so the
+// rows past the sequence end need no branches and every chunk issues the same memory
+// instructions (the compiler can then count them exactly in its vmcnt waits).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+template <typename V>
+__device__ __forceinline__ V bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float bload4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ void bstore16(float4 v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+}
 
 // Inclusive prefix sum over the 64 lanes with DPP (row_shr inside rows of 16, then
 // row_bcast:15 / row_bcast:31 across rows); no LDS traffic.
@@ -173,14 +198,15 @@ __device__ __forceinline__ V vzero() {
     return v;
 }
 
+// Two workgroups per CU where the LDS tile allows it (bf16 inputs: <= 56 KB each), so each
+// SIMD interleaves two waves' MFMA, LDS and VALU phases; this caps registers at 256 per lane.
 template <typename TIN, bool SPLIT, int NN, bool FULL>
-__global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
+__global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
     __shared__ __attribute__((aligned(16))) Smem<SPLIT, NN, FULL> sm;
     using SM = Smem<SPLIT, NN, FULL>;
     constexpr int NB = NN / 16;   // state n-blocks per wave
     constexpr int KS = NN / 32;   // k-steps over n
-    constexpr bool PRE_C = FULL && sizeof(TIN) == 2;
-    using RW = Raw<TIN, NN, PRE_C>;
+    using RW = Raw<TIN, NN>;
     constexpr int L1 = SPLIT ? 1 : 0;   // index of the lo copy (aliases hi when unused)
 
     int wg = blockIdx.x;
@@ -192,7 +218,10 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     const int bh = wg / a.nseg;
     const int h = bh % a.H, b = bh / a.H;
     const int g = h / (a.H / a.G);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // w is wave-uniform: readfirstlane lets the compiler keep it (and the j-block loop
+    // bounds derived from it) in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, q4 = lane >> 4;
     const int ic = 16 * w + l16;        // this lane's output row in the chunk
     const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);      // B staging row / column
@@ -204,58 +233,55 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
     const int c_begin = seg * a.chunks_per_seg;
     const int c_end = min(c_begin + a.chunks_per_seg, a.nchunks);
 
-    // Per-thread global pointers at chunk c_begin, advanced by one chunk per iteration.
-    const long rbase = (long)b * a.L + (long)c_begin * Q;
-    const TIN* xg = reinterpret_cast<const TIN*>(a.x) + (rbase + lane) * a.ldx + (long)h * P + 16 * w;
-    const TIN* bg = reinterpret_cast<const TIN*>(a.Bm) + (rbase + br) * a.ldb + (long)g * a.N + bc;
-    const TIN* cg = reinterpret_cast<const TIN*>(a.Cm) + (rbase + ic) * a.ldc + (long)g * a.N + 8 * q4;
-    const float* dtg = a.dt + (rbase + lane) * a.lddt + h;
-    const long xstep = (long)Q * a.ldx, bstep = (long)Q * a.ldb, cstep = (long)Q * a.ldc,
-               dstep = (long)Q * a.lddt;
+    // Chunk c starts at row b*L + c*Q of every (B, L, ...) tensor; per-lane byte offsets
+    // inside a chunk are the same for every chunk (the host checks that Q rows of every
+    // tensor span less than 2^31 bytes).
+    constexpr unsigned SZ = sizeof(TIN);
+    const long brow = (long)b * a.L;
+    const TIN* x0 = reinterpret_cast<const TIN*>(a.x) + brow * a.ldx + (long)h * P;
+    const TIN* b0 = reinterpret_cast<const TIN*>(a.Bm) + brow * a.ldb + (long)g * a.N;
+    const TIN* cm0 = reinterpret_cast<const TIN*>(a.Cm) + brow * a.ldc + (long)g * a.N;
+    const float* d0 = a.dt + brow * a.lddt + h;
+    const unsigned ox = (unsigned)(lane * a.ldx + 16 * w) * SZ;
+    const unsigned ob = (unsigned)(br * a.ldb + bc) * SZ;
+    const unsigned obk = (unsigned)(RW::BR * a.ldb) * SZ;
+    const unsigned oc = (unsigned)(ic * a.ldc + 8 * q4) * SZ;
+    const unsigned od = (unsigned)(lane * a.lddt) * 4u;
+    // rows of chunk c that exist; 0 past the segment, so a prefetch there reads nothing
+    auto rows_of = [&](int c) { return c < c_end ? min(Q, a.L - c * Q) : 0; };
+    auto span = [](int qv, long ld, int width, unsigned esz) {
+        return qv > 0 ? (unsigned)(((long)(qv - 1) * ld + width) * esz) : 0u;
+    };
 
     RW raw;
-    auto ld8 = [&](const TIN* p, typename RW::v8* out) {
-#pragma unroll
-        for (int u = 0; u < RW::V8N; ++u) out[u] = *reinterpret_cast<const typename RW::v8*>(p + 4 * u);
-    };
-    auto z8 = [&](typename RW::v8* out) {
-#pragma unroll
-        for (int u = 0; u < RW::V8N; ++u) out[u] = vzero<typename RW::v8>();
-    };
-    // rows past the sequence end are never read: their slots are zero (uniform branch on
-    // the chunk being partial, so full chunks carry no per-row guards)
-    // xg / bg / cg / dtg always point at the chunk load_raw reads next
+    using v8 = typename RW::v8;
     auto load_raw = [&](int c) {
-        const int qv = min(Q, a.L - c * Q);
-        const TIN* xp = xg;
-        const TIN* bp = bg;
-        const TIN* cp = cg;
-        if (qv == Q) {
-            ld8(xp, raw.x[0]);
-            ld8(xp + 8, raw.x[1]);
+        const int qv = rows_of(c);
+        const long r0 = (long)c * Q;
+        const auto rd = rsrc(d0 + r0 * a.lddt, span(qv, a.lddt, 1, 4));
+        const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
+        const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
+        raw.dt = bload4(rd, od);
 #pragma unroll
-            for (int k = 0; k < RW::BPASS; ++k) ld8(bp + (long)RW::BR * k * a.ldb, raw.b[k]);
-            if constexpr (PRE_C)
+        for (int hlf = 0; hlf < 2; ++hlf)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) ld8(cp + 32 * ks, raw.c[ks]);
-            raw.dt = *dtg;
-        } else {
-            if (lane < qv) { ld8(xp, raw.x[0]); ld8(xp + 8, raw.x[1]); }
-            else { z8(raw.x[0]); z8(raw.x[1]); }
+            for (int u = 0; u < RW::V8N; ++u) raw.x[hlf][u] = bload16<v8>(rx, ox + (8 * hlf + 4 * u) * SZ);
 #pragma unroll
-            for (int k = 0; k < RW::BPASS; ++k) {
-                if (br + RW::BR * k < qv) ld8(bp + (long)RW::BR * k * a.ldb, raw.b[k]);
-                else z8(raw.b[k]);
-            }
-            if constexpr (PRE_C)
+        for (int k = 0; k < RW::BPASS; ++k)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    if (ic < qv) ld8(cp + 32 * ks, raw.c[ks]);
-                    else z8(raw.c[ks]);
-                }
-            raw.dt = lane < qv ? *dtg : 0.f;
+            for (int u = 0; u < RW::V8N; ++u) raw.b[k][u] = bload16<v8>(rb, ob + k * obk + 4 * u * SZ);
+    };
+    // C rows of the wave's strip: row ic, n = 32ks + 8q4 + 0..7 (MFMA B-operand fragments)
+    v8 craw[FULL ? KS : 1][RW::V8N];
+    auto load_c = [&](int c) {
+        if constexpr (FULL) {
+            const int qv = rows_of(c);
+            const auto rc = rsrc(cm0 + (long)c * Q * a.ldc, span(qv, a.ldc, NN, SZ));
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int u = 0; u < RW::V8N; ++u) craw[ks][u] = bload16<v8>(rc, oc + (32 * ks + 4 * u) * SZ);
         }
-        xg += xstep; bg += bstep; cg += cstep; dtg += dstep;
     };
 
     // ---- entering state -> accumulators (wave w: rows p = 16w + 4*q4 + r, cols 16nb + l16)
@@ -289,7 +315,16 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
         }
     };
     if (FULL && state_live) write_state_lds();
-    if (c_begin < c_end) load_raw(c_begin);
+    load_raw(c_begin);
+    load_c(c_begin);
+    if constexpr (FULL) {
+        // Four stores into an empty range (dropped by the range check) make the memory
+        // instructions in flight at loop entry match the back edge (C loads, then the four
+        // y stores), so the wait for C never includes the previous chunk's stores.
+        const auto none = rsrc(a.y, 0u);
+#pragma unroll
+        for (int pb = 0; pb < P / 16; ++pb) bstore16(make_float4(0.f, 0.f, 0.f, 0.f), none, 64u * pb);
+    }
 
     for (int c = c_begin; c < c_end; ++c) {
         const int t0 = c * Q;
@@ -297,13 +332,10 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
         const long row0 = (long)b * a.L + t0;
 
         // ---- dt' and the inclusive prefix of dt' * A (every wave; lane = time step)
-        float dv = 0.f, av = 0.f;
-        if (lane < qv) {
-            dv = raw.dt + dtb;
-            if (a.softplus) dv = ssm::softplus_fast(dv);
-            dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
-            av = dv * Ah;
-        }
+        float dv = raw.dt + dtb;
+        if (a.softplus) dv = ssm::softplus_fast(dv);
+        dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
+        const float av = dv * Ah;
         const float sc = wave_prefix_sum(av);
         const float acend = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
@@ -377,25 +409,18 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
         // ---- C rows of this wave's strip as MFMA fragments: row ic, n = 32ks + 8q4 + 0..7
         bf16x8 cfh[FULL ? KS : 1], cfl[FULL ? KS : 1];
         if constexpr (FULL) {
-            if constexpr (PRE_C) {
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) cfh[ks] = raw.c[ks][0];
-            } else {
-                const TIN* cp = cg - cstep;   // load_raw(c) already advanced cg past chunk c
+            for (int ks = 0; ks < KS; ++ks) {
+                if constexpr (sizeof(TIN) == 2) {
+                    cfh[ks] = craw[ks][0];
+                } else {
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    typename RW::v8 cv[RW::V8N];
-                    if (ic < qv) ld8(cp + 32 * ks, cv);
-                    else z8(cv);
-                    if constexpr (sizeof(TIN) == 4) {
+                    for (int u = 0; u < 2; ++u) {
+                        const float e4[4] = {craw[ks][u].x, craw[ks][u].y, craw[ks][u].z, craw[ks][u].w};
 #pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            const float e4[4] = {cv[u].x, cv[u].y, cv[u].z, cv[u].w};
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                cfh[ks][4 * u + e] = hi_of(e4[e]);
-                                cfl[ks][4 * u + e] = lo_of(e4[e], cfh[ks][4 * u + e]);
-                            }
+                        for (int e = 0; e < 4; ++e) {
+                            cfh[ks][4 * u + e] = hi_of(e4[e]);
+                            cfl[ks][4 * u + e] = lo_of(e4[e], cfh[ks][4 * u + e]);
                         }
                     }
                 }
@@ -403,8 +428,9 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
         }
         __syncthreads();   // staging (and the state LDS copy) visible to every wave
 
-        // ---- the next chunk's raw inputs are in flight while this one computes
-        if (c + 1 < c_end) load_raw(c + 1);
+        // ---- the next chunk's raw inputs are in flight while this one computes (a chunk past
+        // the segment has an empty range: the loads return zeros without touching memory)
+        load_raw(c + 1);
 
         if constexpr (FULL) {
             const float aci = sm.ac[ic];
@@ -436,81 +462,98 @@ __global__ __launch_bounds__(256) void ssd_kernel(SsdArgs a) {
                 for (int pb = 0; pb < P / 16; ++pb) Y[pb] *= e;
             }
 
-            // ---- Y_diag over j-block pairs (2 x 16 rows of j per MFMA k-step)
-            for (int jb2 = 0; 2 * jb2 <= w; ++jb2) {
-                float sv[8];
+            // ---- Y_diag: wave w's rows i = 16w + l16 need the j-blocks 0..w. The body is
+            // unrolled per wave (switch on the wave-uniform w) so the independent C B^T chains
+            // of the j-blocks interleave. D_h x_i rides on the diagonal (j == i) of the decay
+            // matrix: y_i = sum_j (L[i,j] + D_h [i == j]) x_j.
+            auto y_diag = [&](auto wc) {
+                constexpr int W = decltype(wc)::value;
+                floatx4 st[W + 1];
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int jb = 2 * jb2 + half;
-                    if (jb <= w) {
-                        floatx4 st = {0.f, 0.f, 0.f, 0.f};
+                for (int jb = 0; jb <= W; ++jb) st[jb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                        for (int ks = 0; ks < KS; ++ks) {
-                            const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(
-                                &sm.b[0][16 * jb + l16][32 * ks + 8 * q4]);
-                            st = mfma(bh_, cfh[ks], st);
-                            if constexpr (SPLIT) {
-                                const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
-                                    &sm.b[L1][16 * jb + l16][32 * ks + 8 * q4]);
-                                st = mfma(bh_, cfl[ks], st);
-                                st = mfma(bl_, cfh[ks], st);
-                            }
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int jb = 0; jb <= W; ++jb) {
+                        const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(
+                            &sm.b[0][16 * jb + l16][32 * ks + 8 * q4]);
+                        st[jb] = mfma(bh_, cfh[ks], st[jb]);
+                        if constexpr (SPLIT) {
+                            const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
+                                &sm.b[L1][16 * jb + l16][32 * ks + 8 * q4]);
+                            st[jb] = mfma(bh_, cfl[ks], st[jb]);
+                            st[jb] = mfma(bl_, cfh[ks], st[jb]);
                         }
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int j = 16 * jb + 4 * q4 + r;
-                            sv[4 * half + r] =
-                                j <= ic ? st[r] * ssm::ex2((aci - sm.ac[j]) * ssm::kLog2e) * sm.dt[j]
-                                        : 0.f;
-                        }
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) sv[4 * half + r] = 0.f;
                     }
-                }
-                bf16x8 sfh, sfl;
+                // S^T[j, i] * exp(acum_i - acum_j) dt'_j for this lane's rows j = 16jb + 4q4 + r;
+                // below the diagonal block every j < i, on it j > i is masked by a select (the
+                // dropped exp may overflow)
+                float sv[2 * (W / 2 + 1)][4];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    sfh[k] = hi_of(sv[k]);
-                    sfl[k] = lo_of(sv[k], sfh[k]);
+                for (int jb = 0; jb < 2 * (W / 2 + 1); ++jb) {
+                    if (jb > W) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sv[jb][r] = 0.f;
+                        continue;
+                    }
+                    const float4 acj = *reinterpret_cast<const float4*>(&sm.ac[16 * jb + 4 * q4]);
+                    const float4 dtj = *reinterpret_cast<const float4*>(&sm.dt[16 * jb + 4 * q4]);
+                    const float ajr[4] = {acj.x, acj.y, acj.z, acj.w};
+                    const float djr[4] = {dtj.x, dtj.y, dtj.z, dtj.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float f = st[jb][r] * ssm::ex2((aci - ajr[r]) * ssm::kLog2e) * djr[r];
+                        if (jb < W) {
+                            sv[jb][r] = f;
+                        } else {
+                            const int dj = 4 * q4 + r;   // j - 16w
+                            sv[jb][r] = dj < l16 ? f : (dj == l16 ? f + Dh : 0.f);
+                        }
+                    }
                 }
                 // X^T fragment: k-slots 0..3 <-> j = 32 jb2 + 4 q4 + 0..3, 4..7 <-> +16
 #pragma unroll
-                for (int pb = 0; pb < P / 16; ++pb) {
-                    const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
-                                          tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
-                    Y[pb] = mfma(xh, sfh, Y[pb]);
-                    if constexpr (SPLIT) {
-                        const bf16x8 xl = cat(tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
-                                              tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
-                        Y[pb] = mfma(xh, sfl, Y[pb]);
-                        Y[pb] = mfma(xl, sfh, Y[pb]);
+                for (int jb2 = 0; jb2 <= W / 2; ++jb2) {
+                    bf16x8 sfh, sfl;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        sfh[r] = hi_of(sv[2 * jb2][r]);
+                        sfh[4 + r] = hi_of(sv[2 * jb2 + 1][r]);
+                        sfl[r] = lo_of(sv[2 * jb2][r], sfh[r]);
+                        sfl[4 + r] = lo_of(sv[2 * jb2 + 1][r], sfh[4 + r]);
+                    }
+#pragma unroll
+                    for (int pb = 0; pb < P / 16; ++pb) {
+                        const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
+                        Y[pb] = mfma(xh, sfh, Y[pb]);
+                        if constexpr (SPLIT) {
+                            const bf16x8 xl = cat(tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                                  tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
+                            Y[pb] = mfma(xh, sfl, Y[pb]);
+                            Y[pb] = mfma(xl, sfh, Y[pb]);
+                        }
                     }
                 }
+            };
+            switch (w) {
+                case 0: y_diag(std::integral_constant<int, 0>{}); break;
+                case 1: y_diag(std::integral_constant<int, 1>{}); break;
+                case 2: y_diag(std::integral_constant<int, 2>{}); break;
+                default: y_diag(std::integral_constant<int, 3>{}); break;
             }
 
-            // ---- y = Y + D x   (lane: row ic, p = 16pb + 4q4 + 0..3; x from the LDS tile)
-            if (ic < qv) {
-                const long r = row0 + ic;
+            // ---- the next chunk's C fragments (the last use of this chunk's was Y_diag)
+            load_c(c + 1);
+
+            // ---- y (lane: row ic, p = 16pb + 4q4 + 0..3); rows past the sequence end fall
+            // outside the descriptor and are dropped
+            {
+                const auto ry = rsrc(a.y + (row0 * a.ldy + (long)h * P), span(qv, a.ldy, P, 4));
+                const unsigned oy = (unsigned)(ic * a.ldy + 4 * q4) * 4u;
 #pragma unroll
-                for (int pb = 0; pb < P / 16; ++pb) {
-                    const int p0 = 16 * pb + 4 * q4;
-                    const bf16x4 xh4 = *reinterpret_cast<const bf16x4*>(&sm.x[0][ic][p0]);
-                    float xv[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) xv[k] = (float)xh4[k];
-                    if constexpr (SPLIT) {
-                        const bf16x4 xl4 = *reinterpret_cast<const bf16x4*>(&sm.x[L1][ic][p0]);
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) xv[k] += (float)xl4[k];
-                    }
-                    float4 o;
-                    o.x = fmaf(Dh, xv[0], Y[pb][0]);
-                    o.y = fmaf(Dh, xv[1], Y[pb][1]);
-                    o.z = fmaf(Dh, xv[2], Y[pb][2]);
-                    o.w = fmaf(Dh, xv[3], Y[pb][3]);
-                    *reinterpret_cast<float4*>(a.y + r * a.ldy + (long)h * P + p0) = o;
-                }
+                for (int pb = 0; pb < P / 16; ++pb)
+                    bstore16(make_float4(Y[pb][0], Y[pb][1], Y[pb][2], Y[pb][3]), ry, oy + 64u * pb);
             }
         }
 
@@ -795,8 +838,13 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
     SSM_REQUIRE(in_dtype == SSM_F32 || in_dtype == SSM_BF16, "ssm_ssd_chunk_scan: bad dtype");
     SSM_REQUIRE(B >= 0 && L >= 0 && H > 0 && G > 0 && H % G == 0 && Pd > 0 && N > 0,
                 "ssm_ssd_chunk_scan: bad shape");
-    const bool mfma_path = Pd == P && (N == 64 || N == 128);
     const long ev = in_dtype == SSM_F32 ? 4 : 8;   // vector-load element alignment
+    const long esz = in_dtype == SSM_F32 ? 4 : 2;
+    // the MFMA kernel addresses one chunk (Q rows) of every tensor with 32-bit byte offsets
+    const long lim = (1L << 31) / Q;
+    const bool offsets_fit = ldx * esz < lim && ldb * esz < lim && ldc * esz < lim &&
+                             ldy * 4 < lim && lddt * 4 < lim;
+    const bool mfma_path = Pd == P && (N == 64 || N == 128) && offsets_fit;
     SSM_REQUIRE(ldx >= (long)H * Pd && ldb >= (long)G * N && ldc >= (long)G * N &&
                     ldy >= (long)H * Pd && lddt >= H,
                 "ssm_ssd_chunk_scan: row stride below row width");
