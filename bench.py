@@ -34,13 +34,27 @@ PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0}   # dense MFMA, TFLOP/s
 
 METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 
+# Measured HBM bytes per launch of each workload's dominant stage: rocprofv3 --pmc FETCH_SIZE
+# and WRITE_SIZE (one counter per run) of `bench.py --workload <w>`, FETCH_SIZE scaled by 2.0
+# and WRITE_SIZE by 1.0 (what `bench.py --workload copy`, 1 GiB read + 1 GiB written, reads on
+# the same counters). Table and commands: profiles/hbm_traffic.md. Re-measured when the
+# kernels change; None where not measured.
+TRAFFIC = {
+    ("cfg2", "m1.in_proj"): 387_553_280,               # rocBLAS sgemm (tile re-reads)
+    ("cfg3", "bf16"): 868_595_712,                     # ssd_kernel
+    ("cfg3", "f32"): 1_167_515_648,                    # ssd_kernel (fp32 inputs)
+    ("cfg4", "m2.step.state_update"): 136_052_736,     # m2_update_kernel
+    ("cfg5", "bf16"): 1_215_353_856,                   # state pass + combine + full pass
+}
+
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--workload", default="cfg2",
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "copy"])
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
@@ -76,7 +90,7 @@ def profiled_stages(dev, torch, fn, steps):
     return {k: (n, ms / n) for k, (n, ms) in rep.items()}   # stage -> (launches, avg ms)
 
 
-def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None):
+def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None, traffic=None):
     """Achieved rate of one kernel/stage against its binding peak."""
     t = avg_ms * 1e-3
     if bound is None:
@@ -92,7 +106,7 @@ def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None):
         peak = HBM_PEAK_GBS
         unit = "GB/s"
     return {"kernel": name, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
-            "frac": round(ach / peak, 4), "traffic": None, "avg_ms": round(avg_ms, 5),
+            "frac": round(ach / peak, 4), "traffic": traffic, "avg_ms": round(avg_ms, 5),
             "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
 
 
@@ -143,7 +157,7 @@ def w_cfg2(torch, np, dev, args):
     for k, (n, avg) in st.items():
         f, b = alg[k]
         bound = "hbm" if f is None else None
-        stages[k] = roofline(k, avg, f, b, "f32", bound)
+        stages[k] = roofline(k, avg, f, b, "f32", bound, TRAFFIC.get(("cfg2", k)))
     dom = max(stages.values(), key=lambda r: r["avg_ms"])
     out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
            "dtype": "f32",
@@ -250,7 +264,8 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype):
                       "d_state": N, "groups": 1, "chunk_len": Q, "input_dtype": dtype,
                       "accumulate": "f32"},
            "roofline": roofline("ssd_chunk_scan", ms, flops, nbytes,
-                                "bf16" if dtype == "bf16" else "f32")}
+                                "bf16" if dtype == "bf16" else "f32",
+                                traffic=TRAFFIC.get((name[:4], dtype)))}
     out["roofline"]["mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 /
                                          PEAK_TFLOPS["bf16" if dtype == "bf16" else "f32"], 4)
     out["roofline"]["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
@@ -308,7 +323,8 @@ def w_cfg4(torch, np, dev, args):
     for kk, (nl_, avg) in stg.items():
         if kk in alg:
             f, b = alg[kk]
-            stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None)
+            stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None,
+                                  TRAFFIC.get(("cfg4", kk)))
     step_bytes = nl * sum(v[1] for v in alg.values()) + 4.0 * V * d
     dom = max(stages.values(), key=lambda r_: r_["avg_ms"])
     out = {"value": Bsz / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
@@ -337,6 +353,20 @@ def w_cfg4(torch, np, dev, args):
     return out
 
 
+def w_copy(torch, args):
+    """Counter calibration, not a bench line: one elementwise kernel (y = x * 1) that reads
+    and writes exactly 1 GiB each, so FETCH_SIZE / WRITE_SIZE of a rocprofv3 --pmc run can be
+    scaled to bytes."""
+    n = (1 << 30) // 4
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(args.steps or 3):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    return {"calibration": "copy", "kernel": "elementwise mul (torch)", "bytes_read": 4 * n,
+            "bytes_written": 4 * n, "launches": args.steps or 3}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -358,6 +388,10 @@ def main():
     torch.cuda.set_stream(stream)
     dev.set_stream(stream.cuda_stream)
     log(f"[bench] device {dev.arch} with {dev.compute_units} CUs; workload {args.workload}")
+    if args.workload == "copy":
+        print(json.dumps(w_copy(torch, args)), flush=True)
+        dev.destroy()
+        return
     if args.workload == "cfg1":
         r = w_cfg1(torch, np, dev, args)
     elif args.workload == "cfg2":

@@ -1,7 +1,9 @@
 """Builds ssmjs_amd/libssm_hip.so (the C ABI in include/ssm_hip.h) for gfx950 with hipcc.
 
 Each .hip source under ssmjs_amd/csrc is compiled separately (in parallel) and linked
-against rocBLAS. Usage:  python -m ssmjs_amd.build  [-j N]
+against rocBLAS. When Node's headers are installed, the Node-API addon
+ssmjs_amd/napi/ssm_napi.node (the binding the TypeScript host loads) is built next to it
+with the host compiler. Usage:  python -m ssmjs_amd.build  [-j N]
 """
 from __future__ import annotations
 
@@ -19,6 +21,9 @@ LIB = os.path.join(HERE, "libssm_hip.so")
 SOURCES = ["conv1d.hip", "scan_m1.hip", "ssd.hip", "glue.hip", "model.hip"]
 ARCH = os.environ.get("SSM_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+NAPI_SRC = os.path.join(HERE, "napi", "ssm_napi.cc")
+NAPI_OUT = os.path.join(HERE, "napi", "ssm_napi.node")
+NODE_INCLUDE = os.environ.get("NODE_INCLUDE", "/usr/include/node")
 
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
@@ -51,7 +56,24 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)
+    if build_napi() and verbose:
+        print("built", NAPI_OUT)
     return LIB
+
+
+def build_napi() -> bool:
+    """Node-API addon over libssm_hip.so; skipped (False) when node_api.h is absent."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        return False
+    tmp = NAPI_OUT + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-shared", "-fPIC", "-Wall",
+           "-DNODE_GYP_MODULE_NAME=ssm_napi", "-I", NODE_INCLUDE, NAPI_SRC, "-o", tmp,
+           "-L" + HERE, "-lssm_hip", "-Wl,-rpath,$ORIGIN/.."]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"Node-API addon build failed:\n{r.stderr[-4000:]}")
+    os.replace(tmp, NAPI_OUT)
+    return True
 
 
 if __name__ == "__main__":

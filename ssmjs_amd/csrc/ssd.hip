@@ -214,8 +214,10 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         const int per = gridDim.x / 8;
         wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
     }
-    const int seg = wg % a.nseg;
-    const int bh = wg / a.nseg;
+    // segment-major order: the heads of one (batch, segment) are adjacent, so after the
+    // XCD remap they run on the same XCD and read that segment's B and C through one L2
+    const int seg = wg / (a.B * a.H);
+    const int bh = wg % (a.B * a.H);
     const int h = bh % a.H, b = bh / a.H;
     const int g = h / (a.H / a.G);
     // w is wave-uniform: readfirstlane lets the compiler keep it (and the j-block loop

@@ -1,8 +1,8 @@
 """MambaSession on the MI355X backend (mirrors src/session/session.ts:206-616).
 
 Same method names, option names, defaults and SessionError codes as the reference. The
-methods are synchronous here (the reference's are async; the Node-API host in addon/ keeps
-the Promise API). Out of this backend's scope, with the reason:
+methods are synchronous here (the reference's are async; the Node-API binding in
+ssmjs_amd/napi keeps the Promise API). Out of this backend's scope, with the reason:
   - BPETokenizer loading (network vocab files): pass `tokenizer` (session.ts:326-334);
   - adapt() (training, MambaTrainer.train): raises after the reference's INPUT_TOO_SHORT check;
   - IndexedDB / download storage (browser APIs): `idbFactory` may be any mutable mapping,

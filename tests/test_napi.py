@@ -1,0 +1,112 @@
+"""The Node-API binding (ssmjs_amd/napi): the module the reference's TypeScript host loads in
+place of MambaCode.js (src/session/session.ts:10-18). CPU tests check that the addon loads
+under Node and maps a missing device to GPU_UNAVAILABLE (session.ts:262-270); the GPU test
+drives initWebGPU -> HybridMambaModel -> loadWeights / generate / forward / evaluate /
+exportWeights / destroy from Node and checks the results against the CPU oracle."""
+import json
+import os
+import shutil
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ADDON = os.path.join(ROOT, "ssmjs_amd", "napi", "ssm_napi.node")
+NODE = shutil.which("node")
+
+needs_addon = pytest.mark.skipif(NODE is None or not os.path.exists(ADDON),
+                                 reason="node or the built addon is absent")
+
+
+def _node(code, env=None, timeout=120):
+    return subprocess.run([NODE, "-e", code], capture_output=True, text=True, cwd=ROOT,
+                          env=env, timeout=timeout)
+
+
+@needs_addon
+def test_addon_exports_the_binding():
+    r = _node("const a = require('./ssmjs_amd/napi/ssm_napi.node');"
+              "const m = require('./ssmjs_amd/napi');"
+              "console.log(JSON.stringify({a: Object.keys(a), m: Object.keys(m), v: a.version()}))")
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout)
+    assert set(out["a"]) >= {"ctxCreate", "ctxDestroy", "modelCreate", "modelDestroy", "loadWeights",
+                             "exportWeights", "forward", "stateCreate", "prefill", "decodeStep",
+                             "generateGreedy"}
+    assert set(out["m"]) >= {"initWebGPU", "HybridMambaModel", "MambaTrainer", "sampleToken"}
+    assert out["v"] >= 1
+
+
+@needs_addon
+def test_no_device_rejects_with_gpu_unavailable():
+    env = dict(os.environ, SSM_HIP_FAULT="nodevice")
+    r = _node("require('./ssmjs_amd/napi').initWebGPU({}).then(() => console.log('OK'),"
+              " (e) => console.log(e.code))", env=env)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "GPU_UNAVAILABLE"
+
+
+@needs_addon
+def test_js_sample_token_matches_python():
+    from ssmjs_amd import sampleToken
+    lg = [0.1, 3.0, -2.0, 3.0, 1.0, 2.5]
+    cases = [(0.8, 1, 0.9, 0.3), (1.0, 50, 0.7, 0.0), (1.0, 50, 0.7, 0.99), (1.0, 3, 1.0, 0.999),
+             (0.0, 50, 0.9, 0.99)]
+    code = ("const m = require('./ssmjs_amd/napi'); const lg = Float32Array.from(%s);"
+            "console.log(JSON.stringify(%s.map(c => m.sampleToken(lg, c[0], c[1], c[2], () => c[3]))))"
+            % (json.dumps(lg), json.dumps(cases)))
+    r = _node(code)
+    assert r.returncode == 0, r.stderr
+    js = json.loads(r.stdout)
+    py = [sampleToken(np.array(lg, np.float32), t, k, p, rng=lambda r_=r_: r_) for t, k, p, r_ in cases]
+    assert js == py
+
+
+@pytest.mark.gpu
+@needs_addon
+def test_node_session_path_matches_oracle(tmp_path):
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    print("[case] node: initWebGPU -> HybridMambaModel -> generate/forward/evaluate", flush=True)
+    from oracle import oracle as O
+    from ssmjs_amd import backend, checkpoint
+    cfg = {"vocabSize": 256, "dModel": 128, "numLayers": 2, "dState": 64, "dConv": 4, "expand": 2,
+           "nHeads": 2, "nGroups": 1, "layers": [{"type": "mamba2"}, {"type": "mamba1"}]}
+    d = backend.Device(0)
+    m = backend.Model(d, cfg, seed=21)
+    dims, T = checkpoint.unpack(m.export_weights())
+    m.destroy()
+    d.destroy()
+    T["embedding"] = T["embedding"] * 40.0          # wide top-1 margins for bit-exact greedy
+    blob = checkpoint.pack(dims, T)
+    ck, cj = tmp_path / "w.ssmw", tmp_path / "cfg.json"
+    ck.write_bytes(blob)
+    cj.write_text(json.dumps(cfg))
+    prompt = list(b"Mamba on MI355X")
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "napi_check.js"), str(ck), str(cj),
+                        ",".join(map(str, prompt)), "16"],
+                       capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout)
+    om = O.Model(blob)
+    ids, margins = O.greedy(om, np.array([prompt], np.uint32), 16)
+    assert margins.min() > 1e-3
+    assert out["generated"] == prompt + ids[0].tolist()
+    assert out["sampled"][:len(prompt)] == prompt and len(out["sampled"]) == len(prompt) + 4
+    ref = om.forward(np.array([prompt], np.uint32))[0]
+    lg = np.array(out["logits"], np.float32).reshape(len(prompt), 256)
+    assert np.abs(lg - ref).max() / np.abs(ref).max() <= 1e-4
+    assert out["badCode"] == "CHECKPOINT_INVALID"
+    assert out["destroyedCode"] == "SESSION_DESTROYED"
+    assert out["exportedBytes"] == len(blob)
+    text = list(b"hello mamba")
+    lgt = om.forward(np.array([text], np.uint32))[0, :-1].astype(np.float64)
+    mx = lgt.max(1)
+    lse = mx + np.log(np.exp(lgt - mx[:, None]).sum(1))
+    nll = float((lse - lgt[np.arange(len(lgt)), text[1:]]).mean())
+    # mean NLL moves by at most twice the logits' error (1e-4 of their range)
+    assert abs(np.log(out["ppl"]) - nll) <= 2e-4 * np.abs(lgt).max()
+    sys.stdout.flush()
