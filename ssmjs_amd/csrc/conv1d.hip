@@ -77,6 +77,29 @@ __global__ __launch_bounds__(256) void conv1d_fwd(const float* __restrict__ x, l
                                 : 0.f;
         }
     }
+    if (t0 + kTT <= L) {
+        // full run: all kTT input rows are issued before the first use (kTT + K - 1 loads in
+        // flight per thread), then the window slides over registers
+        float xs[kTT][VEC];
+#pragma unroll
+        for (int i = 0; i < kTT; ++i) load_v<VEC>(xb + (long)(t0 + i) * ldx, xs[i]);
+#pragma unroll
+        for (int i = 0; i < kTT; ++i) {
+            float out[VEC];
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                float acc = bv[v];
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    const int src = i - (K - 1) + k;   // < 0: from the carried window
+                    acc = fmaf(wk[k][v], src < 0 ? win[K - 1 + src][v] : xs[src][v], acc);
+                }
+                out[v] = silu ? ssm::silu_fast(acc) : acc;
+            }
+            store_v<VEC>(yb + (long)(t0 + i) * ldy, out);
+        }
+        return;
+    }
     const int tend = min(t0 + kTT, L);
     for (int t = t0; t < tend; ++t) {
         load_v<VEC>(xb + (long)t * ldx, win[K - 1]);
@@ -86,7 +109,7 @@ __global__ __launch_bounds__(256) void conv1d_fwd(const float* __restrict__ x, l
             float acc = bv[v];
 #pragma unroll
             for (int k = 0; k < K; ++k) acc = fmaf(wk[k][v], win[k][v], acc);
-            out[v] = silu ? ssm::silu(acc) : acc;
+            out[v] = silu ? ssm::silu_fast(acc) : acc;
         }
         store_v<VEC>(yb + (long)t * ldy, out);
 #pragma unroll
@@ -128,7 +151,7 @@ __global__ void conv1d_update_kernel(const float* __restrict__ x, long ldx,
     acc = fmaf(w[(long)c * K + K - 1], xn, acc);
     for (int k = 0; k + 1 < K - 1; ++k) st[k] = st[k + 1];
     if (K > 1) st[K - 2] = xn;
-    y[(long)b * ldy + c] = silu ? ssm::silu(acc) : acc;
+    y[(long)b * ldy + c] = silu ? ssm::silu_fast(acc) : acc;
 }
 
 template <int K>

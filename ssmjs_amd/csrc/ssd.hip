@@ -653,75 +653,62 @@ void plan(int B, int L, int H, int& nchunks, int& nseg, int& per) {
 }
 
 // ---------------------------------------------------------------- one-token update (K7)
-// Workgroup per (b, h): lanes run along n in float4 steps (N/4 lanes per row of the state),
-// rows p are spread over the remaining lanes and looped. y[p] reduces over the row's lanes.
-// Persistent form: a bounded grid walks the (b, h) tiles; each thread owns the same float4
-// slots of every tile it visits and prefetches the next tile's state while it updates and
-// writes back the current one, so reads and write-backs overlap across the whole kernel.
-template <int LPR, int MAXR>
+// HBM-bound: the (B,H,P,N) state is read and written once. Work split: a workgroup owns R
+// passes of RPP = 256 / LPR rows of one (b, h) state (LPR = N / 4 lanes per row, one float4
+// each), so the grid is B*H*ceil(P / (RPP*R)) workgroups of straight-line code, each thread
+// with R state loads in flight; y[p] = C . h[p,:] + D x[p] is reduced over the row's lanes.
+template <int LPR, int R>
 __global__ __launch_bounds__(256) void m2_update_kernel(
     const float* __restrict__ x, long ldx, const float* __restrict__ dt, long lddt,
     const float* __restrict__ dt_bias, int softplus, float dt_min, float dt_max,
     const float* __restrict__ A, const float* __restrict__ Bm, long ldb,
     const float* __restrict__ Cm, long ldc, const float* __restrict__ Dsk,
     const float* __restrict__ z, long ldz, float* __restrict__ y, long ldy,
-    float* __restrict__ hs, int B, int H, int Pd, int G, int N) {
-    constexpr int RPP = 256 / LPR;      // rows per pass; MAXR * RPP >= Pd
+    float* __restrict__ hs, int H, int Pd, int G, int N, int blocks_per_head) {
+    constexpr int RPP = 256 / LPR;
     const int tid = threadIdx.x;
-    const int c4 = tid % LPR;           // float4 column
-    const int rsub = tid / LPR;         // first row
-    const int ntiles = B * H;
-    float4 v[MAXR];
-    auto load_tile = [&](int bh) {
-        const float* hb = hs + (long)bh * Pd * N;
+    const int c4 = tid % LPR;            // float4 column
+    const int rsub = tid / LPR;
+    const int bh = blockIdx.x / blocks_per_head;
+    const int p0 = (blockIdx.x % blocks_per_head) * RPP * R + rsub;
+    const int h = bh % H, b = bh / H, g = h / (H / G);
+    float* hb = hs + (long)bh * Pd * N;
+
+    float4 v[R];
+    float xp[R];
 #pragma unroll
-        for (int k = 0; k < MAXR; ++k) {
-            const int p = rsub + k * RPP;
-            if (p < Pd) v[k] = *(reinterpret_cast<const float4*>(hb + (long)p * N) + c4);
+    for (int k = 0; k < R; ++k) {
+        const int p = p0 + k * RPP;
+        if (p < Pd) {
+            v[k] = *(reinterpret_cast<const float4*>(hb + (long)p * N) + c4);
+            xp[k] = x[(long)b * ldx + (long)h * Pd + p];
         }
-    };
-    int bh = blockIdx.x;
-    if (bh < ntiles) load_tile(bh);
-    for (; bh < ntiles; bh += gridDim.x) {
-        const int h = bh % H, b = bh / H, g = h / (H / G);
-        float dl = dt[(long)b * lddt + h] + (dt_bias ? dt_bias[h] : 0.f);
-        if (softplus) dl = ssm::softplus(dl);
-        dl = fminf(fmaxf(dl, dt_min), dt_max);
-        const float dA = ssm::ex2(dl * A[h] * ssm::kLog2e);
-        const float Dh = Dsk ? Dsk[h] : 0.f;
-        const float4 bv = *reinterpret_cast<const float4*>(Bm + (long)b * ldb + (long)g * N + 4 * c4);
-        const float4 cv = *reinterpret_cast<const float4*>(Cm + (long)b * ldc + (long)g * N + 4 * c4);
-        float xp[MAXR];
+    }
+    const float4 bv = *reinterpret_cast<const float4*>(Bm + (long)b * ldb + (long)g * N + 4 * c4);
+    const float4 cv = *reinterpret_cast<const float4*>(Cm + (long)b * ldc + (long)g * N + 4 * c4);
+    float dl = dt[(long)b * lddt + h] + (dt_bias ? dt_bias[h] : 0.f);
+    if (softplus) dl = ssm::softplus(dl);
+    dl = fminf(fmaxf(dl, dt_min), dt_max);
+    const float dA = ssm::ex2(dl * A[h] * ssm::kLog2e);
+    const float Dh = Dsk ? Dsk[h] : 0.f;
 #pragma unroll
-        for (int k = 0; k < MAXR; ++k) {
-            const int p = rsub + k * RPP;
-            xp[k] = p < Pd ? x[(long)b * ldx + (long)h * Pd + p] : 0.f;
-        }
-        float4 cur[MAXR];
+    for (int k = 0; k < R; ++k) {
+        const int p = p0 + k * RPP;
+        if (p >= Pd) break;
+        const float dx = dl * xp[k];
+        float4 u = v[k];
+        u.x = fmaf(dA, u.x, dx * bv.x);
+        u.y = fmaf(dA, u.y, dx * bv.y);
+        u.z = fmaf(dA, u.z, dx * bv.z);
+        u.w = fmaf(dA, u.w, dx * bv.w);
+        *(reinterpret_cast<float4*>(hb + (long)p * N) + c4) = u;
+        float acc = u.x * cv.x + u.y * cv.y + u.z * cv.z + u.w * cv.w;
 #pragma unroll
-        for (int k = 0; k < MAXR; ++k) cur[k] = v[k];
-        const int nxt = bh + gridDim.x;
-        if (nxt < ntiles) load_tile(nxt);
-        float* hb = hs + (long)bh * Pd * N;
-#pragma unroll
-        for (int k = 0; k < MAXR; ++k) {
-            const int p = rsub + k * RPP;
-            if (p >= Pd) break;
-            const float dx = dl * xp[k];
-            float4 u = cur[k];
-            u.x = fmaf(dA, u.x, dx * bv.x);
-            u.y = fmaf(dA, u.y, dx * bv.y);
-            u.z = fmaf(dA, u.z, dx * bv.z);
-            u.w = fmaf(dA, u.w, dx * bv.w);
-            *(reinterpret_cast<float4*>(hb + (long)p * N) + c4) = u;
-            float acc = u.x * cv.x + u.y * cv.y + u.z * cv.z + u.w * cv.w;
-#pragma unroll
-            for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
-            if (c4 == 0) {
-                acc = fmaf(Dh, xp[k], acc);
-                if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
-                y[(long)b * ldy + (long)h * Pd + p] = acc;
-            }
+        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+        if (c4 == 0) {
+            acc = fmaf(Dh, xp[k], acc);
+            if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
+            y[(long)b * ldy + (long)h * Pd + p] = acc;
         }
     }
 }
@@ -903,28 +890,22 @@ extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float*
     if (B == 0) return SSM_OK;
     hipStream_t st = (hipStream_t)stream;
     const int lpr = N / 4, rpp = 256 / lpr;
-    if (Pd > 16 * rpp)
-        return ssm::fail(SSM_ERR_UNSUPPORTED, "ssm_m2_state_update: head dim %d too large for "
-                         "d_state %d", Pd, N);
-    // up to 4 resident tiles per CU-slot pass; the kernel strides over the rest
-    const unsigned grid = (unsigned)std::min<long>((long)B * H, 1024);
-#define M2U(LPR, MAXR)                                                                           \
-    m2_update_kernel<LPR, MAXR><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus,       \
-                                                      dt_min, dt_max, A, Bm, ldb, Cm, ldc, Dsk,  \
-                                                      z, ldz, y, ldy, h, B, H, Pd, G, N)
-#define M2R(LPR)                                   \
-    if (Pd <= 4 * rpp) M2U(LPR, 4);                \
-    else if (Pd <= 8 * rpp) M2U(LPR, 8);           \
-    else M2U(LPR, 16);
+    // two rows per thread (R = 2): B*H*ceil(P / (2*rpp)) workgroups
+    constexpr int R = 2;
+    const int bph = (int)ssm::cdiv(Pd, rpp * R);
+    const unsigned grid = (unsigned)((long)B * H * bph);
+#define M2U(LPR)                                                                             \
+    m2_update_kernel<LPR, R><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus, dt_min, \
+                                                   dt_max, A, Bm, ldb, Cm, ldc, Dsk, z, ldz, y, \
+                                                   ldy, h, H, Pd, G, N, bph)
     switch (lpr) {
-        case 2: M2R(2); break;
-        case 4: M2R(4); break;
-        case 8: M2R(8); break;
-        case 16: M2R(16); break;
-        case 32: M2R(32); break;
-        default: M2R(64); break;
+        case 2: M2U(2); break;
+        case 4: M2U(4); break;
+        case 8: M2U(8); break;
+        case 16: M2U(16); break;
+        case 32: M2U(32); break;
+        default: M2U(64); break;
     }
-#undef M2R
 #undef M2U
     return ssm::check_launch("m2_state_update");
 }
