@@ -68,4 +68,40 @@ __device__ __forceinline__ float silu_fast(float z) {
     return z * __builtin_amdgcn_rcpf(1.f + __expf(-z));
 }
 
+// softplus_fast without branches (every lane evaluates both transcendentals): v_exp_f32 and
+// v_log_f32 (log2) times ln 2; same three regions and bounds as softplus_fast.
+__device__ __forceinline__ float softplus_sel(float x) {
+    const float e = ex2(fminf(x, 20.f) * kLog2e);
+    const float l = __builtin_amdgcn_logf(1.f + e) * 0.6931471805599453f;
+    return x > 20.f ? x : (x < -8.f ? e : l);
+}
+
+// ---------------------------------------------------------------- buffer access
+// Raw buffer resources (stride 0; dword 3 = 0x00020000 on gfx9): a lane whose byte offset
+// lies at or past num_records reads zeros and its stores are dropped, so a descriptor that
+// ends with a tensor's last valid row makes tail rows branch-free. Offsets are 32-bit.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+template <typename V>
+__device__ __forceinline__ V bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float bload4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ void bstore4(float v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
+}
+
+__device__ __forceinline__ void bstore16(float4 v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+}
+
 }  // namespace ssm

@@ -24,8 +24,26 @@ constexpr int kTargetWaves = 4096;
 
 __device__ __forceinline__ float delta_of(float raw, float bias, int softplus) {
     const float v = raw + bias;
-    return softplus ? ssm::softplus_fast(v) : v;
+    return softplus ? ssm::softplus_sel(v) : v;
 }
+
+// Inner loops of both passes. Per step every lane loads its u / dt (/ z) element through a
+// chunk-wide buffer descriptor (32-bit offsets; the prefetch one row past the chunk reads
+// zeros instead of faulting) and the wave-uniform B_t row through scalar loads one step
+// ahead (C_t's scalar load is issued at the top of its own step). `#pragma unroll 2` lets the compiler rename the carried registers instead of
+// copying them back every step.
+template <int N, bool EXACT>
+struct Rows {
+    const float* base;   // row 0 of the chunk
+    long ld;
+    int last;            // index of the chunk's last row
+    int Nr;
+    __device__ __forceinline__ void load(int k, float (&v)[N], const float (&msk)[N]) const {
+        const float* r = base + (long)min(k, last) * ld;
+#pragma unroll
+        for (int n = 0; n < N; ++n) v[n] = EXACT ? r[n] : r[n < Nr ? n : Nr - 1] * msk[n];
+    }
+};
 
 // N: state size the kernel is compiled for; Nr: runtime size (<= N). Entries n >= Nr get
 // A = 0 and B = C = 0 (clamped loads times a zero mask), so they stay exactly zero and add
@@ -49,26 +67,33 @@ __global__ __launch_bounds__(kWave) void scan_chunk_state(
         h[n] = 0.f;
     }
     const float bias = dt_bias ? dt_bias[d] : 0.f;
-    const int t0 = c * T, t1 = min(t0 + T, L);
+    const int t0 = c * T, steps = min(T, L - t0);
+    const long r0 = (long)b * L + t0;
+    const auto ru = ssm::rsrc(u + r0 * ldu, (unsigned)(((long)(steps - 1) * ldu + D) * 4));
+    const auto rd = ssm::rsrc(dt + r0 * lddt, (unsigned)(((long)(steps - 1) * lddt + D) * 4));
+    const unsigned su = (unsigned)ldu * 4u, sd = (unsigned)lddt * 4u;
+    unsigned ou = (unsigned)d * 4u, od = (unsigned)d * 4u;
+    const Rows<N, EXACT> Br{Bm + r0 * ldb, ldb, steps - 1, Nr};
     float sdt = 0.f;
-    // software pipeline: the next step's dt and u are in flight while this step computes
-    long r = (long)b * L + t0;
-    float dt_n = dt[r * lddt + d], u_n = u[r * ldu + d];
-    for (int t = t0; t < t1; ++t, ++r) {
-        const float dtc = dt_n, uc = u_n;
-        if (t + 1 < t1) {
-            dt_n = dt[(r + 1) * lddt + d];
-            u_n = u[(r + 1) * ldu + d];
-        }
-        const float dl = delta_of(dtc, bias, softplus);
-        const float du = dl * uc;
+    float dtv = ssm::bload4(rd, od), uv = ssm::bload4(ru, ou);
+    float bc[N];
+    Br.load(0, bc, msk);
+#pragma unroll 2
+    for (int k = 0; k < steps; ++k) {
+        ou += su;
+        od += sd;
+        const float dtn = ssm::bload4(rd, od), un = ssm::bload4(ru, ou);
+        float bn[N];
+        Br.load(k + 1, bn, msk);
+        const float dl = delta_of(dtv, bias, softplus);
+        const float du = dl * uv;
         sdt += dl;
-        const float* Br = Bm + r * ldb;
 #pragma unroll
-        for (int n = 0; n < N; ++n) {
-            const float bn = EXACT ? Br[n] : Br[n < Nr ? n : Nr - 1] * msk[n];
-            h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bn);
-        }
+        for (int n = 0; n < N; ++n) h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bc[n]);
+        dtv = dtn;
+        uv = un;
+#pragma unroll
+        for (int n = 0; n < N; ++n) bc[n] = bn[n];
     }
     float* hp = hc + (((long)b * NC + c) * Nr) * D + d;
 #pragma unroll
@@ -120,32 +145,46 @@ __global__ __launch_bounds__(kWave) void scan_chunk_output(
     }
     const float bias = dt_bias ? dt_bias[d] : 0.f;
     const float Dd = Dsk ? Dsk[d] : 0.f;
-    const int t0 = c * T, t1 = min(t0 + T, L);
-    long r = (long)b * L + t0;
-    float dt_n = dt[r * lddt + d], u_n = u[r * ldu + d], z_n = z ? z[r * ldz + d] : 0.f;
-    for (int t = t0; t < t1; ++t, ++r) {
-        const float dtc = dt_n, uu = u_n, zc = z_n;
-        if (t + 1 < t1) {
-            dt_n = dt[(r + 1) * lddt + d];
-            u_n = u[(r + 1) * ldu + d];
-            if (z) z_n = z[(r + 1) * ldz + d];
-        }
-        const float dl = delta_of(dtc, bias, softplus);
-        const float du = dl * uu;
-        const float* Br = Bm + r * ldb;
-        const float* Cr = Cm + r * ldc;
-        float acc = 0.f;
+    const int t0 = c * T, steps = min(T, L - t0);
+    const long r0 = (long)b * L + t0;
+    const auto ru = ssm::rsrc(u + r0 * ldu, (unsigned)(((long)(steps - 1) * ldu + D) * 4));
+    const auto rd = ssm::rsrc(dt + r0 * lddt, (unsigned)(((long)(steps - 1) * lddt + D) * 4));
+    // without z the descriptor is empty: its loads read zeros and the gate is skipped
+    const auto rz = ssm::rsrc(z ? z + r0 * ldz : u, z ? (unsigned)(((long)(steps - 1) * ldz + D) * 4) : 0u);
+    const auto ry = ssm::rsrc(y + r0 * ldy, (unsigned)(((long)(steps - 1) * ldy + D) * 4));
+    const unsigned su = (unsigned)ldu * 4u, sd = (unsigned)lddt * 4u,
+                   sz = z ? (unsigned)ldz * 4u : 0u, sy = (unsigned)ldy * 4u;
+    unsigned ou = (unsigned)d * 4u, od = ou, oz = ou, oy = ou;
+    const Rows<N, EXACT> Br{Bm + r0 * ldb, ldb, steps - 1, Nr};
+    const Rows<N, EXACT> Cr{Cm + r0 * ldc, ldc, steps - 1, Nr};
+    float dtv = ssm::bload4(rd, od), uv = ssm::bload4(ru, ou), zv = ssm::bload4(rz, oz);
+    float bc[N], cc[N];
+    Br.load(0, bc, msk);
+#pragma unroll 2
+    for (int k = 0; k < steps; ++k) {
+        ou += su;
+        od += sd;
+        oz += sz;
+        const float dtn = ssm::bload4(rd, od), un = ssm::bload4(ru, ou), zn = ssm::bload4(rz, oz);
+        float bn[N];
+        Br.load(k + 1, bn, msk);   // B one step ahead; C (used after the state update) in-step
+        Cr.load(k, cc, msk);
+        const float dl = delta_of(dtv, bias, softplus);
+        const float du = dl * uv;
+        float acc = Dd * uv;
 #pragma unroll
         for (int n = 0; n < N; ++n) {
-            const int nn = EXACT ? n : (n < Nr ? n : Nr - 1);
-            const float bn = EXACT ? Br[n] : Br[nn] * msk[n];
-            const float cn = EXACT ? Cr[n] : Cr[nn] * msk[n];
-            h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bn);
-            acc = fmaf(h[n], cn, acc);
+            h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bc[n]);
+            acc = fmaf(h[n], cc[n], acc);
         }
-        acc = fmaf(Dd, uu, acc);
-        if (z) acc *= ssm::silu_fast(zc);
-        y[r * ldy + d] = acc;
+        if (z) acc *= ssm::silu_fast(zv);
+        ssm::bstore4(acc, ry, oy);
+        oy += sy;
+        dtv = dtn;
+        uv = un;
+        zv = zn;
+#pragma unroll
+        for (int n = 0; n < N; ++n) bc[n] = bn[n];
     }
 }
 

@@ -152,25 +152,10 @@ struct Raw {
 // Every chunk gets descriptors whose num_records ends with its last valid time step, so the
 // rows past the sequence end need no branches and every chunk issues the same memory
 // instructions (the compiler can then count them exactly in its vmcnt waits).
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             0x00020000);
-}
-
-template <typename V>
-__device__ __forceinline__ V bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-
-__device__ __forceinline__ float bload4(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-
-__device__ __forceinline__ void bstore16(float4 v, __amdgpu_buffer_rsrc_t r, unsigned off) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
-}
+using ssm::bload16;
+using ssm::bload4;
+using ssm::bstore16;
+using ssm::rsrc;
 
 // Inclusive prefix sum over the 64 lanes with DPP (row_shr inside rows of 16, then
 // row_bcast:15 / row_bcast:31 across rows); no LDS traffic.
