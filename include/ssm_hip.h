@@ -160,6 +160,18 @@ ssm_status ssm_gated_rmsnorm(const float* x, long ldx, const float* z, long ldz,
                              const float* w, float* y, long ldy, int M, int n, int G, float eps,
                              void* stream);
 
+/* Projection of a few rows (one per decoded sequence, 1 <= M <= 64) with the block's norm
+ * fused in front of it (the per-token Linear layers of the MambaCode.js model behind
+ * model.forward / model.generate, streaming.ts:31-35, session.ts:421-425):
+ *   y[m,n] = beta*y[m,n] + s[m] * sum_k p[m,k] W[n,k],   W (N,K) row-major
+ *   mode 0: p = x,                  s = 1
+ *   mode 1: p = x*g[k],             s = rsqrt(mean_k x^2 + eps)               (RMSNorm)
+ *   mode 2: p = x*silu(z)*g[k],     s = rsqrt(mean_k (x*silu(z))^2 + eps)      (gated RMSNorm)
+ * K % 16 == 0; x, z, g, W 16-byte aligned with row strides multiple of 4. fp32 MFMA. */
+ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const float* z, long ldz,
+                           const float* g, const float* W, float* y, long ldy, int M, int N, int K,
+                           float beta, float eps, void* stream);
+
 /* ------------------------------------------------------------------ model level */
 #define SSM_LAYER_MAMBA1 1
 #define SSM_LAYER_MAMBA2 2

@@ -21,4 +21,10 @@ ssm_status launch_argmax(const float* x, long ldx, int rows, int n, uint32_t* ou
 ssm_status launch_init(float* p, long n, int kind, float a0, float a1, uint64_t seed,
                        uint64_t tensor_id, int row, hipStream_t st);
 ssm_status launch_neg_exp(const float* x, float* y, long n, hipStream_t st);
+// Few-row projection with fused RMSNorm (mode 1) / gated RMSNorm (mode 2) prologue
+// (rowgemm.hip); rowgemm_ok says whether the shape is supported.
+bool rowgemm_ok(int M, int N, int K);
+ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, long ldz,
+                          const float* g, const float* W, float* Y, long ldy, int M, int N, int K,
+                          float beta, float eps, hipStream_t st);
 }  // namespace ssm

@@ -549,9 +549,38 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
     return SSM_OK;
 }
 
-// One-token mixer step for B sequences with the recurrent state.
-ssm_status mixer_step(ssm_model* m, const LayerW& Ly, const float* x, float* out, int B,
-                      float* ssm_st, float* conv_st, const Ws& w) {
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// y (M, N) [ld ldy] = beta*y + s * p(x) W^T (mode 1: RMSNorm with weight g; mode 2: gated
+// RMSNorm with z, one group): the few-row kernel with the norm in its prologue where that is
+// faster, otherwise the norm as its own kernel into `tmp` and rocBLAS for the product.
+ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const float* z, long ldz,
+                     const float* g, const float* W, float* y, long ldy, int M, int N, int K,
+                     float beta, float* tmp) {
+    ssm_ctx* c = m->ctx;
+    const Dims& d = m->dm;
+    // The few-row kernel reads each W tile once per 16-row block; it beats norm + rocBLAS only
+    // for the gated-norm out_proj (narrow N, long K), so the other projections keep rocBLAS.
+    const bool fits = mode == 2 && ssm::rowgemm_ok(M, N, K) && al16(x) && al16(W) &&
+                      ldx % 4 == 0 && al16(g) && al16(z) && ldz % 4 == 0 && d.G == 1;
+    if (fits)
+        return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, d.eps,
+                                   c->stream);
+    if (mode == 1) {
+        SSM_TRY(ssm_rmsnorm(x, ldx, g, tmp, K, M, K, d.eps, c->stream));
+        return gemm(c, M, N, K, tmp, K, W, y, ldy, beta);
+    }
+    if (mode == 2) {
+        SSM_TRY(ssm_gated_rmsnorm(x, ldx, z, ldz, g, tmp, K, M, K, d.G, d.eps, c->stream));
+        return gemm(c, M, N, K, tmp, K, W, y, ldy, beta);
+    }
+    return gemm(c, M, N, K, x, ldx, W, y, ldy, beta);
+}
+
+// One-token layer step for B sequences with the recurrent state:
+// hid += mixer(RMSNorm(hid)). The norms ride in the projections' prologues (proj_rows).
+ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* ssm_st,
+                      float* conv_st, const Ws& w) {
     const Dims& d = m->dm;
     ssm_ctx* c = m->ctx;
     hipStream_t st = c->stream;
@@ -560,21 +589,31 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, const float* x, float* out
     if (Ly.type == SSM_LAYER_MAMBA1) {
         float *xz = w.a, *xc = w.b, *dbl = w.c, *dtv = w.d, *y = w.e;
         const int RN = d.R + 2 * d.N;
-        { Stage g(c, "m1.step.in_proj"); SSM_TRY(gemm(c, B, 2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
+        { Stage g(c, "m1.step.in_proj");
+          SSM_TRY(proj_rows(m, 1, hid, d.d, nullptr, 0, W + Ly.norm, W + Ly.in_proj, xz, 2 * d.D,
+                            B, 2 * d.D, d.d, 0.f, w.nrm)); }
         { Stage g(c, "m1.step.conv");
           SSM_TRY(ssm_conv1d_update(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, conv_st, B,
                                     d.D, d.K, 1, st)); }
-        { Stage g(c, "m1.step.x_proj"); SSM_TRY(gemm(c, B, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
-        { Stage g(c, "m1.step.dt_proj"); SSM_TRY(gemm(c, B, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
+        { Stage g(c, "m1.step.x_proj");
+          SSM_TRY(proj_rows(m, 0, xc, d.D, nullptr, 0, nullptr, W + Ly.x_proj, dbl, RN, B, RN,
+                            d.D, 0.f, nullptr)); }
+        { Stage g(c, "m1.step.dt_proj");
+          SSM_TRY(proj_rows(m, 0, dbl, RN, nullptr, 0, nullptr, W + Ly.dt_w, dtv, d.D, B, d.D,
+                            d.R, 0.f, nullptr)); }
         { Stage g(c, "m1.step.state_update");
           SSM_TRY(ssm_m1_state_update(xc, d.D, dtv, d.D, W + Ly.dt_b, 1, A, dbl + d.R, RN,
                                       dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D, y, d.D,
                                       ssm_st, B, d.D, d.N, st)); }
-        { Stage g(c, "m1.step.out_proj"); SSM_TRY(gemm(c, B, d.d, d.D, y, d.D, W + Ly.out_proj, out, d.d, 1.f)); }
+        { Stage g(c, "m1.step.out_proj");
+          SSM_TRY(proj_rows(m, 0, y, d.D, nullptr, 0, nullptr, W + Ly.out_proj, hid, d.d, B, d.d,
+                            d.D, 1.f, nullptr)); }
     } else {
         float *zx = w.a, *xbc = w.b, *y = w.c, *yn = w.d;
         const int GN = d.G * d.N;
-        { Stage g(c, "m2.step.in_proj"); SSM_TRY(gemm(c, B, d.nin, d.d, x, d.d, W + Ly.in_proj, zx, d.nin, 0.f)); }
+        { Stage g(c, "m2.step.in_proj");
+          SSM_TRY(proj_rows(m, 1, hid, d.d, nullptr, 0, W + Ly.norm, W + Ly.in_proj, zx, d.nin, B,
+                            d.nin, d.d, 0.f, w.nrm)); }
         { Stage g(c, "m2.step.conv");
           SSM_TRY(ssm_conv1d_update(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc, d.cd,
                                     conv_st, B, d.cd, d.K, 1, st)); }
@@ -583,30 +622,33 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, const float* x, float* out
                                       INFINITY, A, xbc + d.D, d.cd, xbc + d.D + GN, d.cd,
                                       W + Ly.Dsk, nullptr, 0, y, d.D, ssm_st, B, d.H, d.P, d.G,
                                       d.N, st)); }
-        { Stage g(c, "m2.step.gated_norm");
-          SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, B, d.D, d.G, d.eps,
-                                    st)); }
-        { Stage g(c, "m2.step.out_proj"); SSM_TRY(gemm(c, B, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, 1.f)); }
+        { Stage g(c, "m2.step.out_proj");
+          SSM_TRY(proj_rows(m, 2, y, d.D, zx, d.nin, W + Ly.gnorm, W + Ly.out_proj, hid, d.d, B,
+                            d.d, d.D, 1.f, yn)); }
     }
     return SSM_OK;
 }
 
-// embeddings -> layers -> final norm; result in w.nrm (T, d).
-ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s, const Ws& w) {
+// embeddings -> layers; then the final norm into w.nrm unless `final_norm` is false (the
+// one-token path, whose LM head applies it in its prologue: the result stays in w.hid).
+ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s, const Ws& w,
+                 bool final_norm = true) {
     const Dims& d = m->dm;
     hipStream_t st = m->ctx->stream;
     const long T = (long)B * L;
     SSM_TRY(ssm::launch_embed(d_ids, m->w + m->emb, w.hid, T, d.d, d.V, m->d_flag, st));
     for (int l = 0; l < d.nl; ++l) {
         const LayerW& Ly = m->layers[l];
-        SSM_TRY(ssm_rmsnorm(w.hid, d.d, m->w + Ly.norm, w.nrm, d.d, (int)T, d.d, d.eps, st));
         float* ss = s ? s->ssm[l] : nullptr;
         float* cs = s ? s->conv[l] : nullptr;
-        if (L == 1 && s)
-            SSM_TRY(mixer_step(m, Ly, w.nrm, w.hid, B, ss, cs, w));
-        else
+        if (L == 1 && s) {
+            SSM_TRY(mixer_step(m, Ly, w.hid, B, ss, cs, w));
+        } else {
+            SSM_TRY(ssm_rmsnorm(w.hid, d.d, m->w + Ly.norm, w.nrm, d.d, (int)T, d.d, d.eps, st));
             SSM_TRY(mixer(m, Ly, w.nrm, w.hid, 1.f, B, L, ss, cs, w));
+        }
     }
+    if (!final_norm) return SSM_OK;
     return ssm_rmsnorm(w.hid, d.d, m->w + m->norm_f, w.nrm, d.d, (int)T, d.d, d.eps, st);
 }
 
@@ -1046,9 +1088,11 @@ extern "C" ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const u
     const Dims& d = m->dm;
     Ws w;
     SSM_TRY(ensure_ws(m, s->B, 1, false, &w));
-    SSM_TRY(trunk(m, d_ids, s->B, 1, s, w));
+    SSM_TRY(trunk(m, d_ids, s->B, 1, s, w, false));
     float* lg = d_logits ? d_logits : s->d_logits;
-    SSM_TRY(gemm(m->ctx, s->B, d.V, d.d, w.nrm, d.d, m->w + m->emb, lg, d.V, 0.f));
+    { Stage g(m->ctx, "head");
+      SSM_TRY(proj_rows(m, 1, w.hid, d.d, nullptr, 0, m->w + m->norm_f, m->w + m->emb, lg, d.V,
+                        s->B, d.V, d.d, 0.f, w.nrm)); }
     if (d_argmax) SSM_TRY(ssm::launch_argmax(lg, d.V, s->B, d.V, d_argmax, m->ctx->stream));
     return SSM_OK;
 }

@@ -143,6 +143,18 @@ def rmsnorm(x, w, eps=1e-5, out=None):
     return y
 
 
+def linear_rows(x, W, mode=0, g=None, z=None, eps=1e-5, out=None, beta=0.0):
+    """y = beta*y + s * p(x) W^T for M <= 64 rows (ssm_linear_rows): mode 0 plain, 1 RMSNorm
+    (weight g), 2 gated RMSNorm (z, weight g)."""
+    M, K = x.shape
+    N = W.shape[0]
+    y = out if out is not None else torch.zeros(M, N, device=x.device, dtype=torch.float32)
+    _lib.call("ssm_linear_rows", mode, _p(x), x.stride(0), _p(z) if z is not None else None,
+              z.stride(0) if z is not None else 0, _p(g) if g is not None else None, _p(W),
+              _p(y), y.stride(0), M, N, K, float(beta), float(eps), _stream())
+    return y
+
+
 def gated_rmsnorm(x, z, w, groups=1, eps=1e-5, out=None):
     M, n = x.shape
     y = out if out is not None else torch.empty_like(x)

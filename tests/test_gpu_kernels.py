@@ -315,9 +315,34 @@ def test_rmsnorm_and_gated():
         assert err(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=g)), ref) <= F32_TOL
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("M,N,Kd,strided", [(1, 16, 48, False), (5, 80, 1536, True),
+                                           (33, 1000, 2048, False), (64, 4384, 1024, True)])
+def test_linear_rows(mode, M, N, Kd, strided):
+    """Few-row projection with the RMSNorm / gated RMSNorm prologue (decode in/out_proj, LM
+    head) against the oracle's norm + linear; beta = 1 adds into the existing y (residual)."""
+    case(f"linear_rows mode={mode} M={M} N={N} K={Kd} strided={strided}")
+    r = rng(16 + mode)
+    pad = 16 if strided else 0
+    xb = r.standard_normal((M, Kd + pad)).astype(np.float32)
+    zb = r.standard_normal((M, Kd + pad)).astype(np.float32)
+    x, z = xb[:, :Kd], zb[:, :Kd]
+    W = (r.standard_normal((N, Kd)) / np.sqrt(Kd)).astype(np.float32)
+    g = r.uniform(0.5, 1.5, Kd).astype(np.float32)
+    y0 = r.standard_normal((M, N)).astype(np.float32)
+    p = x if mode == 0 else O.rmsnorm(x, g) if mode == 1 else O.gated_rmsnorm(x, z, g)
+    ref = O.linear(np.ascontiguousarray(p), W)
+    xd, zd = dev(xb)[:, :Kd], dev(zb)[:, :Kd]
+    for beta in (0.0, 1.0):
+        out = dev(y0)
+        K().linear_rows(xd, dev(W), mode, g=dev(g) if mode else None,
+                        z=zd if mode == 2 else None, out=out, beta=beta)
+        assert err(host(out), ref + beta * y0) <= F32_TOL
+
+
 def test_m2_state_update_decode_shape():
-    """Config-4 shape (64 sequences x 32 heads): more tiles than the persistent grid, so
-    every workgroup walks several (b, h) tiles."""
+    """Config-4 shape (64 sequences x 32 heads): the row-split grid (8192 workgroups of two
+    rows per thread) over the full (B, H, P, N) state."""
     case("m2_state_update decode shape")
     r = rng(15)
     B, H, P, G, N = 64, 32, 64, 1, 128
