@@ -172,6 +172,11 @@ ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const float* z, l
                            const float* g, const float* W, float* y, long ldy, int M, int N, int K,
                            float beta, float eps, void* stream);
 
+/* Greedy pick per row (sampleToken with topK = 1, src/session/streaming.ts:74-75): index
+ * of the largest value, lowest index among equal maxima; NaN never wins (0 for an all-NaN
+ * row). x (rows, n) with row stride ldx; out (rows) uint32. */
+ssm_status ssm_argmax(const float* x, long ldx, int rows, int n, uint32_t* out, void* stream);
+
 /* ------------------------------------------------------------------ model level */
 #define SSM_LAYER_MAMBA1 1
 #define SSM_LAYER_MAMBA2 2

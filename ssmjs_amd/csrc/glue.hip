@@ -78,33 +78,55 @@ __global__ void gather_rows_kernel(const float* __restrict__ x, long row_stride,
 }
 
 // Greedy pick: largest logit, lowest index among equal maxima (the order a stable
-// descending sort gives, src/session/streaming.ts:74-75). NaN never wins.
-__global__ __launch_bounds__(kBlock) void argmax_kernel(const float* __restrict__ x, long ldx,
-                                                        int n, uint32_t* __restrict__ out) {
-    __shared__ float sv[kBlock];
-    __shared__ int si[kBlock];
+// descending sort gives, src/session/streaming.ts:74-75). NaN never wins. One 1024-thread
+// workgroup per row: float4 loads unrolled 8 deep keep a whole vocabulary row (32000 logits
+// = 128 KB) in flight at once; each thread scans ascending indices, then wave shuffles and
+// LDS combine (value, index) pairs.
+constexpr int kArgBlock = 1024;
+
+__device__ __forceinline__ void arg_take(float v, int i, float& best, int& bi, int n) {
+    if (v > best || (bi == n && v == best)) { best = v; bi = i; }
+}
+
+__device__ __forceinline__ void arg_merge(float ov, int oi, float& best, int& bi) {
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+}
+
+__global__ __launch_bounds__(kArgBlock) void argmax_kernel(const float* __restrict__ x, long ldx,
+                                                           int n, int vec, uint32_t* __restrict__ out) {
+    __shared__ float sv[kArgBlock / 64];
+    __shared__ int si[kArgBlock / 64];
     const float* xr = x + (long)blockIdx.x * ldx;
     float best = -INFINITY;
     int bi = n;
-    for (int i = threadIdx.x; i < n; i += kBlock) {
-        const float v = xr[i];
-        if (v > best || (bi == n && v == best)) { best = v; bi = i; }
-    }
-    sv[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int s = kBlock / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-            const float ov = sv[threadIdx.x + s];
-            const int oi = si[threadIdx.x + s];
-            if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-                sv[threadIdx.x] = ov;
-                si[threadIdx.x] = oi;
-            }
+    int tail = 0;
+    if (vec) {
+        const int n4 = n / 4;
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+#pragma unroll 8
+        for (int i = threadIdx.x; i < n4; i += kArgBlock) {
+            const float4 v = x4[i];
+            arg_take(v.x, 4 * i, best, bi, n);
+            arg_take(v.y, 4 * i + 1, best, bi, n);
+            arg_take(v.z, 4 * i + 2, best, bi, n);
+            arg_take(v.w, 4 * i + 3, best, bi, n);
         }
-        __syncthreads();
+        tail = 4 * n4;
     }
-    if (threadIdx.x == 0) out[blockIdx.x] = si[0] < n ? (uint32_t)si[0] : 0u;
+    for (int i = tail + threadIdx.x; i < n; i += kArgBlock) arg_take(xr[i], i, best, bi, n);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        arg_merge(ov, oi, best, bi);
+    }
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) { sv[w] = best; si[w] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < kArgBlock / 64; ++k) arg_merge(sv[k], si[k], best, bi);
+        out[blockIdx.x] = bi < n ? (uint32_t)bi : 0u;
+    }
 }
 
 // ---- counter-based random init: value i of tensor `tid` depends only on (seed, tid, i)
@@ -173,7 +195,8 @@ ssm_status launch_gather_rows(const float* x, long row_stride, long first, float
 ssm_status launch_argmax(const float* x, long ldx, int rows, int n, uint32_t* out,
                          hipStream_t st) {
     if (rows == 0) return SSM_OK;
-    argmax_kernel<<<rows, kBlock, 0, st>>>(x, ldx, n, out);
+    const int vec = ((uintptr_t)x % 16 == 0 && ldx % 4 == 0) ? 1 : 0;
+    argmax_kernel<<<rows, kArgBlock, 0, st>>>(x, ldx, n, vec, out);
     return check_launch("argmax");
 }
 
@@ -211,4 +234,11 @@ extern "C" ssm_status ssm_gated_rmsnorm(const float* x, long ldx, const float* z
     gated_rmsnorm_kernel<<<M, kBlock, 0, (hipStream_t)stream>>>(x, ldx, z, ldz, w, y, ldy, n, G,
                                                                  eps);
     return ssm::check_launch("gated_rmsnorm");
+}
+
+extern "C" ssm_status ssm_argmax(const float* x, long ldx, int rows, int n, uint32_t* out,
+                                 void* stream) {
+    SSM_REQUIRE(x && out, "ssm_argmax: null x/out");
+    SSM_REQUIRE(rows >= 0 && n >= 1 && ldx >= n, "ssm_argmax: bad shape");
+    return ssm::launch_argmax(x, ldx, rows, n, out, (hipStream_t)stream);
 }

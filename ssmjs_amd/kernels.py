@@ -143,6 +143,14 @@ def rmsnorm(x, w, eps=1e-5, out=None):
     return y
 
 
+def argmax(x, out=None):
+    """Row-wise greedy pick (ssm_argmax): lowest index among equal maxima, NaN never wins."""
+    rows, n = x.shape
+    o = out if out is not None else torch.empty(rows, dtype=torch.int32, device=x.device)
+    _lib.call("ssm_argmax", _p(x), x.stride(0), rows, n, _p(o), _stream())
+    return o
+
+
 def linear_rows(x, W, mode=0, g=None, z=None, eps=1e-5, out=None, beta=0.0):
     """y = beta*y + s * p(x) W^T for M <= 64 rows (ssm_linear_rows): mode 0 plain, 1 RMSNorm
     (weight g), 2 gated RMSNorm (z, weight g)."""

@@ -340,6 +340,26 @@ def test_linear_rows(mode, M, N, Kd, strided):
         assert err(host(out), ref + beta * y0) <= F32_TOL
 
 
+@pytest.mark.parametrize("n,pad", [(32000, 0), (1001, 3), (7, 0)])
+def test_argmax_ties_nan_and_tails(n, pad):
+    """Greedy pick = sampleToken with topK 1 (streaming.ts:74-75): the lowest index among
+    equal maxima; NaN never wins; an all -inf row gives its first index, an all-NaN row 0."""
+    case(f"argmax n={n} pad={pad}")
+    r = rng(40 + n)
+    rows = 6
+    xb = r.standard_normal((rows, n + pad)).astype(np.float32)
+    x = xb[:, :n]
+    x[1, [n // 3, n // 2, n - 1]] = 9.0          # tie: lowest index wins
+    x[2, :] = np.nan
+    x[2, n - 1] = -1.0                          # only non-NaN value
+    x[3, :] = -np.inf
+    x[4, :] = np.nan                            # no winner -> 0
+    x[5, 0] = np.nan
+    x[5, n // 2] = 50.0
+    got = host(K().argmax(dev(xb)[:, :n])).astype(np.int64)
+    assert got.tolist() == [int(np.argmax(x[0])), n // 3, n - 1, 0, 0, n // 2]
+
+
 def test_m2_state_update_decode_shape():
     """Config-4 shape (64 sequences x 32 heads): the row-split grid (8192 workgroups of two
     rows per thread) over the full (B, H, P, N) state."""
