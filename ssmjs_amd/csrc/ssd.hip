@@ -4,10 +4,10 @@
 // One workgroup (4 waves) owns one (batch, head, segment) and walks the segment's chunks in
 // order with the P x N state held in MFMA accumulator registers, so the chunk-state tensor is
 // never written to HBM. Per chunk of Q = 64 steps:
-//   dt/decay  wave 0 computes dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix sum
-//             of dt' * A_h over the chunk with a 64-lane shuffle scan.
-//   staging   X^T, (X * w)^T with w_j = exp(acum_end - acum_j) dt'_j, B and B^T go to LDS as
-//             bf16 (hi, plus lo when SPLIT); each wave keeps its 16 rows of C in registers.
+//   dt/decay  every wave computes dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix
+//             sum of dt' * A_h over the chunk with a 64-lane DPP scan.
+//   staging   X, X * w with w_j = exp(acum_end - acum_j) dt'_j, and B go to LDS as bf16 (hi,
+//             plus lo when SPLIT); each wave keeps its 16 rows of C in registers.
 //   Y_off     Y^T[p,i] = exp(acum_i) * sum_n S[p,n] C[i,n]              (MFMA, K = N)
 //   Y_diag    S^T[j,i] = sum_n B[j,n] C[i,n]; mask j <= i; * exp(acum_i - acum_j) dt'_j;
 //             Y^T[p,i] += sum_j X^T[p,j] S^T[j,i]                          (MFMA, K = N, Q)
@@ -36,7 +36,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int Q = 64;     // internal chunk length
 constexpr int P = 64;     // head dim handled by this kernel
-constexpr int PADB = 8;   // bf16 row padding in LDS (16 bytes) against bank conflicts
 constexpr int kTargetWG = 512;
 
 struct SsdArgs {
@@ -98,9 +97,10 @@ __device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v -
 // inside each 16-lane group, lane 4a+b receives element b of the 8-byte chunks addressed by
 // lanes a, a+4, a+8, a+12. If lane m points at row j0 + m/4, column base + 4 (m % 4), lane L
 // receives M[j0 .. j0+3][base + L]: four K-consecutive values of column base + L.
-// Row pitches (in 4-byte banks of the 64-bank LDS): X, X w and state^T 36, B 72 (N=128) /
-// 40 (N=64), so both the transposed reads (4 rows x 32 bytes) and the b128 row reads of a
-// phase land on distinct banks.
+// Row pitches: X, X w and state^T P + 8, B N + 16 (bf16 elements). The b128 row reads of B
+// are conflict-free at pitch 144; the transposed reads over rows j0 + 8 q4 (+4) meet 2-way
+// bank conflicts at every pitch (SQ_LDS_BANK_CONFLICT). A layout without them (k-slot rows
+// 4 q4 apart, pitches of 16 mod 32) ran no faster: LDS is not what bounds this kernel.
 template <bool SPLIT, int NN, bool FULL>
 struct Smem {
     static constexpr int NS = SPLIT ? 2 : 1;
@@ -130,10 +130,12 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Per-thread raw prefetch of one chunk: X row j = lane, columns 16w..16w+15 (so the lane that
-// owns time step j also owns its weight w_j); B rows t/(NN/8) + (256/(NN/8)) k, 8 elements at
-// 8 (t % (NN/8)); dt of time step lane. The C fragments of the wave's strip are prefetched
-// separately (they are still in use when the X / B prefetch is issued).
+// Per-thread raw prefetch of one chunk. X: wave w reads rows 16w .. 16w+15 as whole rows,
+// XL lanes of 16 bytes (XE elements) per row and XR rows per load, so every load covers full
+// 128-byte lines; lane t holds row 16w + XR k + t / XL, columns XE (t % XL) + 0 .. XE-1 of
+// load k. B: rows t/(NN/8) + (256/(NN/8)) k, 8 elements at 8 (t % (NN/8)). dt: time step
+// lane. The C fragments of the wave's strip are prefetched separately (they are still in use
+// when the X / B prefetch is issued).
 template <typename TIN, int NN>
 struct Raw {
     static constexpr int KS = NN / 32;
@@ -142,7 +144,11 @@ struct Raw {
     static constexpr int BPASS = Q / BR;
     using v8 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x8>::type;
     static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // 16-byte units per 8 elements
-    v8 x[2][V8N];
+    static constexpr int XE = 16 / (int)sizeof(TIN);       // X elements per 16-byte load
+    static constexpr int XL = P / XE;                      // lanes per X row
+    static constexpr int XR = 64 / XL;                     // X rows per load
+    static constexpr int XK = 16 / XR;                     // X loads per wave
+    v8 x[XK];
     v8 b[BPASS][V8N];
     float dt;
 };
@@ -174,6 +180,17 @@ __device__ __forceinline__ float wave_prefix_sum(float v) {
     v = add_dpp<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
     v = add_dpp<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
     return v;
+}
+
+// Value of the neighbouring lane (lane ^ 1, DPP quad_perm [1,0,3,2]) for every dword of v.
+template <typename V>
+__device__ __forceinline__ V swap_pair(V v) {
+    static_assert(sizeof(V) == 16, "16-byte vectors");
+    ssm::u32x4 u = __builtin_bit_cast(ssm::u32x4, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        u[i] = (unsigned)__builtin_amdgcn_update_dpp(0, (int)u[i], 0xB1, 0xf, 0xf, false);
+    return __builtin_bit_cast(V, u);
 }
 
 template <typename V>
@@ -229,10 +246,19 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
     const TIN* b0 = reinterpret_cast<const TIN*>(a.Bm) + brow * a.ldb + (long)g * a.N;
     const TIN* cm0 = reinterpret_cast<const TIN*>(a.Cm) + brow * a.ldc + (long)g * a.N;
     const float* d0 = a.dt + brow * a.lddt + h;
-    const unsigned ox = (unsigned)(lane * a.ldx + 16 * w) * SZ;
+    const int xr = lane / RW::XL, xc = RW::XE * (lane % RW::XL);   // X row in a load / column
+    const unsigned ox = (unsigned)((16 * w + xr) * a.ldx + xc) * SZ;
+    const unsigned oxk = (unsigned)(RW::XR * a.ldx) * SZ;
     const unsigned ob = (unsigned)(br * a.ldb + bc) * SZ;
     const unsigned obk = (unsigned)(RW::BR * a.ldb) * SZ;
+    // Lanes l16 = 2r and 2r + 1 share the 128-byte lines of rows 16w + 2r and 16w + 2r + 1: the
+    // C load (h, sel) and the y store (h, sel) of lane (l16, q4) cover row
+    // 16w + (l16 & ~1) + sel at byte 128 h + 64 (l16 & 1) + 16 q4 of the row, so each load or
+    // store instruction moves whole lines of 8 rows. A DPP swap between the two lanes puts every
+    // value where the MFMA layout has it.
+    const int podd = l16 & 1;
     const unsigned oc = (unsigned)(ic * a.ldc + 8 * q4) * SZ;
+    const unsigned oc2 = (unsigned)((16 * w + l16 - podd) * a.ldc + 32 * podd + 8 * q4) * SZ;
     const unsigned od = (unsigned)(lane * a.lddt) * 4u;
     // rows of chunk c that exist; 0 past the segment, so a prefetch there reads nothing
     auto rows_of = [&](int c) { return c < c_end ? min(Q, a.L - c * Q) : 0; };
@@ -250,9 +276,7 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         raw.dt = bload4(rd, od);
 #pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf)
-#pragma unroll
-            for (int u = 0; u < RW::V8N; ++u) raw.x[hlf][u] = bload16<v8>(rx, ox + (8 * hlf + 4 * u) * SZ);
+        for (int k = 0; k < RW::XK; ++k) raw.x[k] = bload16<v8>(rx, ox + k * oxk);
 #pragma unroll
         for (int k = 0; k < RW::BPASS; ++k)
 #pragma unroll
@@ -264,10 +288,20 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         if constexpr (FULL) {
             const int qv = rows_of(c);
             const auto rc = rsrc(cm0 + (long)c * Q * a.ldc, span(qv, a.ldc, NN, SZ));
+            if constexpr (sizeof(TIN) == 2) {
+                // craw[2h + sel]: row 16w + (l16 & ~1) + sel, n = 64h + 32 (l16 & 1) + 8 q4 + 0..7
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
+                for (int hh = 0; hh < KS / 2; ++hh)
 #pragma unroll
-                for (int u = 0; u < RW::V8N; ++u) craw[ks][u] = bload16<v8>(rc, oc + (32 * ks + 4 * u) * SZ);
+                    for (int sel = 0; sel < 2; ++sel)
+                        craw[2 * hh + sel][0] =
+                            bload16<v8>(rc, oc2 + (unsigned)(sel * a.ldc * SZ) + 128u * hh);
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int u = 0; u < RW::V8N; ++u) craw[ks][u] = bload16<v8>(rc, oc + (32 * ks + 4 * u) * SZ);
+            }
         }
     };
 
@@ -333,42 +367,42 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         }
         const float wl = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
 
-        // ---- stage X and X w: lane = row j, columns 16w..16w+15 (two 8-wide halves)
+        // ---- stage X and X w (rows of the X prefetch; w_j comes from lane j of this wave)
 #pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf) {
-            float xv[8];
+        for (int k = 0; k < RW::XK; ++k) {
+            constexpr int E = RW::XE;
+            const int j = 16 * w + RW::XR * k + xr;
+            const float wj = __builtin_bit_cast(
+                float, __builtin_amdgcn_ds_bpermute(4 * j, __builtin_bit_cast(int, wl)));
+            float xv[E];
             if constexpr (sizeof(TIN) == 4) {
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    xv[4 * u] = raw.x[hlf][u].x; xv[4 * u + 1] = raw.x[hlf][u].y;
-                    xv[4 * u + 2] = raw.x[hlf][u].z; xv[4 * u + 3] = raw.x[hlf][u].w;
-                }
+                xv[0] = raw.x[k].x; xv[1] = raw.x[k].y; xv[2] = raw.x[k].z; xv[3] = raw.x[k].w;
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xv[e] = (float)raw.x[hlf][0][e];
+                for (int e = 0; e < E; ++e) xv[e] = (float)raw.x[k][e];
             }
-            const int col = 16 * w + 8 * hlf;
-            bf16x8 wh, wlo;
+            using bfE = typename std::conditional<E == 8, bf16x8, bf16x4>::type;
+            bfE wh, wlo;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float u = xv[e] * wl;
+            for (int e = 0; e < E; ++e) {
+                const float u = xv[e] * wj;
                 wh[e] = hi_of(u);
                 wlo[e] = lo_of(u, wh[e]);
             }
-            *reinterpret_cast<bf16x8*>(&sm.xw[0][lane][col]) = wh;
-            if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&sm.xw[L1][lane][col]) = wlo;
+            *reinterpret_cast<bfE*>(&sm.xw[0][j][xc]) = wh;
+            if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.xw[L1][j][xc]) = wlo;
             if constexpr (FULL) {
                 if constexpr (sizeof(TIN) == 2) {
-                    *reinterpret_cast<bf16x8*>(&sm.x[0][lane][col]) = raw.x[hlf][0];
+                    *reinterpret_cast<bf16x8*>(&sm.x[0][j][xc]) = raw.x[k];
                 } else {
-                    bf16x8 hh, ll;
+                    bfE hh, ll;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
+                    for (int e = 0; e < E; ++e) {
                         hh[e] = hi_of(xv[e]);
                         ll[e] = lo_of(xv[e], hh[e]);
                     }
-                    *reinterpret_cast<bf16x8*>(&sm.x[0][lane][col]) = hh;
-                    if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&sm.x[L1][lane][col]) = ll;
+                    *reinterpret_cast<bfE*>(&sm.x[0][j][xc]) = hh;
+                    if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.x[L1][j][xc]) = ll;
                 }
             }
         }
@@ -399,7 +433,15 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if constexpr (sizeof(TIN) == 2) {
-                    cfh[ks] = craw[ks][0];
+                    // fragment ks = 2h + e of row ic: the own load (h, sel = l16 & 1) holds
+                    // e = l16 & 1, the neighbour's load (h, sel = l16 & 1) the other one
+                    if (ks % 2 == 0) {
+                        const int hh = ks / 2;
+                        const bf16x8 s0 = swap_pair(craw[2 * hh][0]);
+                        const bf16x8 s1 = swap_pair(craw[2 * hh + 1][0]);
+                        cfh[ks] = podd ? s1 : craw[2 * hh][0];
+                        cfh[ks + 1] = podd ? craw[2 * hh + 1][0] : s0;
+                    }
                 } else {
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
@@ -533,14 +575,21 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
             // ---- the next chunk's C fragments (the last use of this chunk's was Y_diag)
             load_c(c + 1);
 
-            // ---- y (lane: row ic, p = 16pb + 4q4 + 0..3); rows past the sequence end fall
-            // outside the descriptor and are dropped
+            // ---- y: Y[pb] holds row ic, p = 16pb + 4q4 + 0..3; store (h, sel) writes p-half h
+            // of row 16w + (l16 & ~1) + sel. Rows past the sequence end fall outside the
+            // descriptor and are dropped.
             {
                 const auto ry = rsrc(a.y + (row0 * a.ldy + (long)h * P), span(qv, a.ldy, P, 4));
-                const unsigned oy = (unsigned)(ic * a.ldy + 4 * q4) * 4u;
+                const unsigned oy = (unsigned)((16 * w + l16 - podd) * a.ldy + 16 * podd + 4 * q4) * 4u;
 #pragma unroll
-                for (int pb = 0; pb < P / 16; ++pb)
-                    bstore16(make_float4(Y[pb][0], Y[pb][1], Y[pb][2], Y[pb][3]), ry, oy + 64u * pb);
+                for (int hh = 0; hh < P / 32; ++hh) {
+                    const floatx4 s0 = swap_pair(Y[2 * hh]), s1 = swap_pair(Y[2 * hh + 1]);
+                    const floatx4 v0 = podd ? s1 : Y[2 * hh];        // row 16w + (l16 & ~1)
+                    const floatx4 v1 = podd ? Y[2 * hh + 1] : s0;    // row 16w + (l16 & ~1) + 1
+                    bstore16(make_float4(v0[0], v0[1], v0[2], v0[3]), ry, oy + 128u * hh);
+                    bstore16(make_float4(v1[0], v1[1], v1[2], v1[3]), ry,
+                             oy + (unsigned)(a.ldy * 4) + 128u * hh);
+                }
             }
         }
 
