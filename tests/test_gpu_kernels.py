@@ -230,12 +230,15 @@ def test_ssd_matches_oracle(B, L, H, G, N, h0, dtype):
     assert e2 <= tol
 
 
+@pytest.mark.parametrize("H,L", [(2, 64 * 40 + 17), (32, 64 * 48 + 5), (64, 64 * 24)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_ssd_long_sequence_segments(dtype):
-    """B*H small -> the sequence is cut into segments (state pass + combine + full pass)."""
-    case(f"ssd segmented {dtype}")
-    r = rng(4000)
-    B, L, H, G, N, P = 1, 64 * 40 + 17, 2, 1, 128, 64
+def test_ssd_long_sequence_segments(dtype, H, L):
+    """B*H small -> the sequence is cut into segments (state pass + combine + full pass). With
+    512 (batch, head, segment) units per launch the three shapes give 41 segments of one chunk,
+    13 segments of 4 chunks (the last segment and chunk partial) and 8 segments of 3 chunks."""
+    case(f"ssd segmented {dtype} H={H} L={L}")
+    r = rng(4000 + H)
+    B, G, N, P = 1, 1, 128, 64
     x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N, bc_scale=128 ** -0.25)
     h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32)
     tdt = torch.float32
