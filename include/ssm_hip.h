@@ -167,10 +167,16 @@ ssm_status ssm_gated_rmsnorm(const float* x, long ldx, const float* z, long ldz,
  *   mode 0: p = x,                  s = 1
  *   mode 1: p = x*g[k],             s = rsqrt(mean_k x^2 + eps)               (RMSNorm)
  *   mode 2: p = x*silu(z)*g[k],     s = rsqrt(mean_k (x*silu(z))^2 + eps)      (gated RMSNorm)
- * K % 16 == 0; x, z, g, W 16-byte aligned with row strides multiple of 4. fp32 MFMA. */
+ * K % 4 == 0; x, z, g, W 16-byte aligned with row strides multiple of 4. fp32 MFMA; W is
+ * read once. With `workspace` of ssm_linear_rows_workspace(M, N, K) bytes (0 when the shape
+ * never splits) a narrow, long-K product is split over K across workgroups and finished by a
+ * second launch that adds the slices in a fixed order; NULL runs it unsplit. Results do not
+ * depend on scheduling either way. One workspace serves one stream at a time. */
+size_t ssm_linear_rows_workspace(int M, int N, int K);
 ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const float* z, long ldz,
                            const float* g, const float* W, float* y, long ldy, int M, int N, int K,
-                           float beta, float eps, void* stream);
+                           float beta, float eps, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /* Greedy pick per row (sampleToken with topK = 1, src/session/streaming.ts:74-75): index
  * of the largest value, lowest index among equal maxima; NaN never wins (0 for an all-NaN

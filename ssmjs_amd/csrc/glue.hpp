@@ -22,9 +22,12 @@ ssm_status launch_init(float* p, long n, int kind, float a0, float a1, uint64_t 
                        uint64_t tensor_id, int row, hipStream_t st);
 ssm_status launch_neg_exp(const float* x, float* y, long n, hipStream_t st);
 // Few-row projection with fused RMSNorm (mode 1) / gated RMSNorm (mode 2) prologue
-// (rowgemm.hip); rowgemm_ok says whether the shape is supported.
+// (rowgemm.hip); rowgemm_ok says whether the shape is supported. With rowgemm_workspace
+// bytes it may split K over workgroups (plus a finishing launch); with less it runs unsplit.
 bool rowgemm_ok(int M, int N, int K);
+size_t rowgemm_workspace(int M, int N, int K);
 ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, long ldz,
                           const float* g, const float* W, float* Y, long ldy, int M, int N, int K,
-                          float beta, float eps, hipStream_t st);
+                          float beta, float eps, void* workspace, size_t workspace_bytes,
+                          hipStream_t st);
 }  // namespace ssm

@@ -309,6 +309,9 @@ struct ssm_model {
     // workspace, grown on demand
     char* ws = nullptr;
     size_t ws_bytes = 0;
+    // few-row projection split-K workspace (partial products), grown on demand
+    char* rg = nullptr;
+    size_t rg_bytes = 0;
     int* d_flag = nullptr;   // out-of-range token id flag
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
@@ -552,20 +555,32 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // y (M, N) [ld ldy] = beta*y + s * p(x) W^T (mode 1: RMSNorm with weight g; mode 2: gated
-// RMSNorm with z, one group): the few-row kernel with the norm in its prologue where that is
-// faster, otherwise the norm as its own kernel into `tmp` and rocBLAS for the product.
+// RMSNorm with z, one group): the few-row kernel (M <= 64) with the norm in its prologue
+// where it is the faster choice, otherwise the norm as its own kernel into `tmp` and rocBLAS.
+// Measured at 64 rows (cfg4): the gated out_proj (N 1024, K 2048) 13.6 us split over K vs
+// 16 us; the LM head (N 32000) 50 us vs 70 us for norm + rocBLAS; the in_proj (N 4384,
+// K 1024) 19.5 us split vs 18.6 us, so mode 1 below 16384 columns stays on rocBLAS.
 ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const float* z, long ldz,
                      const float* g, const float* W, float* y, long ldy, int M, int N, int K,
                      float beta, float* tmp) {
     ssm_ctx* c = m->ctx;
     const Dims& d = m->dm;
-    // The few-row kernel reads each W tile once per 16-row block; it beats norm + rocBLAS only
-    // for the gated-norm out_proj (narrow N, long K), so the other projections keep rocBLAS.
-    const bool fits = mode == 2 && ssm::rowgemm_ok(M, N, K) && al16(x) && al16(W) &&
-                      ldx % 4 == 0 && al16(g) && al16(z) && ldz % 4 == 0 && d.G == 1;
-    if (fits)
+    const bool wanted = mode == 2 || (mode == 1 && N >= 16384);
+    const bool fits = wanted && ssm::rowgemm_ok(M, N, K) && al16(x) && al16(W) && ldx % 4 == 0 &&
+                      al16(g) && (mode != 2 || (al16(z) && ldz % 4 == 0 && d.G == 1));
+    if (fits) {
+        const size_t need = ssm::rowgemm_workspace(M, N, K);
+        if (need > m->rg_bytes) {
+            SSM_HIP_TRY(hipStreamSynchronize(c->stream));
+            if (m->rg) SSM_HIP_TRY(hipFree(m->rg));
+            m->rg = nullptr;
+            m->rg_bytes = 0;
+            SSM_HIP_TRY(hipMalloc((void**)&m->rg, need));
+            m->rg_bytes = need;
+        }
         return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, d.eps,
-                                   c->stream);
+                                   m->rg, m->rg_bytes, c->stream);
+    }
     if (mode == 1) {
         SSM_TRY(ssm_rmsnorm(x, ldx, g, tmp, K, M, K, d.eps, c->stream));
         return gemm(c, M, N, K, tmp, K, W, y, ldy, beta);
@@ -746,6 +761,7 @@ extern "C" ssm_status ssm_model_destroy(ssm_model* m) {
         hipSetDevice(m->ctx->device);
         hipStreamSynchronize(m->ctx->stream);
         hipFree(m->w); hipFree(m->Ab); hipFree(m->ws); hipFree(m->d_flag); hipFree(m->d_ids);
+        hipFree(m->rg);
     }
     m->destroyed = true;
     return SSM_OK;

@@ -7,13 +7,25 @@
 //   mode GATED  P = X * silu(Z) * g   s = rsqrt(mean_k (X silu(Z))^2 + eps)   (gated norm -> proj)
 //
 // The row scale s[m] is independent of n, so it is applied once per output; the normalised
-// activations never go to memory. Work split: a workgroup owns 16 rows and 16*NB output
-// columns (grid = column tiles x row blocks, padded to a multiple of 8 and remapped so one
-// tile's row blocks share an XCD and its L2); its 4 waves take interleaved 16-wide chunks of K, issue 8 chunks' loads at a
-// time, and meet in LDS at the end.
-// Per chunk a lane loads one float4 of each operand row it covers (row l%16, k = k0 + 4(l/16)
-// + 0..3) and issues 4 v_mfma_f32_16x16x4_f32 per (row block, column block): MFMA j uses
-// k-slots {k0 + 4q + j}, the same permutation on both operands. fp32 MFMA throughout.
+// activations never go to memory. fp32 MFMA (v_mfma_f32_16x16x4_f32) throughout: MFMA t of a
+// 16-wide k step uses k = 4q + t for lane group q (lanes 16q .. 16q+15) on both operands.
+//
+// With M <= 64 the product streams W (N x K) once while the small X (L2-resident) is read
+// again by every column tile, so a workgroup owns ALL rows and 64 output columns: W is read
+// exactly once. K runs in blocks of 32 whose X (with the prologue applied) and W go through a
+// double-buffered LDS tile with whole-line loads issued three blocks ahead of their use (HBM
+// latency is several blocks of MFMA work); the 4 waves (2 x 2) each own a 32 x 32 quarter of
+// the tile as 2 x 2 accumulators.
+//
+// When the column tiles alone cannot fill the chip (narrow N, long K: the gated out_proj),
+// K is split into S slices over S workgroups per tile, which write their partial tiles (and
+// their slice's row sums of squares) to a workspace; a second kernel adds the slices in
+// slice order (deterministic), applies s[m] and beta, and stores Y. The kernel boundary
+// orders the two: a device-scope release/acquire per workgroup, which would let the last
+// workgroup finish the tile instead, costs far more on this chip (each XCD's L2 is written
+// back and invalidated).
+#include <algorithm>
+
 #include "common.hpp"
 #include "glue.hpp"
 
@@ -21,200 +33,336 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 64;   // most rows per launch (row blocks of 16)
+constexpr int kRows = 64;        // most rows per launch
+constexpr int kTileN = 64;       // output columns per workgroup
+constexpr int kKB = 32;          // K per block
+constexpr int kPitch = kKB + 4;  // LDS row pitch (floats)
+constexpr int kMaxSplit = 16;
+constexpr int kTargetWG = 256;   // (tile, slice) workgroups worth splitting K for
 
 enum { MODE_PLAIN = 0, MODE_RMS = 1, MODE_GATED = 2 };
+
+struct RgArgs {
+    const float* X; long ldx;
+    const float* Z; long ldz;
+    const float* g;
+    const float* W;
+    float* Y; long ldy;
+    int M, N, K;
+    float beta, eps;
+    int S, kslice, ntiles;     // splits of K, K per split (multiple of 4 blocks), column tiles
+    float* part;               // (S, M, N) partial products (S > 1)
+    float* ssqp;               // (S, M) partial row sums of squares (S > 1, norm modes)
+};
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <int MODE, int NB>
-__global__ __launch_bounds__(256) void rowgemm_kernel(
-    const float* __restrict__ X, long ldx, const float* __restrict__ Z, long ldz,
-    const float* __restrict__ g, const float* __restrict__ W, float* __restrict__ Y, long ldy,
-    int M, int N, int K, float beta, float eps, int rbs, int ntiles_rbs) {
-    constexpr int WAVES = 4, U = 4, NT = 16 * NB;
-    __shared__ floatx4 part[WAVES][NB][64];
-    __shared__ float ssq[WAVES][16];
+// P = X (* silu(Z)); the caller multiplies by g after taking the sum of squares
+template <int MODE>
+__device__ __forceinline__ float4 prologue(float4 x, float4 z) {
+    if (MODE == MODE_GATED) {
+        x.x *= ssm::silu_fast(z.x);
+        x.y *= ssm::silu_fast(z.y);
+        x.z *= ssm::silu_fast(z.z);
+        x.w *= ssm::silu_fast(z.w);
+    }
+    return x;
+}
+
+__device__ __forceinline__ float sumsq(float4 p, float s) {
+    s = fmaf(p.x, p.x, s);
+    s = fmaf(p.y, p.y, s);
+    s = fmaf(p.z, p.z, s);
+    return fmaf(p.w, p.w, s);
+}
+
+__device__ __forceinline__ float4 mul4(float4 a, float4 b) {
+    return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void rowgemm_kernel(RgArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[2][kRows][kPitch];
+    __shared__ __attribute__((aligned(16))) float wsm[2][kTileN][kPitch];
+    __shared__ float ssq[kRows];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, q = lane >> 4;
-    // the grid is padded to a multiple of 8 so that consecutive logical workgroups (a column
-    // tile's row blocks) land on one XCD and read the tile's W rows through one L2
-    const int wg = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
-    if (wg >= ntiles_rbs) return;
-    const int rb = wg % rbs, n0 = (wg / rbs) * NT, m0 = 16 * rb;
+    const int wm = w >> 1, wn = w & 1;            // this wave's 32 x 32 quarter
+    // split-major order, remapped so that consecutive workgroups (one slice's column tiles,
+    // which read the same slice of X) share an XCD and its L2
+    const int per = gridDim.x / 8;
+    const int wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (wg >= a.ntiles * a.S) return;
+    const int s = wg / a.ntiles, tile = wg % a.ntiles;
+    const int n0 = tile * kTileN;
+    const int k0 = s * a.kslice;
+    const int M = a.M, K = a.K;
+    const int klen = min(a.kslice, K - k0);
+    // blocks in groups of four (the tail of the last group reads zeros)
+    const int nblk = (klen + 4 * kKB - 1) / (4 * kKB) * 4;
 
-    // rows past M and columns past N read zeros through the descriptors' ranges
-    const auto rx = ssm::rsrc(X + (long)m0 * ldx, (unsigned)(((long)(min(M - m0, 16) - 1) * ldx + K) * 4));
-    const auto rz = ssm::rsrc(MODE == MODE_GATED ? Z + (long)m0 * ldz : X,
-                              MODE == MODE_GATED ? (unsigned)(((long)(min(M - m0, 16) - 1) * ldz + K) * 4) : 0u);
-    const auto rw = ssm::rsrc(W + (long)n0 * K, (unsigned)(((long)(min(N - n0, NT) - 1) * K + K) * 4));
-    const auto rg = ssm::rsrc(g ? g : X, g ? (unsigned)K * 4u : 0u);
-    const unsigned ox = (unsigned)(l16 * ldx) * 4u, oz = (unsigned)(l16 * ldz) * 4u;
-
-    floatx4 acc[NB];
+    // Global -> register staging: thread t covers rows (t / 8) + 32 h, k = 4 (t % 8) + 0..3 of a
+    // block (8 threads read one row's 128 bytes). Rows past M / N and k past the slice read
+    // zeros through the descriptors' ranges, so every block issues the same loads.
+    const int sr = tid >> 3, sk = 4 * (tid & 7);
+    const auto rx = ssm::rsrc(a.X + k0, (unsigned)(((long)(M - 1) * a.ldx + klen) * 4));
+    const auto rz = ssm::rsrc(MODE == MODE_GATED ? a.Z + k0 : a.X,
+                              MODE == MODE_GATED ? (unsigned)(((long)(M - 1) * a.ldz + klen) * 4) : 0u);
+    const auto rw = ssm::rsrc(a.W + (long)n0 * K + k0,
+                              (unsigned)(((long)(min(a.N - n0, kTileN) - 1) * K + klen) * 4));
+    const auto rg = ssm::rsrc(a.g ? a.g + k0 : a.X, a.g ? (unsigned)klen * 4u : 0u);
+    struct Regs { float4 x[2], z[2], w[2], g; };
+    auto gload = [&](Regs& r, int b) {
+        // k past the slice reads zeros: the offset lies beyond every range (the slice length
+        // is a multiple of 4, so a float4 is all in or out)
+        const int k = kKB * b + sk;
+        const unsigned kb = k < klen ? (unsigned)k * 4u : 0x80000000u;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float ss = 0.f;
-
-    // wave w takes the 16-wide k chunks w, w + 4, ...; rounds of U chunks are double-buffered
-    // (round r + 1's loads are in flight while round r computes). Every load is issued: a
-    // chunk past K gets an out-of-range offset and reads zeros, so the compiler's vmcnt waits
-    // count exactly.
-    const int nchunks = K / 16;
-    const int rounds = ((nchunks + WAVES - 1) / WAVES + U - 1) / U;
-    struct Buf { float4 w[U][NB], x[U], z[U], g[U]; };
-    auto load = [&](Buf& bf, int r) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = w + WAVES * (U * r + u);
-            const unsigned kb = c < nchunks ? (unsigned)(16 * c + 4 * q) * 4u : 0x80000000u;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                bf.w[u][nb] = ssm::bload16<float4>(rw, (unsigned)((16 * nb + l16) * K) * 4u + kb);
-            bf.x[u] = ssm::bload16<float4>(rx, ox + kb);
-            if (MODE == MODE_GATED) bf.z[u] = ssm::bload16<float4>(rz, oz + kb);
-            if (MODE != MODE_PLAIN) bf.g[u] = ssm::bload16<float4>(rg, kb);
+        for (int h = 0; h < 2; ++h) {
+            const int row = sr + 32 * h;
+            r.x[h] = ssm::bload16<float4>(rx, (unsigned)(row * a.ldx) * 4u + kb);
+            if (MODE == MODE_GATED) r.z[h] = ssm::bload16<float4>(rz, (unsigned)(row * a.ldz) * 4u + kb);
+            r.w[h] = ssm::bload16<float4>(rw, (unsigned)(row * K) * 4u + kb);
         }
+        if (MODE != MODE_PLAIN) r.g = ssm::bload16<float4>(rg, kb);
     };
-    auto compute = [&](const Buf& bf) {
+    float ss[2] = {0.f, 0.f};
+    auto lstore = [&](const Regs& r, int buf) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float4 p = bf.x[u];
-            if (MODE == MODE_GATED) {
-                p.x *= ssm::silu_fast(bf.z[u].x);
-                p.y *= ssm::silu_fast(bf.z[u].y);
-                p.z *= ssm::silu_fast(bf.z[u].z);
-                p.w *= ssm::silu_fast(bf.z[u].w);
-            }
+        for (int h = 0; h < 2; ++h) {
+            float4 p = prologue<MODE>(r.x[h], r.z[h]);
             if (MODE != MODE_PLAIN) {
-                ss = fmaf(p.x, p.x, ss);
-                ss = fmaf(p.y, p.y, ss);
-                ss = fmaf(p.z, p.z, ss);
-                ss = fmaf(p.w, p.w, ss);
-                p.x *= bf.g[u].x;
-                p.y *= bf.g[u].y;
-                p.z *= bf.g[u].z;
-                p.w *= bf.g[u].w;
+                ss[h] = sumsq(p, ss[h]);
+                p = mul4(p, r.g);
             }
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                acc[nb] = mfma4(p.x, bf.w[u][nb].x, acc[nb]);
-                acc[nb] = mfma4(p.y, bf.w[u][nb].y, acc[nb]);
-                acc[nb] = mfma4(p.z, bf.w[u][nb].z, acc[nb]);
-                acc[nb] = mfma4(p.w, bf.w[u][nb].w, acc[nb]);
-            }
+            *reinterpret_cast<float4*>(&xs[buf][sr + 32 * h][sk]) = p;
+            *reinterpret_cast<float4*>(&wsm[buf][sr + 32 * h][sk]) = r.w[h];
         }
     };
-    // (a round past the last one loads and multiplies zeros: no branch breaks the counting)
-    Buf ba, bb;
-    load(ba, 0);
-    for (int r = 0; r < rounds; r += 2) {
-        load(bb, r + 1);
-        compute(ba);
-        load(ba, r + 2);
-        compute(bb);
+
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            float4 av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                av[i] = *reinterpret_cast<const float4*>(&xs[buf][32 * wm + 16 * i + l16][16 * hh + 4 * q]);
+                bv[i] = *reinterpret_cast<const float4*>(&wsm[buf][32 * wn + 16 * i + l16][16 * hh + 4 * q]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = mfma4(av[i].x, bv[j].x, acc[i][j]);
+                    acc[i][j] = mfma4(av[i].y, bv[j].y, acc[i][j]);
+                    acc[i][j] = mfma4(av[i].z, bv[j].z, acc[i][j]);
+                    acc[i][j] = mfma4(av[i].w, bv[j].w, acc[i][j]);
+                }
+        }
+    };
+
+    // pipeline: block j computes from LDS buffer j % 2 while block j + 1 is stored into the
+    // other buffer from register set (j + 1) % 4, which then takes the loads of block j + 5:
+    // every block's loads are issued three blocks before they are needed. The loop body is one
+    // group of four blocks with no exit inside, so the register sets stay distinct;
+    // sched_barrier keeps the next block's prologue arithmetic from being hoisted above the
+    // LDS barrier (which would make the wave wait for newer loads).
+    Regs r0, r1, r2, r3;
+    gload(r0, 0);
+    gload(r1, 1);
+    gload(r2, 2);
+    gload(r3, 3);
+    lstore(r0, 0);
+    gload(r0, 4);
+    __syncthreads();
+    auto phase = [&](int buf, Regs& nxt, int nb) {
+        compute(buf);
+        lstore(nxt, buf ^ 1);
+        gload(nxt, nb);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int b = 0; b < nblk; b += 4) {
+        phase(0, r1, b + 5);   // computes block b, stores b + 1
+        phase(1, r2, b + 6);
+        phase(0, r3, b + 7);
+        phase(1, r0, b + 8);
     }
 
-    // ---- cross-wave reduction: partial tiles and row sums of squares through LDS
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) part[w][nb][lane] = acc[nb];
+    // row sums of squares: the 8 threads of a row hold its k-slices
     if (MODE != MODE_PLAIN) {
-        // lanes l, l^16, l^32, l^48 hold the same row's four k-slots
-        float v = ss;
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (q == 0) ssq[w][l16] = v;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float v = ss[h];
+            v += __shfl_xor(v, 1, 64);
+            v += __shfl_xor(v, 2, 64);
+            v += __shfl_xor(v, 4, 64);
+            if ((tid & 7) == 0) ssq[sr + 32 * h] = v;
+        }
     }
     __syncthreads();
-    // epilogue: wave nb finishes column block nb; lane holds rows m0 + 4q + r, column l16
-    for (int nb = w; nb < NB; nb += WAVES) {
-        floatx4 s = part[0][nb][lane];
+
+    // lane holds rows 32wm + 16i + 4q + r, column 32wn + 16j + l16 of acc[i][j]
+    if (a.S == 1) {
 #pragma unroll
-        for (int v = 1; v < WAVES; ++v) s += part[v][nb][lane];
-        const int n = n0 + 16 * nb + l16;
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float scale = 1.f;
-            if (MODE != MODE_PLAIN) {
-                const float tot = ssq[0][4 * q + r] + ssq[1][4 * q + r] + ssq[2][4 * q + r] +
-                                  ssq[3][4 * q + r];
-                scale = rsqrtf(tot / (float)K + eps);
-            }
-            o[r] = s[r] * scale;
-        }
-        const bool col_ok = n < N;
-        if (beta != 0.f) {
-            float old[4];
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + 4 * q + r;
-                old[r] = (m < M && col_ok) ? Y[(long)m * ldy + n] : 0.f;
-            }
+                const int m = 32 * wm + 16 * i + 4 * q + r;
+                if (m >= M) continue;
+                const float sc = MODE != MODE_PLAIN ? rsqrtf(ssq[m] / (float)K + a.eps) : 1.f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] = fmaf(beta, old[r], o[r]);
-        }
+                for (int j = 0; j < 2; ++j) {
+                    const int n = n0 + 32 * wn + 16 * j + l16;
+                    if (n >= a.N) continue;
+                    float* yp = a.Y + (long)m * a.ldy + n;
+                    float o = acc[i][j][r] * sc;
+                    if (a.beta != 0.f) o = fmaf(a.beta, *yp, o);
+                    *yp = o;
+                }
+            }
+        return;
+    }
+    // split K: this slice's partial tile, and (from the first column tile) its row sums of
+    // squares, for the finishing kernel
+    float* pp = a.part + (long)s * M * a.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 4 * q + r;
-            if (m < M && col_ok) Y[(long)m * ldy + n] = o[r];
+            const int m = 32 * wm + 16 * i + 4 * q + r;
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + 32 * wn + 16 * j + l16;
+                if (n < a.N) pp[(long)m * a.N + n] = acc[i][j][r];
+            }
         }
-    }
+    if (MODE != MODE_PLAIN && tile == 0 && tid < M) a.ssqp[(long)s * M + tid] = ssq[tid];
 }
 
-template <int MODE, int NB>
-void launch(const float* X, long ldx, const float* Z, long ldz, const float* g, const float* W,
-            float* Y, long ldy, int M, int N, int K, float beta, float eps, hipStream_t st) {
-    const int rbs = (int)ssm::cdiv(M, 16);
-    const int work = (int)(ssm::cdiv(N, 16 * NB) * rbs);
-    const unsigned grid = (unsigned)(8 * ssm::cdiv(work, 8));
-    rowgemm_kernel<MODE, NB><<<grid, 256, 0, st>>>(X, ldx, Z, ldz, g, W, Y, ldy, M, N, K, beta,
-                                                    eps, rbs, work);
-}
-
+// Split-K finish: Y = beta * Y + s[m] * (sum of the slices in slice order), one thread per
+// output; every slice's load is issued before the sum consumes them.
 template <int MODE>
-void pick(const float* X, long ldx, const float* Z, long ldz, const float* g, const float* W,
-          float* Y, long ldy, int M, int N, int K, float beta, float eps, hipStream_t st) {
-    // 32 columns per workgroup when that still gives about 512+ workgroups
-    if ((long)ssm::cdiv(N, 32) * ssm::cdiv(M, 16) >= 512)
-        launch<MODE, 2>(X, ldx, Z, ldz, g, W, Y, ldy, M, N, K, beta, eps, st);
-    else
-        launch<MODE, 1>(X, ldx, Z, ldz, g, W, Y, ldy, M, N, K, beta, eps, st);
+__global__ __launch_bounds__(256) void rowgemm_reduce(RgArgs a) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    const long MN = (long)a.M * a.N;
+    if (i >= MN) return;
+    const int m = (int)(i / a.N), n = (int)(i % a.N);
+    float pv[kMaxSplit], tv[kMaxSplit];
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s) {
+        pv[s] = s < a.S ? a.part[s * MN + i] : 0.f;
+        tv[s] = (MODE != MODE_PLAIN && s < a.S) ? a.ssqp[(long)s * a.M + m] : 0.f;
+    }
+    float v = 0.f, t = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s) {
+        v += pv[s];
+        t += tv[s];
+    }
+    if (MODE != MODE_PLAIN) v *= rsqrtf(t / (float)a.K + a.eps);
+    float* yp = a.Y + (long)m * a.ldy + n;
+    if (a.beta != 0.f) v = fmaf(a.beta, *yp, v);
+    *yp = v;
+}
+
+// Splits of K for a shape: enough (column tile, slice) workgroups to fill the chip, each
+// slice a whole number of groups of four K blocks.
+struct Split {
+    int S, kslice, ntiles;
+};
+
+Split choose(int N, int K, bool can_split) {
+    Split p{};
+    p.ntiles = (int)ssm::cdiv(N, kTileN);
+    const int blocks = (int)ssm::cdiv(K, kKB);
+    int S = 1;
+    if (can_split && p.ntiles < kTargetWG) {
+        S = (int)ssm::cdiv(kTargetWG, p.ntiles);
+        S = std::min(S, kMaxSplit);
+        S = std::min(S, std::max(1, blocks / 4));
+    }
+    p.kslice = 4 * kKB * (int)ssm::cdiv(blocks, 4 * S);
+    p.S = (int)ssm::cdiv(K, p.kslice);
+    return p;
+}
+
+size_t split_bytes(const Split& p, int M, int N) {
+    if (p.S <= 1) return 0;
+    return sizeof(float) * (size_t)p.S * M * ((size_t)N + 1);
 }
 
 }  // namespace
 
 namespace ssm {
 
-bool rowgemm_ok(int M, int N, int K) { return M >= 1 && M <= kRows && N >= 1 && K >= 16 && K % 16 == 0; }
+bool rowgemm_ok(int M, int N, int K) { return M >= 1 && M <= kRows && N >= 1 && K >= 4 && K % 4 == 0; }
+
+size_t rowgemm_workspace(int M, int N, int K) {
+    if (!rowgemm_ok(M, N, K)) return 0;
+    return split_bytes(choose(N, K, true), M, N);
+}
 
 ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, long ldz,
                           const float* g, const float* W, float* Y, long ldy, int M, int N, int K,
-                          float beta, float eps, hipStream_t st) {
+                          float beta, float eps, void* workspace, size_t workspace_bytes,
+                          hipStream_t st) {
     if (!rowgemm_ok(M, N, K))
-        return fail(SSM_ERR_UNSUPPORTED, "row GEMM: need 1 <= M <= %d and K %% 16 == 0 (M=%d K=%d)",
+        return fail(SSM_ERR_UNSUPPORTED, "row GEMM: need 1 <= M <= %d and K %% 4 == 0 (M=%d K=%d)",
                     kRows, M, K);
-    // the kernel addresses X, Z and one workgroup's W rows with 32-bit byte offsets
-    if ((long)M * ldx * 4 >= (1L << 31) || (long)M * ldz * 4 >= (1L << 31) ||
-        (long)32 * K * 4 >= (1L << 31))
+    // the kernel addresses X, Z and one tile's W rows with 32-bit byte offsets
+    if ((long)kRows * ldx * 4 >= (1L << 31) || (long)kRows * ldz * 4 >= (1L << 31) ||
+        (long)kTileN * K * 4 >= (1L << 31))
         return fail(SSM_ERR_UNSUPPORTED, "row GEMM: operands too large for 32-bit offsets");
+    Split p = choose(N, K, true);
+    if (p.S > 1 && (!workspace || workspace_bytes < split_bytes(p, M, N))) p = choose(N, K, false);
+    RgArgs a{};
+    a.X = X; a.ldx = ldx; a.Z = Z; a.ldz = ldz; a.g = g; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.N = N; a.K = K; a.beta = beta; a.eps = eps;
+    a.S = p.S; a.kslice = p.kslice; a.ntiles = p.ntiles;
+    if (p.S > 1) {
+        a.part = (float*)workspace;
+        a.ssqp = a.part + (size_t)p.S * M * N;
+    }
+    const unsigned grid = (unsigned)(8 * cdiv((long)p.ntiles * p.S, 8));
+    const unsigned rgrid = (unsigned)cdiv((long)M * N, 256);
     switch (mode) {
-        case 0: pick<MODE_PLAIN>(X, ldx, Z, ldz, g, W, Y, ldy, M, N, K, beta, eps, st); break;
-        case 1: pick<MODE_RMS>(X, ldx, Z, ldz, g, W, Y, ldy, M, N, K, beta, eps, st); break;
-        default: pick<MODE_GATED>(X, ldx, Z, ldz, g, W, Y, ldy, M, N, K, beta, eps, st); break;
+        case 0:
+            rowgemm_kernel<MODE_PLAIN><<<grid, 256, 0, st>>>(a);
+            if (p.S > 1) rowgemm_reduce<MODE_PLAIN><<<rgrid, 256, 0, st>>>(a);
+            break;
+        case 1:
+            rowgemm_kernel<MODE_RMS><<<grid, 256, 0, st>>>(a);
+            if (p.S > 1) rowgemm_reduce<MODE_RMS><<<rgrid, 256, 0, st>>>(a);
+            break;
+        default:
+            rowgemm_kernel<MODE_GATED><<<grid, 256, 0, st>>>(a);
+            if (p.S > 1) rowgemm_reduce<MODE_GATED><<<rgrid, 256, 0, st>>>(a);
+            break;
     }
     return check_launch("rowgemm");
 }
 
 }  // namespace ssm
 
+extern "C" size_t ssm_linear_rows_workspace(int M, int N, int K) {
+    return ssm::rowgemm_workspace(M, N, K);
+}
+
 extern "C" ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const float* z, long ldz,
                                       const float* g, const float* W, float* y, long ldy, int M,
-                                      int N, int K, float beta, float eps, void* stream) {
+                                      int N, int K, float beta, float eps, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
     SSM_REQUIRE(x && W && y, "ssm_linear_rows: null x/W/y");
     SSM_REQUIRE(mode >= 0 && mode <= 2, "ssm_linear_rows: mode must be 0, 1 or 2");
     SSM_REQUIRE(mode == 0 || g, "ssm_linear_rows: norm modes need the weight g");
@@ -225,6 +373,6 @@ extern "C" ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const 
                     (!g || (uintptr_t)g % 16 == 0),
                 "ssm_linear_rows: x, z, g, W must be 16-byte aligned with ld % 4 == 0");
     if (M == 0 || N == 0) return SSM_OK;
-    return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, eps,
-                               (hipStream_t)stream);
+    return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, eps, workspace,
+                               workspace_bytes, (hipStream_t)stream);
 }

@@ -151,15 +151,24 @@ def argmax(x, out=None):
     return o
 
 
-def linear_rows(x, W, mode=0, g=None, z=None, eps=1e-5, out=None, beta=0.0):
+def linear_rows_workspace(M, N, K, device):
+    """Split-K workspace for linear_rows (None when the shape never splits)."""
+    n = _lib.lib().ssm_linear_rows_workspace(M, N, K)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def linear_rows(x, W, mode=0, g=None, z=None, eps=1e-5, out=None, beta=0.0, workspace=None):
     """y = beta*y + s * p(x) W^T for M <= 64 rows (ssm_linear_rows): mode 0 plain, 1 RMSNorm
-    (weight g), 2 gated RMSNorm (z, weight g)."""
+    (weight g), 2 gated RMSNorm (z, weight g). `workspace` (linear_rows_workspace) lets the
+    kernel split K; without it the kernel runs unsplit."""
     M, K = x.shape
     N = W.shape[0]
     y = out if out is not None else torch.zeros(M, N, device=x.device, dtype=torch.float32)
+    ws = _p(workspace) if workspace is not None else None
+    nws = workspace.numel() if workspace is not None else 0
     _lib.call("ssm_linear_rows", mode, _p(x), x.stride(0), _p(z) if z is not None else None,
               z.stride(0) if z is not None else 0, _p(g) if g is not None else None, _p(W),
-              _p(y), y.stride(0), M, N, K, float(beta), float(eps), _stream())
+              _p(y), y.stride(0), M, N, K, float(beta), float(eps), ws, nws, _stream())
     return y
 
 

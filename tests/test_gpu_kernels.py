@@ -320,10 +320,16 @@ def test_rmsnorm_and_gated():
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("M,N,Kd,strided", [(1, 16, 48, False), (5, 80, 1536, True),
-                                           (33, 1000, 2048, False), (64, 4384, 1024, True)])
+                                           (33, 1000, 2048, False), (64, 4384, 1024, True),
+                                           (64, 1024, 2048, False), (64, 32000, 1024, False),
+                                           (3, 9000, 36, True), (64, 20000, 300, False)])
 def test_linear_rows(mode, M, N, Kd, strided):
     """Few-row projection with the RMSNorm / gated RMSNorm prologue (decode in/out_proj, LM
-    head) against the oracle's norm + linear; beta = 1 adds into the existing y (residual)."""
+    head) against the oracle's norm + linear; beta = 1 adds into the existing y (residual).
+    Each case runs unsplit (no workspace) and, where the shape splits, split over K twice on
+    one workspace (the second call finds the first one's partial sums there): the split
+    calls give the same bits (slices are added in a fixed order). K = 36 and 300 end in a
+    partial 32-wide block."""
     case(f"linear_rows mode={mode} M={M} N={N} K={Kd} strided={strided}")
     r = rng(16 + mode)
     pad = 16 if strided else 0
@@ -336,11 +342,17 @@ def test_linear_rows(mode, M, N, Kd, strided):
     p = x if mode == 0 else O.rmsnorm(x, g) if mode == 1 else O.gated_rmsnorm(x, z, g)
     ref = O.linear(np.ascontiguousarray(p), W)
     xd, zd = dev(xb)[:, :Kd], dev(zb)[:, :Kd]
+    Wd, gd = dev(W), dev(g) if mode else None
+    ws = K().linear_rows_workspace(M, N, Kd, "cuda")
     for beta in (0.0, 1.0):
-        out = dev(y0)
-        K().linear_rows(xd, dev(W), mode, g=dev(g) if mode else None,
-                        z=zd if mode == 2 else None, out=out, beta=beta)
-        assert err(host(out), ref + beta * y0) <= F32_TOL
+        outs = []
+        for wsp in (None, ws, ws):
+            out = dev(y0)
+            K().linear_rows(xd, Wd, mode, g=gd, z=zd if mode == 2 else None, out=out, beta=beta,
+                            workspace=wsp)
+            outs.append(host(out))
+            assert err(outs[-1], ref + beta * y0) <= F32_TOL
+        assert np.array_equal(outs[1], outs[2])
 
 
 @pytest.mark.parametrize("n,pad", [(32000, 0), (1001, 3), (7, 0)])
