@@ -37,14 +37,15 @@ METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 # Measured HBM bytes per launch of each workload's dominant stage: rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE (one counter per run) of `bench.py --workload <w>`, FETCH_SIZE scaled by 2.0
 # and WRITE_SIZE by 1.0 (what `bench.py --workload copy`, 1 GiB read + 1 GiB written, reads on
-# the same counters). Table and commands: profiles/hbm_traffic.md. Re-measured when the
+# the same counters). The commands and per-kernel counts sit with the rocprof summaries in
+# profiles/. Re-measured when the
 # kernels change; None where not measured.
 TRAFFIC = {
-    ("cfg2", "m1.in_proj"): 387_553_280,               # rocBLAS sgemm (tile re-reads)
-    ("cfg3", "bf16"): 868_595_712,                     # ssd_kernel
-    ("cfg3", "f32"): 1_167_515_648,                    # ssd_kernel (fp32 inputs)
-    ("cfg4", "m2.step.state_update"): 136_052_736,     # m2_update_kernel
-    ("cfg5", "bf16"): 1_215_353_856,                   # state pass + combine + full pass
+    ("cfg2", "m1.in_proj"): 387_225_600,               # rocBLAS sgemm (tile re-reads)
+    ("cfg3", "bf16"): 869_853_184,                     # ssd_kernel
+    ("cfg3", "f32"): 1_169_659_904,                    # ssd_kernel (fp32 inputs)
+    ("cfg4", "m2.step.state_update"): 136_509_440,     # m2_update_kernel
+    ("cfg5", "bf16"): 1_214_856_192,                   # state pass + combine + full pass
 }
 
 
