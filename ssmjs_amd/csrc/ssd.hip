@@ -112,8 +112,8 @@ struct Smem {
     alignas(16) __bf16 b[NS][Q][BP];                   // B         (j, n)
     alignas(16) __bf16 x[FULL ? NS : 1][FULL ? Q : 1][XP];   // X   (j, p)
     alignas(16) __bf16 s[FULL ? NS : 1][FULL ? NN : 1][XP];  // state^T (n, p)
-    alignas(16) float dt[Q];
-    alignas(16) float ac[Q];
+    alignas(16) float g[Q];    // acum_j log2(e) - log2(dt'_j): the decay weight exponent
+    alignas(16) float ac[Q];   // acum_j log2(e)
 };
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -362,8 +362,10 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
         decay_sum += acend;
         if (w == 0) {
-            sm.dt[lane] = dv;
-            sm.ac[lane] = sc;
+            // exp(acum_i - acum_j) dt'_j = exp2(ac_i - g_j); dt'_j = 0 gives g_j = +inf, weight 0
+            const float sl = sc * ssm::kLog2e;
+            sm.g[lane] = sl - __builtin_amdgcn_logf(dv);
+            sm.ac[lane] = sl;
         }
         const float wl = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
 
@@ -486,7 +488,7 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                         }
                     }
                 }
-                const float e = ssm::ex2(aci * ssm::kLog2e);
+                const float e = ssm::ex2(aci);
 #pragma unroll
                 for (int pb = 0; pb < P / 16; ++pb) Y[pb] *= e;
             }
@@ -525,13 +527,11 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                         for (int r = 0; r < 4; ++r) sv[jb][r] = 0.f;
                         continue;
                     }
-                    const float4 acj = *reinterpret_cast<const float4*>(&sm.ac[16 * jb + 4 * q4]);
-                    const float4 dtj = *reinterpret_cast<const float4*>(&sm.dt[16 * jb + 4 * q4]);
-                    const float ajr[4] = {acj.x, acj.y, acj.z, acj.w};
-                    const float djr[4] = {dtj.x, dtj.y, dtj.z, dtj.w};
+                    const float4 gj = *reinterpret_cast<const float4*>(&sm.g[16 * jb + 4 * q4]);
+                    const float gjr[4] = {gj.x, gj.y, gj.z, gj.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float f = st[jb][r] * ssm::ex2((aci - ajr[r]) * ssm::kLog2e) * djr[r];
+                        const float f = st[jb][r] * ssm::ex2(aci - gjr[r]);
                         if (jb < W) {
                             sv[jb][r] = f;
                         } else {
