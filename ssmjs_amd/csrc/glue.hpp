@@ -24,10 +24,13 @@ ssm_status launch_neg_exp(const float* x, float* y, long n, hipStream_t st);
 // Few-row projection with fused RMSNorm (mode 1) / gated RMSNorm (mode 2) prologue
 // (rowgemm.hip); rowgemm_ok says whether the shape is supported. With rowgemm_workspace
 // bytes it may split K over workgroups (plus a finishing launch); with less it runs unsplit.
+// With g2 and nout, a split finish also writes nout = RMSNorm(Y) * g2 (row stride ldn) and
+// sets *normed; otherwise *normed is false and the caller normalises Y itself.
 bool rowgemm_ok(int M, int N, int K);
 size_t rowgemm_workspace(int M, int N, int K);
 ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, long ldz,
                           const float* g, const float* W, float* Y, long ldy, int M, int N, int K,
                           float beta, float eps, void* workspace, size_t workspace_bytes,
-                          hipStream_t st);
+                          hipStream_t st, const float* g2 = nullptr, float* nout = nullptr,
+                          long ldn = 0, bool* normed = nullptr);
 }  // namespace ssm

@@ -560,9 +560,14 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Measured at 64 rows (cfg4): the gated out_proj (N 1024, K 2048) 13.6 us split over K vs
 // 16 us; the LM head (N 32000) 50 us vs 70 us for norm + rocBLAS; the in_proj (N 4384,
 // K 1024) 19.5 us split vs 18.6 us, so mode 1 below 16384 columns stays on rocBLAS.
+//
+// g2 / nout: when the few-row kernel's split finish can, it also writes nout = RMSNorm(y) * g2
+// (the next layer's normalised input) and sets *normed.
 ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const float* z, long ldz,
                      const float* g, const float* W, float* y, long ldy, int M, int N, int K,
-                     float beta, float* tmp) {
+                     float beta, float* tmp, const float* g2 = nullptr, float* nout = nullptr,
+                     bool* normed = nullptr) {
+    if (normed) *normed = false;
     ssm_ctx* c = m->ctx;
     const Dims& d = m->dm;
     const bool wanted = mode == 2 || (mode == 1 && N >= 16384);
@@ -579,7 +584,7 @@ ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const flo
             m->rg_bytes = need;
         }
         return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, d.eps,
-                                   m->rg, m->rg_bytes, c->stream);
+                                   m->rg, m->rg_bytes, c->stream, g2, nout, N, normed);
     }
     if (mode == 1) {
         SSM_TRY(ssm_rmsnorm(x, ldx, g, tmp, K, M, K, d.eps, c->stream));
@@ -594,8 +599,14 @@ ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const flo
 
 // One-token layer step for B sequences with the recurrent state:
 // hid += mixer(RMSNorm(hid)). The norms ride in the projections' prologues (proj_rows).
+//
+// normed_in: w.nrm already holds RMSNorm(hid) * norm (the previous layer's out_proj wrote it);
+// g_next: the next layer's norm weight, so that this layer's out_proj can write the next
+// layer's normalised input into w.nrm (then *normed_out is set).
 ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* ssm_st,
-                      float* conv_st, const Ws& w) {
+                      float* conv_st, const Ws& w, bool normed_in, const float* g_next,
+                      bool* normed_out) {
+    *normed_out = false;
     const Dims& d = m->dm;
     ssm_ctx* c = m->ctx;
     hipStream_t st = c->stream;
@@ -605,8 +616,11 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* 
         float *xz = w.a, *xc = w.b, *dbl = w.c, *dtv = w.d, *y = w.e;
         const int RN = d.R + 2 * d.N;
         { Stage g(c, "m1.step.in_proj");
-          SSM_TRY(proj_rows(m, 1, hid, d.d, nullptr, 0, W + Ly.norm, W + Ly.in_proj, xz, 2 * d.D,
-                            B, 2 * d.D, d.d, 0.f, w.nrm)); }
+          if (normed_in)
+              SSM_TRY(gemm(c, B, 2 * d.D, d.d, w.nrm, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f));
+          else
+              SSM_TRY(proj_rows(m, 1, hid, d.d, nullptr, 0, W + Ly.norm, W + Ly.in_proj, xz,
+                                2 * d.D, B, 2 * d.D, d.d, 0.f, w.nrm)); }
         { Stage g(c, "m1.step.conv");
           SSM_TRY(ssm_conv1d_update(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, conv_st, B,
                                     d.D, d.K, 1, st)); }
@@ -627,8 +641,11 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* 
         float *zx = w.a, *xbc = w.b, *y = w.c, *yn = w.d;
         const int GN = d.G * d.N;
         { Stage g(c, "m2.step.in_proj");
-          SSM_TRY(proj_rows(m, 1, hid, d.d, nullptr, 0, W + Ly.norm, W + Ly.in_proj, zx, d.nin, B,
-                            d.nin, d.d, 0.f, w.nrm)); }
+          if (normed_in)
+              SSM_TRY(gemm(c, B, d.nin, d.d, w.nrm, d.d, W + Ly.in_proj, zx, d.nin, 0.f));
+          else
+              SSM_TRY(proj_rows(m, 1, hid, d.d, nullptr, 0, W + Ly.norm, W + Ly.in_proj, zx,
+                                d.nin, B, d.nin, d.d, 0.f, w.nrm)); }
         { Stage g(c, "m2.step.conv");
           SSM_TRY(ssm_conv1d_update(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc, d.cd,
                                     conv_st, B, d.cd, d.K, 1, st)); }
@@ -639,7 +656,7 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* 
                                       d.N, st)); }
         { Stage g(c, "m2.step.out_proj");
           SSM_TRY(proj_rows(m, 2, y, d.D, zx, d.nin, W + Ly.gnorm, W + Ly.out_proj, hid, d.d, B,
-                            d.d, d.D, 1.f, yn)); }
+                            d.d, d.D, 1.f, yn, g_next, g_next ? w.nrm : nullptr, normed_out)); }
     }
     return SSM_OK;
 }
@@ -652,12 +669,14 @@ ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s
     hipStream_t st = m->ctx->stream;
     const long T = (long)B * L;
     SSM_TRY(ssm::launch_embed(d_ids, m->w + m->emb, w.hid, T, d.d, d.V, m->d_flag, st));
+    bool normed = false;   // w.nrm holds the next layer's normalised input (one-token path)
     for (int l = 0; l < d.nl; ++l) {
         const LayerW& Ly = m->layers[l];
         float* ss = s ? s->ssm[l] : nullptr;
         float* cs = s ? s->conv[l] : nullptr;
         if (L == 1 && s) {
-            SSM_TRY(mixer_step(m, Ly, w.hid, B, ss, cs, w));
+            const float* g_next = l + 1 < d.nl ? m->w + m->layers[l + 1].norm : nullptr;
+            SSM_TRY(mixer_step(m, Ly, w.hid, B, ss, cs, w, normed, g_next, &normed));
         } else {
             SSM_TRY(ssm_rmsnorm(w.hid, d.d, m->w + Ly.norm, w.nrm, d.d, (int)T, d.d, d.eps, st));
             SSM_TRY(mixer(m, Ly, w.nrm, w.hid, 1.f, B, L, ss, cs, w));

@@ -276,6 +276,58 @@ __global__ __launch_bounds__(256) void rowgemm_reduce(RgArgs a) {
     *yp = v;
 }
 
+// Split-K finish fused with the next layer's RMSNorm (decode: the out_proj's result is the
+// residual stream that the next in_proj normalises): one 1024-thread workgroup per row m
+// finishes the row as rowgemm_reduce does (a thread per column, its slice loads issued
+// together), keeps it in LDS, and writes nout[m, :] = Y[m, :] * g2 *
+// rsqrt(mean(Y[m, :]^2) + eps).
+constexpr int kNormCols = 8192;   // widest row the fused finish keeps in LDS
+template <int MODE>
+__global__ __launch_bounds__(1024) void rowgemm_reduce_norm(RgArgs a, const float* __restrict__ g2,
+                                                           float* __restrict__ nout, long ldn) {
+    __shared__ float row[kNormCols];
+    __shared__ float part_ss[16];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    const long MN = (long)a.M * a.N;
+    float rs = 1.f;
+    if (MODE != MODE_PLAIN) {
+        float tv[kMaxSplit];
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; ++s) tv[s] = s < a.S ? a.ssqp[(long)s * a.M + m] : 0.f;
+        float t = 0.f;
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; ++s) t += tv[s];
+        rs = rsqrtf(t / (float)a.K + a.eps);
+    }
+    const float* pm = a.part + (long)m * a.N;
+    float* ym = a.Y + (long)m * a.ldy;
+    float ss = 0.f;
+    for (int n = tid; n < a.N; n += 1024) {
+        float pv[kMaxSplit];
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; ++s) pv[s] = s < a.S ? pm[s * MN + n] : 0.f;
+        float v = 0.f;
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; ++s) v += pv[s];
+        v *= rs;
+        if (a.beta != 0.f) v = fmaf(a.beta, ym[n], v);
+        ym[n] = v;
+        row[n] = v;
+        ss = fmaf(v, v, ss);
+    }
+    // block sum of squares (16 waves)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63) == 0) part_ss[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) tot += part_ss[v];
+    const float r2 = rsqrtf(tot / (float)a.N + a.eps);
+    float* om = nout + (long)m * ldn;
+    for (int n = tid; n < a.N; n += 1024) om[n] = row[n] * r2 * g2[n];
+}
+
 // Splits of K for a shape: enough (column tile, slice) workgroups to fill the chip, each
 // slice a whole number of groups of four K blocks.
 struct Split {
@@ -316,7 +368,8 @@ size_t rowgemm_workspace(int M, int N, int K) {
 ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, long ldz,
                           const float* g, const float* W, float* Y, long ldy, int M, int N, int K,
                           float beta, float eps, void* workspace, size_t workspace_bytes,
-                          hipStream_t st) {
+                          hipStream_t st, const float* g2, float* nout, long ldn, bool* normed) {
+    if (normed) *normed = false;
     if (!rowgemm_ok(M, N, K))
         return fail(SSM_ERR_UNSUPPORTED, "row GEMM: need 1 <= M <= %d and K %% 4 == 0 (M=%d K=%d)",
                     kRows, M, K);
@@ -336,20 +389,19 @@ ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, lo
     }
     const unsigned grid = (unsigned)(8 * cdiv((long)p.ntiles * p.S, 8));
     const unsigned rgrid = (unsigned)cdiv((long)M * N, 256);
+    // the next RMSNorm rides on the split finish when there is one and the row fits in LDS
+    const bool fuse = g2 && nout && p.S > 1 && N <= kNormCols;
+    if (fuse && normed) *normed = true;
+#define RG_LAUNCH(MD)                                                                       \
+    rowgemm_kernel<MD><<<grid, 256, 0, st>>>(a);                                            \
+    if (fuse) rowgemm_reduce_norm<MD><<<(unsigned)M, 1024, 0, st>>>(a, g2, nout, ldn);     \
+    else if (p.S > 1) rowgemm_reduce<MD><<<rgrid, 256, 0, st>>>(a)
     switch (mode) {
-        case 0:
-            rowgemm_kernel<MODE_PLAIN><<<grid, 256, 0, st>>>(a);
-            if (p.S > 1) rowgemm_reduce<MODE_PLAIN><<<rgrid, 256, 0, st>>>(a);
-            break;
-        case 1:
-            rowgemm_kernel<MODE_RMS><<<grid, 256, 0, st>>>(a);
-            if (p.S > 1) rowgemm_reduce<MODE_RMS><<<rgrid, 256, 0, st>>>(a);
-            break;
-        default:
-            rowgemm_kernel<MODE_GATED><<<grid, 256, 0, st>>>(a);
-            if (p.S > 1) rowgemm_reduce<MODE_GATED><<<rgrid, 256, 0, st>>>(a);
-            break;
+        case 0: RG_LAUNCH(MODE_PLAIN); break;
+        case 1: RG_LAUNCH(MODE_RMS); break;
+        default: RG_LAUNCH(MODE_GATED); break;
     }
+#undef RG_LAUNCH
     return check_launch("rowgemm");
 }
 
@@ -374,5 +426,5 @@ extern "C" ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const 
                 "ssm_linear_rows: x, z, g, W must be 16-byte aligned with ld % 4 == 0");
     if (M == 0 || N == 0) return SSM_OK;
     return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, eps, workspace,
-                               workspace_bytes, (hipStream_t)stream);
+                               workspace_bytes, (hipStream_t)stream, nullptr, nullptr, 0, nullptr);
 }
