@@ -114,11 +114,26 @@ __global__ void scan_chunk_prefix(const float* __restrict__ A, int L, int D, int
     const int b = (int)(i / ((long)D * N));
     const float A2 = A[(long)d * N + n] * ssm::kLog2e;
     float carry = h0 ? h0[((long)b * D + d) * N + n] : 0.f;
-    for (int c = 0; c < NC; ++c) {
-        float* p = hc + (((long)b * NC + c) * N + n) * D + d;
-        const float hend = *p;
-        *p = carry;
-        carry = fmaf(ssm::ex2(A2 * sdt[((long)b * NC + c) * D + d]), carry, hend);
+    // the chunk-end states and dt sums of kPre chunks are loaded before the carry chain
+    // consumes them (the chain itself has no memory latency in it)
+    constexpr int kPre = 8;
+    const long cstride = (long)N * D;
+    float* p0 = hc + ((long)b * NC * N + n) * D + d;
+    const float* s0 = sdt + (long)b * NC * D + d;
+    for (int c0 = 0; c0 < NC; c0 += kPre) {
+        float he[kPre], sd[kPre];
+#pragma unroll
+        for (int u = 0; u < kPre; ++u) {
+            const bool live = c0 + u < NC;
+            he[u] = live ? p0[(long)(c0 + u) * cstride] : 0.f;
+            sd[u] = live ? s0[(long)(c0 + u) * D] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kPre; ++u) {
+            if (c0 + u >= NC) break;
+            p0[(long)(c0 + u) * cstride] = carry;
+            carry = fmaf(ssm::ex2(A2 * sd[u]), carry, he[u]);
+        }
     }
     if (hT) hT[((long)b * D + d) * N + n] = carry;
 }
