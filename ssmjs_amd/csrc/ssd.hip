@@ -1,13 +1,15 @@
 // K3-K6: Mamba-2 SSD prefill (Dao & Gu 2024, section 6) for gfx950, and K7: the one-token
 // Mamba-2 state update.
 //
-// One workgroup (4 waves) owns one (batch, head, segment) and walks the segment's chunks in
-// order with the P x N state held in MFMA accumulator registers, so the chunk-state tensor is
-// never written to HBM. Per chunk of Q = 64 steps:
+// One workgroup owns one (batch, segment) and HPW heads of one group (4 waves per head; two
+// heads for bf16 inputs, one for fp32) and walks the segment's chunks in order with each
+// head's P x N state held in MFMA accumulator registers, so the chunk-state tensor is never
+// written to HBM. Per chunk of Q = 64 steps:
 //   dt/decay  every wave computes dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix
 //             sum of dt' * A_h over the chunk with a 64-lane DPP scan.
 //   staging   X, X * w with w_j = exp(acum_end - acum_j) dt'_j, and B go to LDS as bf16 (hi,
-//             plus lo when SPLIT); each wave keeps its 16 rows of C in registers.
+//             plus lo when SPLIT). C goes to LDS too when two heads share it; with one head
+//             each wave keeps its 16 rows of C in registers.
 //   Y_off     Y^T[p,i] = exp(acum_i) * sum_n S[p,n] C[i,n]              (MFMA, K = N)
 //   Y_diag    S^T[j,i] = sum_n B[j,n] C[i,n]; mask j <= i; * exp(acum_i - acum_j) dt'_j;
 //             Y^T[p,i] += sum_j X^T[p,j] S^T[j,i]                          (MFMA, K = N, Q)
@@ -101,19 +103,22 @@ __device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v -
 // are conflict-free at pitch 144; the transposed reads over rows j0 + 8 q4 (+4) meet 2-way
 // bank conflicts at every pitch (SQ_LDS_BANK_CONFLICT). A layout without them (k-slot rows
 // 4 q4 apart, pitches of 16 mod 32) ran no faster: LDS is not what bounds this kernel.
-template <bool SPLIT, int NN, bool FULL>
+template <bool SPLIT, int NN, bool FULL, int HPW>
 struct Smem {
     static constexpr int NS = SPLIT ? 2 : 1;
     static constexpr int XP = P + 8;                   // X / Xw row pitch (bf16)
-    static constexpr int BP = NN + 16;                 // B row pitch
+    static constexpr int BP = NN + 16;                 // B / C row pitch
     // 16-byte alignment lets the compiler use ds_read_b128 / ds_write_b128 for the 8-wide
-    // bf16 rows (every pitch is a multiple of 8 elements)
-    alignas(16) __bf16 xw[NS][Q][XP];                  // X * w_j   (j, p)
+    // bf16 rows (every pitch is a multiple of 8 elements). B and C belong to the group and
+    // are staged once for the HPW heads of the workgroup; the other tiles are per head.
+    alignas(16) __bf16 xw[HPW][NS][Q][XP];             // X * w_j   (j, p)
     alignas(16) __bf16 b[NS][Q][BP];                   // B         (j, n)
-    alignas(16) __bf16 x[FULL ? NS : 1][FULL ? Q : 1][XP];   // X   (j, p)
-    alignas(16) __bf16 s[FULL ? NS : 1][FULL ? NN : 1][XP];  // state^T (n, p)
-    alignas(16) float g[Q];    // acum_j log2(e) - log2(dt'_j): the decay weight exponent
-    alignas(16) float ac[Q];   // acum_j log2(e)
+    static constexpr bool CST = FULL && HPW > 1;       // C staged (shared by two heads)
+    alignas(16) __bf16 c[CST ? NS : 1][CST ? Q : 1][BP];              // C   (i, n)
+    alignas(16) __bf16 x[HPW][FULL ? NS : 1][FULL ? Q : 1][XP];       // X   (j, p)
+    alignas(16) __bf16 s[HPW][FULL ? NS : 1][FULL ? NN : 1][XP];      // state^T (n, p)
+    alignas(16) float g[HPW][Q];    // acum_j log2(e) - log2(dt'_j): the decay weight exponent
+    alignas(16) float ac[HPW][Q];   // acum_j log2(e)
 };
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -130,17 +135,18 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Per-thread raw prefetch of one chunk. X: wave w reads rows 16w .. 16w+15 as whole rows,
-// XL lanes of 16 bytes (XE elements) per row and XR rows per load, so every load covers full
-// 128-byte lines; lane t holds row 16w + XR k + t / XL, columns XE (t % XL) + 0 .. XE-1 of
-// load k. B: rows t/(NN/8) + (256/(NN/8)) k, 8 elements at 8 (t % (NN/8)). dt: time step
-// lane. The C fragments of the wave's strip are prefetched separately (they are still in use
-// when the X / B prefetch is issued).
-template <typename TIN, int NN>
+// Per-thread raw prefetch of one chunk. X (of the wave's head): wave w reads rows
+// 16w .. 16w+15 as whole rows, XL lanes of 16 bytes (XE elements) per row and XR rows per
+// load, so every load covers full 128-byte lines; lane t holds row 16w + XR k + t / XL,
+// columns XE (t % XL) + 0 .. XE-1 of load k. B, and C when two heads share it (shared by the
+// workgroup's heads): thread t of the workgroup reads rows t / (NN/8) + BR k, 8 elements at
+// 8 (t % (NN/8)). dt: time step lane. With one head per workgroup each wave loads its own C
+// rows as MFMA fragments instead (no staging).
+template <typename TIN, int NN, bool FULL, int HPW>
 struct Raw {
     static constexpr int KS = NN / 32;
-    static constexpr int BL = NN / 8;          // lanes per B row
-    static constexpr int BR = 256 / BL;        // B rows per pass
+    static constexpr int BL = NN / 8;                // lanes per B / C row
+    static constexpr int BR = 256 * HPW / BL;        // B / C rows per pass
     static constexpr int BPASS = Q / BR;
     using v8 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x8>::type;
     static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // 16-byte units per 8 elements
@@ -150,6 +156,7 @@ struct Raw {
     static constexpr int XK = 16 / XR;                     // X loads per wave
     v8 x[XK];
     v8 b[BPASS][V8N];
+    v8 c[FULL && HPW > 1 ? BPASS : 1][V8N];
     float dt;
 };
 
@@ -200,35 +207,45 @@ __device__ __forceinline__ V vzero() {
     return v;
 }
 
-// Two workgroups per CU where the LDS tile allows it (bf16 inputs: <= 56 KB each), so each
-// SIMD interleaves two waves' MFMA, LDS and VALU phases; this caps registers at 256 per lane.
-template <typename TIN, bool SPLIT, int NN, bool FULL>
-__global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
-    __shared__ __attribute__((aligned(16))) Smem<SPLIT, NN, FULL> sm;
-    using SM = Smem<SPLIT, NN, FULL>;
+// Launch shape: HPW heads of one group per workgroup (4 waves per head). bf16 inputs run two
+// heads per workgroup (8 waves, 111 KB LDS, one workgroup per CU): B and C are loaded and
+// staged once for both heads, which halves their share of the memory instructions. fp32
+// inputs (SPLIT) keep one head and one workgroup per CU (hi and lo tiles).
+template <typename TIN, bool SPLIT, int NN, bool FULL, int HPW>
+__global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void ssd_kernel(SsdArgs a) {
+    __shared__ __attribute__((aligned(16))) Smem<SPLIT, NN, FULL, HPW> sm;
+    using SM = Smem<SPLIT, NN, FULL, HPW>;
     constexpr int NB = NN / 16;   // state n-blocks per wave
     constexpr int KS = NN / 32;   // k-steps over n
-    using RW = Raw<TIN, NN>;
+    using RW = Raw<TIN, NN, FULL, HPW>;
     constexpr int L1 = SPLIT ? 1 : 0;   // index of the lo copy (aliases hi when unused)
+    constexpr bool CST = SM::CST;       // C staged in LDS (two heads) or loaded per wave
 
     int wg = blockIdx.x;
     if (a.remap) {
         const int per = gridDim.x / 8;
         wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
     }
-    // segment-major order: the heads of one (batch, segment) are adjacent, so after the
+    // segment-major order: the head groups of one (batch, segment) are adjacent, so after the
     // XCD remap they run on the same XCD and read that segment's B and C through one L2
-    const int seg = wg / (a.B * a.H);
-    const int bh = wg % (a.B * a.H);
-    const int h = bh % a.H, b = bh / a.H;
-    const int g = h / (a.H / a.G);
+    const int HW = a.H / HPW;   // workgroups per (batch, segment)
+    const int seg = wg / (a.B * HW);
+    const int bhw = wg % (a.B * HW);
+    const int b = bhw / HW;
     // w is wave-uniform: readfirstlane lets the compiler keep it (and the j-block loop
-    // bounds derived from it) in scalar registers
+    // bounds derived from it) in scalar registers. Wave w works on head hw = w / 4 of the
+    // workgroup as its wave wl: w % 4 for the first head, 3 - w % 4 for the second. Waves w and
+    // w + 4 share a SIMD, and Y_diag grows with wl, so each SIMD gets one light and one heavy
+    // wave.
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hw = w >> 2, wl = (hw & 1) ? 3 - (w & 3) : (w & 3);
+    const int h = HPW * (bhw % HW) + hw;
+    const int bh = b * a.H + h;
+    const int g = h / (a.H / a.G);
     const int l16 = lane & 15, q4 = lane >> 4;
-    const int ic = 16 * w + l16;        // this lane's output row in the chunk
-    const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);      // B staging row / column
+    const int ic = 16 * wl + l16;       // this lane's output row in the chunk
+    const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);      // B / C staging row / column
 
     const float Ah = a.A[h];
     const float dtb = a.dt_bias ? a.dt_bias[h] : 0.f;
@@ -247,19 +264,21 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
     const TIN* cm0 = reinterpret_cast<const TIN*>(a.Cm) + brow * a.ldc + (long)g * a.N;
     const float* d0 = a.dt + brow * a.lddt + h;
     const int xr = lane / RW::XL, xc = RW::XE * (lane % RW::XL);   // X row in a load / column
-    const unsigned ox = (unsigned)((16 * w + xr) * a.ldx + xc) * SZ;
+    const unsigned ox = (unsigned)((16 * wl + xr) * a.ldx + xc) * SZ;
     const unsigned oxk = (unsigned)(RW::XR * a.ldx) * SZ;
     const unsigned ob = (unsigned)(br * a.ldb + bc) * SZ;
     const unsigned obk = (unsigned)(RW::BR * a.ldb) * SZ;
-    // Lanes l16 = 2r and 2r + 1 share the 128-byte lines of rows 16w + 2r and 16w + 2r + 1: the
-    // C load (h, sel) and the y store (h, sel) of lane (l16, q4) cover row
-    // 16w + (l16 & ~1) + sel at byte 128 h + 64 (l16 & 1) + 16 q4 of the row, so each load or
-    // store instruction moves whole lines of 8 rows. A DPP swap between the two lanes puts every
+    const unsigned occ = (unsigned)(br * a.ldc + bc) * SZ;
+    const unsigned occk = (unsigned)(RW::BR * a.ldc) * SZ;
+    const unsigned od = (unsigned)(lane * a.lddt) * 4u;
+    // Lanes l16 = 2r and 2r + 1 share the 128-byte lines of rows 16wl + 2r and 16wl + 2r + 1:
+    // the y store (and, without C staging, the C load) (h, sel) of lane (l16, q4) covers row
+    // 16wl + (l16 & ~1) + sel at byte 128 h + 64 (l16 & 1) + 16 q4 of the row, so each such
+    // instruction moves whole lines of 8 rows. A DPP swap between the two lanes puts every
     // value where the MFMA layout has it.
     const int podd = l16 & 1;
     const unsigned oc = (unsigned)(ic * a.ldc + 8 * q4) * SZ;
-    const unsigned oc2 = (unsigned)((16 * w + l16 - podd) * a.ldc + 32 * podd + 8 * q4) * SZ;
-    const unsigned od = (unsigned)(lane * a.lddt) * 4u;
+    const unsigned oc2 = (unsigned)((16 * wl + l16 - podd) * a.ldc + 32 * podd + 8 * q4) * SZ;
     // rows of chunk c that exist; 0 past the segment, so a prefetch there reads nothing
     auto rows_of = [&](int c) { return c < c_end ? min(Q, a.L - c * Q) : 0; };
     auto span = [](int qv, long ld, int width, unsigned esz) {
@@ -281,15 +300,23 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         for (int k = 0; k < RW::BPASS; ++k)
 #pragma unroll
             for (int u = 0; u < RW::V8N; ++u) raw.b[k][u] = bload16<v8>(rb, ob + k * obk + 4 * u * SZ);
+        if constexpr (CST) {
+            const auto rc = rsrc(cm0 + r0 * a.ldc, span(qv, a.ldc, NN, SZ));
+#pragma unroll
+            for (int k = 0; k < RW::BPASS; ++k)
+#pragma unroll
+                for (int u = 0; u < RW::V8N; ++u) raw.c[k][u] = bload16<v8>(rc, occ + k * occk + 4 * u * SZ);
+        }
     };
-    // C rows of the wave's strip: row ic, n = 32ks + 8q4 + 0..7 (MFMA B-operand fragments)
-    v8 craw[FULL ? KS : 1][RW::V8N];
+    // Without C staging: C rows of the wave's strip, row ic, n = 32ks + 8q4 + 0..7 (MFMA
+    // B-operand fragments), prefetched after their last use in the previous chunk
+    v8 craw[FULL && !CST ? KS : 1][RW::V8N];
     auto load_c = [&](int c) {
-        if constexpr (FULL) {
+        if constexpr (FULL && !CST) {
             const int qv = rows_of(c);
             const auto rc = rsrc(cm0 + (long)c * Q * a.ldc, span(qv, a.ldc, NN, SZ));
             if constexpr (sizeof(TIN) == 2) {
-                // craw[2h + sel]: row 16w + (l16 & ~1) + sel, n = 64h + 32 (l16 & 1) + 8 q4 + 0..7
+                // craw[2h + sel]: row 16wl + (l16 & ~1) + sel, n = 64h + 32 (l16 & 1) + 8 q4 + 0..7
 #pragma unroll
                 for (int hh = 0; hh < KS / 2; ++hh)
 #pragma unroll
@@ -304,8 +331,27 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
             }
         }
     };
+    // 8 elements of B or C to LDS (hi, plus lo when SPLIT)
+    auto stage8 = [&](__bf16 (*tile)[Q][SM::BP], int j, const v8* src) {
+        if constexpr (sizeof(TIN) == 2) {
+            *reinterpret_cast<bf16x8*>(&tile[0][j][bc]) = src[0];
+        } else {
+            bf16x8 hh, ll;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float e4[4] = {src[u].x, src[u].y, src[u].z, src[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hh[4 * u + e] = hi_of(e4[e]);
+                    ll[4 * u + e] = lo_of(e4[e], hh[4 * u + e]);
+                }
+            }
+            *reinterpret_cast<bf16x8*>(&tile[0][j][bc]) = hh;
+            if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&tile[L1][j][bc]) = ll;
+        }
+    };
 
-    // ---- entering state -> accumulators (wave w: rows p = 16w + 4*q4 + r, cols 16nb + l16)
+    // ---- entering state -> accumulators (wave wl: rows p = 16wl + 4*q4 + r, cols 16nb + l16)
     const float* init = nullptr;
     if (FULL) {
         if (a.nseg > 1) init = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
@@ -316,11 +362,11 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            S[nb][r] = init ? init[(long)(16 * w + 4 * q4 + r) * NN + 16 * nb + l16] : 0.f;
+            S[nb][r] = init ? init[(long)(16 * wl + 4 * q4 + r) * NN + 16 * nb + l16] : 0.f;
     bool state_live = init != nullptr;
     float decay_sum = 0.f;
 
-    // The accumulators hold S[p = 16w + 4q4 + r][n = 16nb + l16] for r = 0..3: four
+    // The accumulators hold S[p = 16wl + 4q4 + r][n = 16nb + l16] for r = 0..3: four
     // consecutive p of one n, i.e. one 8-byte run of the state^T tile.
     auto write_state_lds = [&]() {
 #pragma unroll
@@ -331,8 +377,8 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                 hv[r] = hi_of(S[nb][r]);
                 lv[r] = lo_of(S[nb][r], hv[r]);
             }
-            *reinterpret_cast<bf16x4*>(&sm.s[0][16 * nb + l16][16 * w + 4 * q4]) = hv;
-            if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.s[L1][16 * nb + l16][16 * w + 4 * q4]) = lv;
+            *reinterpret_cast<bf16x4*>(&sm.s[hw][0][16 * nb + l16][16 * wl + 4 * q4]) = hv;
+            if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.s[hw][L1][16 * nb + l16][16 * wl + 4 * q4]) = lv;
         }
     };
     if (FULL && state_live) write_state_lds();
@@ -340,8 +386,8 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
     load_c(c_begin);
     if constexpr (FULL) {
         // Four stores into an empty range (dropped by the range check) make the memory
-        // instructions in flight at loop entry match the back edge (C loads, then the four
-        // y stores), so the wait for C never includes the previous chunk's stores.
+        // instructions in flight at loop entry match the back edge (the prefetches, then the
+        // four y stores), so the wait for a prefetch never includes the previous chunk's stores.
         const auto none = rsrc(a.y, 0u);
 #pragma unroll
         for (int pb = 0; pb < P / 16; ++pb) bstore16(make_float4(0.f, 0.f, 0.f, 0.f), none, 64u * pb);
@@ -361,21 +407,21 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         const float acend = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
         decay_sum += acend;
-        if (w == 0) {
+        if (wl == 0) {
             // exp(acum_i - acum_j) dt'_j = exp2(ac_i - g_j); dt'_j = 0 gives g_j = +inf, weight 0
             const float sl = sc * ssm::kLog2e;
-            sm.g[lane] = sl - __builtin_amdgcn_logf(dv);
-            sm.ac[lane] = sl;
+            sm.g[hw][lane] = sl - __builtin_amdgcn_logf(dv);
+            sm.ac[hw][lane] = sl;
         }
-        const float wl = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
+        const float wl_ = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
 
         // ---- stage X and X w (rows of the X prefetch; w_j comes from lane j of this wave)
 #pragma unroll
         for (int k = 0; k < RW::XK; ++k) {
             constexpr int E = RW::XE;
-            const int j = 16 * w + RW::XR * k + xr;
+            const int j = 16 * wl + RW::XR * k + xr;
             const float wj = __builtin_bit_cast(
-                float, __builtin_amdgcn_ds_bpermute(4 * j, __builtin_bit_cast(int, wl)));
+                float, __builtin_amdgcn_ds_bpermute(4 * j, __builtin_bit_cast(int, wl_)));
             float xv[E];
             if constexpr (sizeof(TIN) == 4) {
                 xv[0] = raw.x[k].x; xv[1] = raw.x[k].y; xv[2] = raw.x[k].z; xv[3] = raw.x[k].w;
@@ -391,11 +437,11 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                 wh[e] = hi_of(u);
                 wlo[e] = lo_of(u, wh[e]);
             }
-            *reinterpret_cast<bfE*>(&sm.xw[0][j][xc]) = wh;
-            if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.xw[L1][j][xc]) = wlo;
+            *reinterpret_cast<bfE*>(&sm.xw[hw][0][j][xc]) = wh;
+            if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.xw[hw][L1][j][xc]) = wlo;
             if constexpr (FULL) {
                 if constexpr (sizeof(TIN) == 2) {
-                    *reinterpret_cast<bf16x8*>(&sm.x[0][j][xc]) = raw.x[k];
+                    *reinterpret_cast<bf16x8*>(&sm.x[hw][0][j][xc]) = raw.x[k];
                 } else {
                     bfE hh, ll;
 #pragma unroll
@@ -403,35 +449,21 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                         hh[e] = hi_of(xv[e]);
                         ll[e] = lo_of(xv[e], hh[e]);
                     }
-                    *reinterpret_cast<bfE*>(&sm.x[0][j][xc]) = hh;
-                    if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.x[L1][j][xc]) = ll;
+                    *reinterpret_cast<bfE*>(&sm.x[hw][0][j][xc]) = hh;
+                    if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.x[hw][L1][j][xc]) = ll;
                 }
             }
         }
+        // ---- stage B and C (shared by the workgroup's heads)
 #pragma unroll
         for (int k = 0; k < RW::BPASS; ++k) {
-            const int j = br + RW::BR * k;
-            if constexpr (sizeof(TIN) == 2) {
-                *reinterpret_cast<bf16x8*>(&sm.b[0][j][bc]) = raw.b[k][0];
-            } else {
-                bf16x8 hh, ll;
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const float e4[4] = {raw.b[k][u].x, raw.b[k][u].y, raw.b[k][u].z, raw.b[k][u].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        hh[4 * u + e] = hi_of(e4[e]);
-                        ll[4 * u + e] = lo_of(e4[e], hh[4 * u + e]);
-                    }
-                }
-                *reinterpret_cast<bf16x8*>(&sm.b[0][j][bc]) = hh;
-                if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&sm.b[L1][j][bc]) = ll;
-            }
+            stage8(sm.b, br + RW::BR * k, raw.b[k]);
+            if constexpr (CST) stage8(sm.c, br + RW::BR * k, raw.c[k]);
         }
-
         // ---- C rows of this wave's strip as MFMA fragments: row ic, n = 32ks + 8q4 + 0..7
+        // (from registers here without C staging, from LDS after the barrier with it)
         bf16x8 cfh[FULL ? KS : 1], cfl[FULL ? KS : 1];
-        if constexpr (FULL) {
+        if constexpr (FULL && !CST) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 if constexpr (sizeof(TIN) == 2) {
@@ -464,7 +496,14 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         load_raw(c + 1);
 
         if constexpr (FULL) {
-            const float aci = sm.ac[ic];
+            if constexpr (CST) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    cfh[ks] = *reinterpret_cast<const bf16x8*>(&sm.c[0][ic][32 * ks + 8 * q4]);
+                    if constexpr (SPLIT) cfl[ks] = *reinterpret_cast<const bf16x8*>(&sm.c[L1][ic][32 * ks + 8 * q4]);
+                }
+            }
+            const float aci = sm.ac[hw][ic];
             floatx4 Y[P / 16];
 #pragma unroll
             for (int pb = 0; pb < P / 16; ++pb) Y[pb] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -477,12 +516,12 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                     for (int ks = 0; ks < KS; ++ks) {
                         // S[p = 16pb + l16][n = 32ks + 8q4 + 0..7] from the state^T tile
                         const int n0 = 32 * ks + 8 * q4;
-                        const bf16x8 ah = cat(tr_read<SM::XP>(&sm.s[0][0][0], n0, 16 * pb, l16),
-                                              tr_read<SM::XP>(&sm.s[0][0][0], n0 + 4, 16 * pb, l16));
+                        const bf16x8 ah = cat(tr_read<SM::XP>(&sm.s[hw][0][0][0], n0, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.s[hw][0][0][0], n0 + 4, 16 * pb, l16));
                         Y[pb] = mfma(ah, cfh[ks], Y[pb]);
                         if constexpr (SPLIT) {
-                            const bf16x8 al = cat(tr_read<SM::XP>(&sm.s[L1][0][0], n0, 16 * pb, l16),
-                                                  tr_read<SM::XP>(&sm.s[L1][0][0], n0 + 4, 16 * pb, l16));
+                            const bf16x8 al = cat(tr_read<SM::XP>(&sm.s[hw][L1][0][0], n0, 16 * pb, l16),
+                                                  tr_read<SM::XP>(&sm.s[hw][L1][0][0], n0 + 4, 16 * pb, l16));
                             Y[pb] = mfma(ah, cfl[ks], Y[pb]);
                             Y[pb] = mfma(al, cfh[ks], Y[pb]);
                         }
@@ -493,8 +532,8 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                 for (int pb = 0; pb < P / 16; ++pb) Y[pb] *= e;
             }
 
-            // ---- Y_diag: wave w's rows i = 16w + l16 need the j-blocks 0..w. The body is
-            // unrolled per wave (switch on the wave-uniform w) so the independent C B^T chains
+            // ---- Y_diag: wave wl's rows i = 16wl + l16 need the j-blocks 0..wl. The body is
+            // unrolled per wave (switch on the wave-uniform wl) so the independent C B^T chains
             // of the j-blocks interleave. D_h x_i rides on the diagonal (j == i) of the decay
             // matrix: y_i = sum_j (L[i,j] + D_h [i == j]) x_j.
             auto y_diag = [&](auto wc) {
@@ -527,7 +566,7 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                         for (int r = 0; r < 4; ++r) sv[jb][r] = 0.f;
                         continue;
                     }
-                    const float4 gj = *reinterpret_cast<const float4*>(&sm.g[16 * jb + 4 * q4]);
+                    const float4 gj = *reinterpret_cast<const float4*>(&sm.g[hw][16 * jb + 4 * q4]);
                     const float gjr[4] = {gj.x, gj.y, gj.z, gj.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -535,7 +574,7 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                         if (jb < W) {
                             sv[jb][r] = f;
                         } else {
-                            const int dj = 4 * q4 + r;   // j - 16w
+                            const int dj = 4 * q4 + r;   // j - 16wl
                             sv[jb][r] = dj < l16 ? f : (dj == l16 ? f + Dh : 0.f);
                         }
                     }
@@ -553,19 +592,19 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
                     }
 #pragma unroll
                     for (int pb = 0; pb < P / 16; ++pb) {
-                        const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
-                                              tr_read<SM::XP>(&sm.x[0][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
+                        const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[hw][0][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.x[hw][0][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
                         Y[pb] = mfma(xh, sfh, Y[pb]);
                         if constexpr (SPLIT) {
-                            const bf16x8 xl = cat(tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
-                                                  tr_read<SM::XP>(&sm.x[L1][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
+                            const bf16x8 xl = cat(tr_read<SM::XP>(&sm.x[hw][L1][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                                  tr_read<SM::XP>(&sm.x[hw][L1][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
                             Y[pb] = mfma(xh, sfl, Y[pb]);
                             Y[pb] = mfma(xl, sfh, Y[pb]);
                         }
                     }
                 }
             };
-            switch (w) {
+            switch (wl) {
                 case 0: y_diag(std::integral_constant<int, 0>{}); break;
                 case 1: y_diag(std::integral_constant<int, 1>{}); break;
                 case 2: y_diag(std::integral_constant<int, 2>{}); break;
@@ -576,16 +615,16 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
             load_c(c + 1);
 
             // ---- y: Y[pb] holds row ic, p = 16pb + 4q4 + 0..3; store (h, sel) writes p-half h
-            // of row 16w + (l16 & ~1) + sel. Rows past the sequence end fall outside the
+            // of row 16wl + (l16 & ~1) + sel. Rows past the sequence end fall outside the
             // descriptor and are dropped.
             {
                 const auto ry = rsrc(a.y + (row0 * a.ldy + (long)h * P), span(qv, a.ldy, P, 4));
-                const unsigned oy = (unsigned)((16 * w + l16 - podd) * a.ldy + 16 * podd + 4 * q4) * 4u;
+                const unsigned oy = (unsigned)((16 * wl + l16 - podd) * a.ldy + 16 * podd + 4 * q4) * 4u;
 #pragma unroll
                 for (int hh = 0; hh < P / 32; ++hh) {
                     const floatx4 s0 = swap_pair(Y[2 * hh]), s1 = swap_pair(Y[2 * hh + 1]);
-                    const floatx4 v0 = podd ? s1 : Y[2 * hh];        // row 16w + (l16 & ~1)
-                    const floatx4 v1 = podd ? Y[2 * hh + 1] : s0;    // row 16w + (l16 & ~1) + 1
+                    const floatx4 v0 = podd ? s1 : Y[2 * hh];        // row 16wl + (l16 & ~1)
+                    const floatx4 v1 = podd ? Y[2 * hh + 1] : s0;    // row 16wl + (l16 & ~1) + 1
                     bstore16(make_float4(v0[0], v0[1], v0[2], v0[3]), ry, oy + 128u * hh);
                     bstore16(make_float4(v1[0], v1[1], v1[2], v1[3]), ry,
                              oy + (unsigned)(a.ldy * 4) + 128u * hh);
@@ -601,12 +640,12 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
 #pragma unroll
             for (int ks = 0; ks < Q / 32; ++ks) {
                 const int j0 = 32 * ks + 8 * q4;
-                const bf16x8 xh = cat(tr_read<SM::XP>(&sm.xw[0][0][0], j0, 16 * w, l16),
-                                      tr_read<SM::XP>(&sm.xw[0][0][0], j0 + 4, 16 * w, l16));
+                const bf16x8 xh = cat(tr_read<SM::XP>(&sm.xw[hw][0][0][0], j0, 16 * wl, l16),
+                                      tr_read<SM::XP>(&sm.xw[hw][0][0][0], j0 + 4, 16 * wl, l16));
                 bf16x8 xl;
                 if constexpr (SPLIT)
-                    xl = cat(tr_read<SM::XP>(&sm.xw[L1][0][0], j0, 16 * w, l16),
-                             tr_read<SM::XP>(&sm.xw[L1][0][0], j0 + 4, 16 * w, l16));
+                    xl = cat(tr_read<SM::XP>(&sm.xw[hw][L1][0][0], j0, 16 * wl, l16),
+                             tr_read<SM::XP>(&sm.xw[hw][L1][0][0], j0 + 4, 16 * wl, l16));
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     const bf16x8 bh_ = cat(tr_read<SM::BP>(&sm.b[0][0][0], j0, 16 * nb, l16),
@@ -632,13 +671,13 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void ssd_kernel(SsdArgs a) {
         if (a.hT && seg == a.nseg - 1) out = a.hT + (long)bh * P * NN;
     } else {
         out = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
-        if (tid == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
+        if (wl == 0 && lane == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
     }
     if (out) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) out[(long)(16 * w + 4 * q4 + r) * NN + 16 * nb + l16] = S[nb][r];
+            for (int r = 0; r < 4; ++r) out[(long)(16 * wl + 4 * q4 + r) * NN + 16 * nb + l16] = S[nb][r];
     }
 }
 
@@ -658,13 +697,16 @@ __global__ void ssd_seg_prefix(SsdArgs a, int PN) {
     }
 }
 
-template <typename TIN, bool SPLIT, int NN>
+template <typename TIN, bool SPLIT, int NN, int HPW>
 ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
-    const int nwg = a.B * a.H * a.nseg;
-    a.remap = (nwg % 8 == 0) ? 1 : 0;
     if (a.nseg > 1) {
+        // the state-only pass runs one head per workgroup: with no Y work its B tile is a
+        // small share of the memory instructions, and independent workgroups overlap better
+        // than two heads in lockstep
         SsdArgs s1 = a;
-        ssd_kernel<TIN, SPLIT, NN, false><<<nwg, 256, 0, st>>>(s1);
+        const int nwg1 = a.B * a.H * a.nseg;
+        s1.remap = (nwg1 % 8 == 0) ? 1 : 0;
+        ssd_kernel<TIN, SPLIT, NN, false, 1><<<nwg1, 256, 0, st>>>(s1);
         ssm_status e = ssm::check_launch("ssd_state_pass");
         if (e != SSM_OK) return e;
         const long n = (long)a.B * a.H * P * NN;
@@ -672,7 +714,9 @@ ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
         e = ssm::check_launch("ssd_seg_prefix");
         if (e != SSM_OK) return e;
     }
-    ssd_kernel<TIN, SPLIT, NN, true><<<nwg, 256, 0, st>>>(a);
+    const int nwg = a.B * (a.H / HPW) * a.nseg;
+    a.remap = (nwg % 8 == 0) ? 1 : 0;
+    ssd_kernel<TIN, SPLIT, NN, true, HPW><<<nwg, 256 * HPW, 0, st>>>(a);
     return ssm::check_launch("ssd_chunk_scan");
 }
 
@@ -904,8 +948,11 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
         a.seg_decay = a.seg_state + (size_t)B * H * a.nseg * P * N;
     }
     if (in_dtype == SSM_F32)
-        return N == 128 ? launch_ssd<float, true, 128>(a, st) : launch_ssd<float, true, 64>(a, st);
-    return N == 128 ? launch_ssd<__bf16, false, 128>(a, st) : launch_ssd<__bf16, false, 64>(a, st);
+        return N == 128 ? launch_ssd<float, true, 128, 1>(a, st) : launch_ssd<float, true, 64, 1>(a, st);
+    // bf16: two heads per workgroup when head pairs share a group
+    if ((H / G) % 2 == 0)
+        return N == 128 ? launch_ssd<__bf16, false, 128, 2>(a, st) : launch_ssd<__bf16, false, 64, 2>(a, st);
+    return N == 128 ? launch_ssd<__bf16, false, 128, 1>(a, st) : launch_ssd<__bf16, false, 64, 1>(a, st);
 }
 
 extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float* dt, long lddt,

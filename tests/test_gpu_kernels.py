@@ -207,6 +207,8 @@ def _bf(a):
     (2, 131, 3, 1, 64, True, "bf16"),
     (2, 256, 4, 1, 128, False, "bf16"),
     (1, 5, 2, 1, 128, True, "f32"),
+    (2, 200, 4, 2, 64, True, "bf16"),     # head pairs per group: two heads per workgroup
+    (1, 100, 6, 2, 128, True, "bf16"),    # three heads per group: one head per workgroup
 ])
 def test_ssd_matches_oracle(B, L, H, G, N, h0, dtype):
     case(f"ssd B={B} L={L} H={H} G={G} N={N} h0={h0} {dtype}")
