@@ -250,6 +250,163 @@ __global__ __launch_bounds__(256, 2) void rowgemm_kernel(RgArgs a) {
     if (MODE != MODE_PLAIN && tile == 0 && tid < M) a.ssqp[(long)s * M + tid] = ssq[tid];
 }
 
+// Direct-W variant for slices of at most 256 (most decode projections): a workgroup owns all
+// rows, 64 output columns (16 per wave) and one K slice of KS = 16 NU. Each wave loads its 16
+// W rows of the slice straight into registers in MFMA operand order, all at once (lane
+// (l16, q) of k group kg holds W[n0 + 16w + l16][16 kg + 4q .. +3]: one 16-byte load per
+// lane and group), while the workgroup stages the slice's operand P (X, or X silu(Z), times g)
+// in LDS; each k group is then 4 b128 LDS reads (the A fragments of the 4 row tiles) and 16
+// MFMAs against the W registers. The whole slice's HBM traffic is in flight together and the
+// MFMAs of a k group start as soon as its W arrives, with no barrier between the first and the
+// last MFMA. The row scale s[m] of the norm modes is left
+// to the finishing kernel, which computes it from X (and Z) itself, so this kernel always
+// writes partial tiles (S >= 2).
+template <int MODE, int NU>
+__global__ __launch_bounds__(256, NU > 16 ? 1 : 2) void rowgemm_direct_kernel(RgArgs a) {
+    constexpr int KS = 16 * NU;          // slice length
+    constexpr int XP = KS + 4;           // LDS row pitch (floats)
+    constexpr int FPR = KS / 4;          // float4 per staged row (64 FPR = 256 NU in all)
+    __shared__ __attribute__((aligned(16))) float xs[kRows][XP];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q = lane >> 4;
+    const int per = gridDim.x / 8;
+    const int wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (wg >= a.ntiles * a.S) return;
+    const int s = wg / a.ntiles, tile = wg % a.ntiles;
+    const int n0 = tile * kTileN;
+    const int k0 = s * KS;
+    const int M = a.M, K = a.K;
+    const int klen = min(KS, K - k0);   // a multiple of 4
+
+    // P staging: float4 j of thread t is element e = t + 256 j of the slice in row-major
+    // order (row e / FPR, float4 column e % FPR), so a row's loads are consecutive lanes; rows
+    // past M and k past the slice read zeros
+    const auto rx = ssm::rsrc(a.X + k0, (unsigned)(((long)(M - 1) * a.ldx + klen) * 4));
+    const auto rz = ssm::rsrc(MODE == MODE_GATED ? a.Z + k0 : a.X,
+                              MODE == MODE_GATED ? (unsigned)(((long)(M - 1) * a.ldz + klen) * 4) : 0u);
+    const auto rg = ssm::rsrc(a.g ? a.g + k0 : a.X, a.g ? (unsigned)klen * 4u : 0u);
+    auto col_of = [&](int j) { return (tid + 256 * j) % FPR; };
+    auto row_of = [&](int j) { return (tid + 256 * j) / FPR; };
+    auto kb_of = [&](int j) { return 4 * col_of(j) < klen ? (unsigned)col_of(j) * 16u : 0x80000000u; };
+    float4 xv[NU], zv[NU], gv[NU];
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+        const int row = row_of(j);
+        xv[j] = ssm::bload16<float4>(rx, (unsigned)(row * a.ldx) * 4u + kb_of(j));
+        if (MODE == MODE_GATED) zv[j] = ssm::bload16<float4>(rz, (unsigned)(row * a.ldz) * 4u + kb_of(j));
+        // the g float4 of the column: one load when every j has the same column
+        if (MODE != MODE_PLAIN)
+            gv[j] = (j == 0 || 256 % FPR != 0) ? ssm::bload16<float4>(rg, kb_of(j)) : gv[0];
+    }
+
+    // W rows n0 + 16w + l16 of the slice, issued after the (L2-resident) P operands so that the
+    // staging below waits for those only; the k groups' MFMAs then consume W as it arrives.
+    // Rows past N and k past the slice read zeros.
+    const int nrw = min(a.N - n0 - 16 * w, 16);
+    const auto rw = ssm::rsrc(a.W + (long)(n0 + 16 * w) * K + k0,
+                              nrw > 0 ? (unsigned)(((long)(nrw - 1) * K + klen) * 4) : 0u);
+    float4 wr[NU];
+#pragma unroll
+    for (int kg = 0; kg < NU; ++kg) {
+        const int k = 16 * kg + 4 * q;
+        wr[kg] = ssm::bload16<float4>(rw, k < klen ? (unsigned)(l16 * K + k) * 4u : 0x80000000u);
+    }
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+        float4 v = prologue<MODE>(xv[j], zv[j]);
+        if (MODE != MODE_PLAIN) v = mul4(v, gv[j]);
+        *reinterpret_cast<float4*>(&xs[row_of(j)][4 * col_of(j)]) = v;
+    }
+    __syncthreads();
+
+    // k group kg: MFMA t uses k = 16 kg + 4q + t for lane group q on both operands. The A
+    // fragments of group kg + 1 are read while group kg computes, and consecutive MFMAs go
+    // to the four independent row-tile accumulators.
+    floatx4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float4 av[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) av[0][i] = *reinterpret_cast<const float4*>(&xs[16 * i + l16][4 * q]);
+#pragma unroll
+    for (int kg = 0; kg < NU; ++kg) {
+        const int cb = kg & 1;
+        if (kg + 1 < NU) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                av[cb ^ 1][i] = *reinterpret_cast<const float4*>(&xs[16 * i + l16][16 * (kg + 1) + 4 * q]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = mfma4(av[cb][i].x, wr[kg].x, acc[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = mfma4(av[cb][i].y, wr[kg].y, acc[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = mfma4(av[cb][i].z, wr[kg].z, acc[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = mfma4(av[cb][i].w, wr[kg].w, acc[i]);
+    }
+
+    // lane holds rows 16i + 4q + r, column n0 + 16w + l16 of this slice's partial tile
+    const int n = n0 + 16 * w + l16;
+    if (n < a.N) {
+        float* pp = a.part + (long)s * M * a.N + n;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * i + 4 * q + r;
+                if (m < M) pp[(long)m * a.N] = acc[i][r];
+            }
+    }
+}
+
+// Row scale of the norm modes from the operands themselves: s[m] = rsqrt(mean_k P[m, k]^2 +
+// eps) with P = X or X silu(Z), summed by the threads of a workgroup in thread order and then
+// over the waves (deterministic). Every thread of the workgroup returns the same value.
+template <int MODE, int NT>
+__device__ __forceinline__ float row_scale(const RgArgs& a, int m, float* red) {
+    const int tid = threadIdx.x;
+    float ss = 0.f;
+    for (int k = 4 * tid; k < a.K; k += 4 * NT) {
+        float4 p = *reinterpret_cast<const float4*>(a.X + (long)m * a.ldx + k);
+        if (MODE == MODE_GATED) p = prologue<MODE>(p, *reinterpret_cast<const float4*>(a.Z + (long)m * a.ldz + k));
+        ss = sumsq(p, ss);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int v = 0; v < NT / 64; ++v) t += red[v];
+    return rsqrtf(t / (float)a.K + a.eps);
+}
+
+// Finish of the direct kernel's slices: a workgroup per (row m, 256 x CPT columns); the norm
+// modes' row scale is computed here from X / Z.
+template <int MODE>
+__global__ __launch_bounds__(256) void rowgemm_direct_reduce(RgArgs a) {
+    __shared__ float red[4];
+    const int m = blockIdx.y;
+    const float rs = MODE != MODE_PLAIN ? row_scale<MODE, 256>(a, m, red) : 1.f;
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.N) return;
+    const long MN = (long)a.M * a.N;
+    const float* pm = a.part + (long)m * a.N + n;
+    float pv[kMaxSplit];
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s) pv[s] = s < a.S ? pm[s * MN] : 0.f;
+    float v = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s) v += pv[s];
+    v *= rs;
+    float* yp = a.Y + (long)m * a.ldy + n;
+    if (a.beta != 0.f) v = fmaf(a.beta, *yp, v);
+    *yp = v;
+}
+
 // Split-K finish: Y = beta * Y + s[m] * (sum of the slices in slice order), one thread per
 // output; every slice's load is issued before the sum consumes them.
 template <int MODE>
@@ -280,9 +437,10 @@ __global__ __launch_bounds__(256) void rowgemm_reduce(RgArgs a) {
 // residual stream that the next in_proj normalises): one 1024-thread workgroup per row m
 // finishes the row as rowgemm_reduce does (a thread per column, its slice loads issued
 // together), keeps it in LDS, and writes nout[m, :] = Y[m, :] * g2 *
-// rsqrt(mean(Y[m, :]^2) + eps).
+// rsqrt(mean(Y[m, :]^2) + eps). FROMX: the row scale of the norm modes comes from X / Z (the
+// direct kernel) instead of the slices' sums of squares.
 constexpr int kNormCols = 8192;   // widest row the fused finish keeps in LDS
-template <int MODE>
+template <int MODE, bool FROMX>
 __global__ __launch_bounds__(1024) void rowgemm_reduce_norm(RgArgs a, const float* __restrict__ g2,
                                                            float* __restrict__ nout, long ldn) {
     __shared__ float row[kNormCols];
@@ -290,7 +448,10 @@ __global__ __launch_bounds__(1024) void rowgemm_reduce_norm(RgArgs a, const floa
     const int m = blockIdx.x, tid = threadIdx.x;
     const long MN = (long)a.M * a.N;
     float rs = 1.f;
-    if (MODE != MODE_PLAIN) {
+    if (MODE != MODE_PLAIN && FROMX) {
+        rs = row_scale<MODE, 1024>(a, m, part_ss);
+        __syncthreads();   // part_ss is reused below
+    } else if (MODE != MODE_PLAIN) {
         float tv[kMaxSplit];
 #pragma unroll
         for (int s = 0; s < kMaxSplit; ++s) tv[s] = s < a.S ? a.ssqp[(long)s * a.M + m] : 0.f;
@@ -328,15 +489,35 @@ __global__ __launch_bounds__(1024) void rowgemm_reduce_norm(RgArgs a, const floa
     for (int n = tid; n < a.N; n += 1024) om[n] = row[n] * r2 * g2[n];
 }
 
-// Splits of K for a shape: enough (column tile, slice) workgroups to fill the chip, each
-// slice a whole number of groups of four K blocks.
+// Splits of K for a shape: enough (column tile, slice) workgroups to fill the chip. The
+// direct-W kernel takes slices of 16 NU (NU in kDirectNU) with at most one workgroup per CU
+// (ntiles S <= kTargetWG, so no CU gets two while others idle); otherwise the LDS-staged kernel
+// splits into slices of whole groups of four K blocks.
 struct Split {
     int S, kslice, ntiles;
+    int NU;   // > 0: direct-W kernel with slices of 16 NU
 };
+
+constexpr int kDirectNU[] = {8, 16, 24};
 
 Split choose(int N, int K, bool can_split) {
     Split p{};
     p.ntiles = (int)ssm::cdiv(N, kTileN);
+    if (can_split && p.ntiles < kTargetWG) {
+        const int S = std::min(kMaxSplit, kTargetWG / p.ntiles);
+        const int need = (int)ssm::cdiv(K, 16 * S);
+        for (int nu : kDirectNU)
+            if (nu >= need) {
+                const int Sd = (int)ssm::cdiv(K, 16 * nu);
+                if (Sd >= 2) {
+                    p.S = Sd;
+                    p.NU = nu;
+                    p.kslice = 16 * nu;
+                    return p;
+                }
+                break;
+            }
+    }
     const int blocks = (int)ssm::cdiv(K, kKB);
     int S = 1;
     if (can_split && p.ntiles < kTargetWG) {
@@ -392,10 +573,21 @@ ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, lo
     // the next RMSNorm rides on the split finish when there is one and the row fits in LDS
     const bool fuse = g2 && nout && p.S > 1 && N <= kNormCols;
     if (fuse && normed) *normed = true;
-#define RG_LAUNCH(MD)                                                                       \
-    rowgemm_kernel<MD><<<grid, 256, 0, st>>>(a);                                            \
-    if (fuse) rowgemm_reduce_norm<MD><<<(unsigned)M, 1024, 0, st>>>(a, g2, nout, ldn);     \
-    else if (p.S > 1) rowgemm_reduce<MD><<<rgrid, 256, 0, st>>>(a)
+    // the direct-W kernel's finish computes the norm modes' row scale itself
+    const bool direct = p.S > 1 && p.NU > 0;
+    const dim3 dgrid((unsigned)cdiv(N, 256), (unsigned)M);
+#define RG_LAUNCH(MD)                                                                         \
+    if (direct) {                                                                             \
+        if (p.NU == 8) rowgemm_direct_kernel<MD, 8><<<grid, 256, 0, st>>>(a);                 \
+        else if (p.NU == 16) rowgemm_direct_kernel<MD, 16><<<grid, 256, 0, st>>>(a);          \
+        else rowgemm_direct_kernel<MD, 24><<<grid, 256, 0, st>>>(a);                          \
+        if (fuse) rowgemm_reduce_norm<MD, true><<<(unsigned)M, 1024, 0, st>>>(a, g2, nout, ldn); \
+        else rowgemm_direct_reduce<MD><<<dgrid, 256, 0, st>>>(a);                             \
+    } else {                                                                                  \
+        rowgemm_kernel<MD><<<grid, 256, 0, st>>>(a);                                          \
+        if (fuse) rowgemm_reduce_norm<MD, false><<<(unsigned)M, 1024, 0, st>>>(a, g2, nout, ldn); \
+        else if (p.S > 1) rowgemm_reduce<MD><<<rgrid, 256, 0, st>>>(a);                       \
+    }
     switch (mode) {
         case 0: RG_LAUNCH(MODE_PLAIN); break;
         case 1: RG_LAUNCH(MODE_RMS); break;

@@ -196,7 +196,7 @@ __device__ __forceinline__ V swap_pair(V v) {
     ssm::u32x4 u = __builtin_bit_cast(ssm::u32x4, v);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        u[i] = (unsigned)__builtin_amdgcn_update_dpp(0, (int)u[i], 0xB1, 0xf, 0xf, false);
+        u[i] = (unsigned)__builtin_amdgcn_mov_dpp((int)u[i], 0xB1, 0xf, 0xf, true);
     return __builtin_bit_cast(V, u);
 }
 
