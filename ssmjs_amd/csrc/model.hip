@@ -14,6 +14,7 @@
 // out_proj GEMM (beta = 1).
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -329,6 +330,22 @@ struct ssm_state {
     uint32_t* d_gen = nullptr;   // generation ids ring
     size_t gen_cap = 0;
     float* d_logits = nullptr;   // (B, V)
+    uint32_t* d_ping = nullptr;  // (2, B) ids of greedy generation steps
+    // Captured one-token steps: a step's kernels depend only on these pointers (the model's
+    // weights and workspaces, this state's buffers, the ids / logits / argmax arguments), so a
+    // step repeated with the same ones replays a HIP graph instead of launching ~5 kernels per
+    // layer one by one.
+    struct StepGraph {
+        const uint32_t* ids;
+        float* logits;
+        uint32_t* argmax;
+        const char* ws;
+        const char* rg;
+        hipGraphExec_t exec;
+        uint64_t used;
+    };
+    std::vector<StepGraph> graphs;
+    uint64_t graph_clock = 0;
     bool destroyed = false;
 };
 
@@ -1006,8 +1023,12 @@ extern "C" ssm_status ssm_state_destroy(ssm_state* s) {
     if (!s->m->destroyed && !s->m->ctx->destroyed) {
         hipSetDevice(s->m->ctx->device);
         hipStreamSynchronize(s->m->ctx->stream);
+        for (auto& g : s->graphs)
+            if (g.exec) hipGraphExecDestroy(g.exec);
         hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits); hipFree(s->d_gen);
+        hipFree(s->d_ping);
     }
+    s->graphs.clear();
     s->destroyed = true;
     return SSM_OK;
 }
@@ -1116,20 +1137,92 @@ extern "C" ssm_status ssm_prefill(ssm_model* m, ssm_state* s, const uint32_t* id
     return finish_host(m, s, last_logits, argmax, s->d_gen);
 }
 
-extern "C" ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const uint32_t* d_ids,
-                                             float* d_logits, uint32_t* d_argmax) {
-    SSM_TRY(state_enter(s));
-    SSM_REQUIRE(s->m == m && d_ids, "ssm_decode_step_device: bad args");
+namespace {
+
+ssm_status decode_body(ssm_model* m, ssm_state* s, const uint32_t* d_ids, float* lg,
+                       uint32_t* d_argmax) {
     const Dims& d = m->dm;
     Ws w;
     SSM_TRY(ensure_ws(m, s->B, 1, false, &w));
     SSM_TRY(trunk(m, d_ids, s->B, 1, s, w, false));
-    float* lg = d_logits ? d_logits : s->d_logits;
     { Stage g(m->ctx, "head");
       SSM_TRY(proj_rows(m, 1, w.hid, d.d, nullptr, 0, m->w + m->norm_f, m->w + m->emb, lg, d.V,
                         s->B, d.V, d.d, 0.f, w.nrm)); }
     if (d_argmax) SSM_TRY(ssm::launch_argmax(lg, d.V, s->B, d.V, d_argmax, m->ctx->stream));
     return SSM_OK;
+}
+
+// Graph replay of repeated steps: off under the stage profiler (its events would be
+// captured) and with SSM_DECODE_GRAPH=0.
+bool graphs_on(const ssm_ctx* c) {
+    if (c->prof) return false;
+    const char* e = std::getenv("SSM_DECODE_GRAPH");
+    return !(e && std::strcmp(e, "0") == 0);
+}
+
+constexpr size_t kMaxStepGraphs = 4;
+
+// The first step with a set of pointers runs eagerly (it also grows any workspace the step
+// needs, so none is allocated under capture); the second is captured and replayed, as are all
+// later ones. The least recently used graph makes room for a new set.
+ssm_status decode_graphed(ssm_model* m, ssm_state* s, const uint32_t* d_ids, float* lg,
+                          uint32_t* d_argmax) {
+    hipStream_t st = m->ctx->stream;
+    ssm_state::StepGraph* e = nullptr;
+    for (auto& g : s->graphs)
+        if (g.ids == d_ids && g.logits == lg && g.argmax == d_argmax) e = &g;
+    if (e && (e->ws != m->ws || e->rg != m->rg)) {   // a workspace moved: capture again
+        if (e->exec) SSM_HIP_TRY(hipGraphExecDestroy(e->exec));
+        e->exec = nullptr;
+        e->ws = m->ws;
+        e->rg = m->rg;
+        return decode_body(m, s, d_ids, lg, d_argmax);
+    }
+    if (e && e->exec) {
+        e->used = ++s->graph_clock;
+        SSM_HIP_TRY(hipGraphLaunch(e->exec, st));
+        return SSM_OK;
+    }
+    if (!e) {
+        SSM_TRY(decode_body(m, s, d_ids, lg, d_argmax));
+        if (s->graphs.size() >= kMaxStepGraphs) {
+            auto old = std::min_element(s->graphs.begin(), s->graphs.end(),
+                                        [](const auto& a, const auto& b) { return a.used < b.used; });
+            if (old->exec) SSM_HIP_TRY(hipGraphExecDestroy(old->exec));
+            s->graphs.erase(old);
+        }
+        s->graphs.push_back({d_ids, lg, d_argmax, m->ws, m->rg, nullptr, ++s->graph_clock});
+        return SSM_OK;
+    }
+    hipGraph_t g = nullptr;
+    SSM_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const ssm_status bs = decode_body(m, s, d_ids, lg, d_argmax);
+    const hipError_t ce = hipStreamEndCapture(st, &g);
+    if (bs != SSM_OK || ce != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return bs != SSM_OK ? bs : ssm::from_hip(ce, "decode step capture");
+    }
+    hipGraphExec_t x = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    SSM_HIP_TRY(ie);
+    e->exec = x;
+    e->ws = m->ws;
+    e->rg = m->rg;
+    e->used = ++s->graph_clock;
+    SSM_HIP_TRY(hipGraphLaunch(x, st));
+    return SSM_OK;
+}
+
+}  // namespace
+
+extern "C" ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const uint32_t* d_ids,
+                                             float* d_logits, uint32_t* d_argmax) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(s->m == m && d_ids, "ssm_decode_step_device: bad args");
+    float* lg = d_logits ? d_logits : s->d_logits;
+    if (!graphs_on(m->ctx)) return decode_body(m, s, d_ids, lg, d_argmax);
+    return decode_graphed(m, s, d_ids, lg, d_argmax);
 }
 
 extern "C" ssm_status ssm_decode_step(ssm_model* m, ssm_state* s, const uint32_t* ids,
@@ -1156,9 +1249,18 @@ extern "C" ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint
     hipStream_t st = m->ctx->stream;
     SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, prompt, T * 4, hipMemcpyHostToDevice, st));
     SSM_TRY(prefill_device(m, s, m->d_ids, Lp, s->d_gen));
-    for (int k = 1; k < n_new; ++k)
-        SSM_TRY(ssm_decode_step_device(m, s, s->d_gen + (size_t)(k - 1) * B, nullptr,
-                                       s->d_gen + (size_t)k * B));
+    // steps alternate between two id buffers (so they replay two captured graphs); each
+    // step's argmax is then copied into the generation ring
+    if (n_new > 1 && !s->d_ping) SSM_HIP_TRY(hipMalloc((void**)&s->d_ping, (size_t)2 * B * 4));
+    if (n_new > 1)
+        SSM_HIP_TRY(hipMemcpyAsync(s->d_ping, s->d_gen, (size_t)B * 4, hipMemcpyDeviceToDevice, st));
+    for (int k = 1; k < n_new; ++k) {
+        uint32_t* in = s->d_ping + (size_t)((k - 1) & 1) * B;
+        uint32_t* outp = s->d_ping + (size_t)(k & 1) * B;
+        SSM_TRY(ssm_decode_step_device(m, s, in, nullptr, outp));
+        SSM_HIP_TRY(hipMemcpyAsync(s->d_gen + (size_t)k * B, outp, (size_t)B * 4,
+                                   hipMemcpyDeviceToDevice, st));
+    }
     std::vector<uint32_t> tmp((size_t)n_new * B);
     SSM_HIP_TRY(hipMemcpyAsync(tmp.data(), s->d_gen, tmp.size() * 4, hipMemcpyDeviceToHost, st));
     SSM_TRY(check_flag(m));

@@ -121,6 +121,39 @@ def test_greedy_ids_bit_exact(device, layers, N):
     m.destroy()
 
 
+def test_decode_graph_replay_matches_eager(device, monkeypatch):
+    """Repeated one-token steps replay a captured HIP graph (from the second step with the same
+    buffers on). Every replayed step must give the same bits as eager launches from the same
+    state, also after another state with a larger batch has moved the shared workspaces (the
+    graph is then captured again)."""
+    case("decode graph replay vs eager")
+    m, _ = _model(device, ["mamba2", "mamba1", "mamba2"], N=64)
+    r = np.random.default_rng(7)
+    ids = r.integers(0, 512, (2, 10)).astype(np.uint32)
+    tmp = m.new_state(2)
+    img = (0.1 * r.standard_normal(tmp.read().size)).astype(np.float32)
+    tmp.destroy()
+    runs = {}
+    for mode in ("eager", "graph"):
+        monkeypatch.setenv("SSM_DECODE_GRAPH", "0" if mode == "eager" else "1")
+        st = m.new_state(2)
+        st.write(img)
+        out = []
+        for t in range(10):
+            if t == 5:
+                big = m.new_state(6)   # larger batch: the shared workspaces grow
+                big.decode(r.integers(0, 512, 6))
+                big.destroy()
+            lg, am = st.decode(ids[:, t])
+            out.append((lg.copy(), am.copy(), st.read()))
+        runs[mode] = out
+        st.destroy()
+    for t, (a, b) in enumerate(zip(runs["eager"], runs["graph"])):
+        for x, y in zip(a, b):
+            assert np.array_equal(x, y), f"step {t} differs"
+    m.destroy()
+
+
 def test_greedy_equals_reprefill(device):
     """generate() (recurrent) == tokenStream semantics (full re-prefill each step,
     src/session/streaming.ts:30-45) for topK = 1."""
