@@ -735,6 +735,9 @@ void plan(int B, int L, int H, int& nchunks, int& nseg, int& per) {
 // passes of RPP = 256 / LPR rows of one (b, h) state (LPR = N / 4 lanes per row, one float4
 // each), so the grid is B*H*ceil(P / (RPP*R)) workgroups of straight-line code, each thread
 // with R state loads in flight; y[p] = C . h[p,:] + D x[p] is reduced over the row's lanes.
+// The state goes through non-temporal loads and stores: it is touched once per step and not
+// again before the other layers' states have streamed through the caches, and keeping it out
+// of L2 and the MALL measured 13% faster (22.8 against 26.1 us at 64 x 32 x 64 x 128).
 template <int LPR, int R>
 __global__ __launch_bounds__(256) void m2_update_kernel(
     const float* __restrict__ x, long ldx, const float* __restrict__ dt, long lddt,
@@ -758,7 +761,9 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
     for (int k = 0; k < R; ++k) {
         const int p = p0 + k * RPP;
         if (p < Pd) {
-            v[k] = *(reinterpret_cast<const float4*>(hb + (long)p * N) + c4);
+            const float* src = hb + (long)p * N + 4 * c4;
+            v[k] = make_float4(__builtin_nontemporal_load(src), __builtin_nontemporal_load(src + 1),
+                               __builtin_nontemporal_load(src + 2), __builtin_nontemporal_load(src + 3));
             xp[k] = x[(long)b * ldx + (long)h * Pd + p];
         }
     }
@@ -779,7 +784,11 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
         u.y = fmaf(dA, u.y, dx * bv.y);
         u.z = fmaf(dA, u.z, dx * bv.z);
         u.w = fmaf(dA, u.w, dx * bv.w);
-        *(reinterpret_cast<float4*>(hb + (long)p * N) + c4) = u;
+        float* dst = hb + (long)p * N + 4 * c4;
+        __builtin_nontemporal_store(u.x, dst);
+        __builtin_nontemporal_store(u.y, dst + 1);
+        __builtin_nontemporal_store(u.z, dst + 2);
+        __builtin_nontemporal_store(u.w, dst + 3);
         float acc = u.x * cv.x + u.y * cv.y + u.z * cv.z + u.w * cv.w;
 #pragma unroll
         for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
