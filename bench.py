@@ -17,8 +17,10 @@ library launches on (torch's current stream, handed to the library context).
 
 The roofline object names the dominant kernel (stage) of the step, its algorithmic FLOPs or
 bytes per launch, and its average duration from HIP events recorded around it inside the
-library during a second, profiled pass of K steps. The cpu_baseline object times the CPU
-restatement (oracle/) single-threaded on a bounded slice of the same workload.
+library during a second, profiled pass of K steps (cfg4: the state update is timed on its own,
+back to back over the 24 layers' states, since the per-stage events of the profiled pass add
+their own overhead to a 25 us kernel). The cpu_baseline object times the CPU restatement
+(oracle/) single-threaded on a bounded slice of the same workload.
 """
 from __future__ import annotations
 
@@ -287,6 +289,49 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype):
     return out
 
 
+def time_state_update(torch, st, nl, B, H, P, N, reps):
+    """Average launch duration of the decode step's dominant kernel, the Mamba-2 state update
+    (ssm_m2_state_update), run on its own: each of the nl layer states in turn (so the states
+    stay HBM-resident, as they are in the step), launched back to back between HIP events on
+    the library's stream. Inputs are synthetic (B, H, P) / (B, N) rows."""
+    from ssmjs_amd import _lib
+    D = H * P
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(B, D, device="cuda", generator=g)
+    dt = torch.randn(B, H, device="cuda", generator=g) - 3.0
+    Bm = torch.randn(B, N, device="cuda", generator=g)
+    Cm = torch.randn(B, N, device="cuda", generator=g)
+    A = -(1.0 + 15.0 * torch.rand(H, device="cuda", generator=g))
+    Dk = torch.ones(H, device="cuda")
+    y = torch.empty(B, D, device="cuda")
+    hs = [st.layer_ptrs(l)[0] for l in range(nl)]
+
+    def launch(l, stream):
+        _lib.call("ssm_m2_state_update", x.data_ptr(), D, dt.data_ptr(), H, None, 1, 0.0,
+                  float("inf"), A.data_ptr(), Bm.data_ptr(), N, Cm.data_ptr(), N, Dk.data_ptr(),
+                  None, 0, y.data_ptr(), D, hs[l], B, H, P, 1, N, stream)
+
+    # all reps x nl launches as one graph, so they run back to back without waiting on the
+    # host (a Python launch takes about as long as the kernel) or between replays
+    s = torch.cuda.current_stream()
+    for l in range(nl):
+        launch(l, s.cuda_stream)
+    torch.cuda.synchronize()
+    g_ = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_):
+        cs = torch.cuda.current_stream().cuda_stream
+        for i in range(reps * nl):
+            launch(i % nl, cs)
+    g_.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    g_.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * nl)
+
+
 def w_cfg4(torch, np, dev, args):
     from ssmjs_amd import _lib, backend
     Bsz, d, nl, H, N, V = 64, 1024, 24, 32, 128, 32000
@@ -320,6 +365,9 @@ def w_cfg4(torch, np, dev, args):
         "m2.step.gated_norm": (None, 4.0 * Bsz * D * 3),
         "m2.step.out_proj": (2.0 * Bsz * D * d, 4.0 * (d * D + Bsz * (D + 2 * d))),
     }
+    # the state update, the dominant stage, is timed on its own (its stage time above carries
+    # the profiler's event overhead); its average matches the kernel trace's duration
+    stg["m2.step.state_update"] = (nl, time_state_update(torch, st, nl, Bsz, H, P, N, 8))
     stages = {}
     for kk, (nl_, avg) in stg.items():
         if kk in alg:
