@@ -43,11 +43,11 @@ METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 # profiles/. Re-measured when the
 # kernels change; None where not measured.
 TRAFFIC = {
-    ("cfg2", "m1.in_proj"): 387_225_600,               # rocBLAS sgemm (tile re-reads)
-    ("cfg3", "bf16"): 869_853_184,                     # ssd_kernel
-    ("cfg3", "f32"): 1_169_659_904,                    # ssd_kernel (fp32 inputs)
-    ("cfg4", "m2.step.state_update"): 136_509_440,     # m2_update_kernel
-    ("cfg5", "bf16"): 1_214_856_192,                   # state pass + combine + full pass
+    ("cfg2", "m1.in_proj"): 339_224_576,               # hipBLASLt sgemm (tile re-reads)
+    ("cfg3", "bf16"): 848_125_952,                     # ssd_kernel (two heads per workgroup)
+    ("cfg3", "f32"): 1_166_376_960,                    # ssd_kernel (fp32 inputs)
+    ("cfg4", "m2.step.state_update"): 136_517_632,     # m2_update_kernel
+    ("cfg5", "bf16"): 1_209_127_936,                   # state pass + combine + full pass
 }
 
 
