@@ -655,10 +655,11 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // y (M, N) [ld ldy] = beta*y + s * p(x) W^T (mode 1: RMSNorm with weight g; mode 2: gated
 // RMSNorm with z, one group): the few-row kernel (M <= 64) with the norm in its prologue
-// where it is the faster choice, otherwise the norm as its own kernel into `tmp` and rocBLAS.
-// Measured at 64 rows (cfg4): the gated out_proj (N 1024, K 2048) 13.6 us split over K vs
-// 16 us; the LM head (N 32000) 50 us vs 70 us for norm + rocBLAS; the in_proj (N 4384,
-// K 1024) 19.5 us split vs 18.6 us, so mode 1 below 16384 columns stays on rocBLAS.
+// where it is the faster choice, otherwise the norm as its own kernel into `tmp` and the
+// library GEMM (gemm()). Measured at 64 rows (cfg4): the gated out_proj (N 1024, K 2048)
+// 7.1 + 7.0 us split over K (the finish also writes the next layer's norm); the LM head
+// (N 32000) 49 us with the norm fused, 70 us for norm + rocBLAS, about 42 us for norm +
+// hipBLASLt; mode 1 below 16384 columns (in_proj) goes to the library GEMM.
 //
 // g2 / nout: when the few-row kernel's split finish can, it also writes nout = RMSNorm(y) * g2
 // (the next layer's normalised input) and sets *normed.
@@ -669,7 +670,9 @@ ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const flo
     if (normed) *normed = false;
     ssm_ctx* c = m->ctx;
     const Dims& d = m->dm;
-    const bool wanted = mode == 2 || (mode == 1 && N >= 16384);
+    // the LM head (RMS mode, wide N) takes RMSNorm + hipBLASLt when there is one (about 42
+    // against 49 us at 64 x 32000 x 1024); the gated out_proj always takes the row kernel
+    const bool wanted = mode == 2 || (mode == 1 && N >= 16384 && !c->lt);
     const bool fits = wanted && ssm::rowgemm_ok(M, N, K) && al16(x) && al16(W) && ldx % 4 == 0 &&
                       al16(g) && (mode != 2 || (al16(z) && ldz % 4 == 0 && d.G == 1));
     if (fits) {
