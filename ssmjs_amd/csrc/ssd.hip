@@ -702,9 +702,11 @@ ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
     if (a.nseg > 1) {
         // the state-only pass runs one head per workgroup: with no Y work its B tile is a
         // small share of the memory instructions, and independent workgroups overlap better
-        // than two heads in lockstep
+        // than two heads in lockstep. The last segment's local state is never combined
+        // (the full pass produces the final state), so only the first nseg - 1 segments run
+        // (the order is segment-major: they are the first B*H*(nseg-1) workgroups).
         SsdArgs s1 = a;
-        const int nwg1 = a.B * a.H * a.nseg;
+        const int nwg1 = a.B * a.H * (a.nseg - 1);
         s1.remap = (nwg1 % 8 == 0) ? 1 : 0;
         ssd_kernel<TIN, SPLIT, NN, false, 1><<<nwg1, 256, 0, st>>>(s1);
         ssm_status e = ssm::check_launch("ssd_state_pass");
