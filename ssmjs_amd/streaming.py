@@ -2,9 +2,10 @@
 
 token_stream re-runs model.forward over the whole sequence every step, exactly as the
 reference's tokenStream does (streaming.ts:30-41); HybridMambaModel.generate is the
-recurrent path. sample_token reproduces sampleToken step for step: float32 temperature
-scaling, a numerically stable softmax whose exponentials are computed in double and stored
-as float32, a stable descending sort of the exponentials, top-K, the nucleus cut at the first
+recurrent path. sample_token reproduces sampleToken step for step: temperature scaling in
+double stored as float32, a numerically stable softmax whose exponentials are computed in
+double and stored as float32 and summed in index order, a stable descending sort of the
+exponentials, top-K, the nucleus cut at the first
 cumulative probability >= topP, and an inverse-CDF draw. With topK = 1 the draw cannot
 change the result, so greedy decoding is deterministic.
 """
@@ -23,10 +24,12 @@ def sample_token(logits, temperature: float = 1.0, topK: int = 50, topP: float =
     """src/session/streaming.ts:53-97. `rng()` returns a float in [0, 1) (Math.random)."""
     lg = np.asarray(logits, dtype=np.float32)
     n = lg.shape[0]
-    scaled = (lg / np.float32(max(temperature, MIN_TEMPERATURE))).astype(np.float32)
+    # JS numbers are doubles: the division is in double, the Float32Array store rounds
+    scaled = (lg.astype(np.float64) / max(temperature, MIN_TEMPERATURE)).astype(np.float32)
     max_l = float(scaled.max()) if n else -math.inf
     exps = np.exp(scaled.astype(np.float64) - max_l).astype(np.float32)
-    sum_e = float(np.sum(exps.astype(np.float64)))
+    # sumE += exps[i] in index order (a cumulative sum is sequential; np.sum is pairwise)
+    sum_e = float(np.cumsum(exps.astype(np.float64))[-1]) if n else 0.0
     # Array.prototype.sort is stable: equal exps keep ascending index order
     order = np.argsort(-exps.astype(np.float64), kind="stable")
     top = order[: max(int(topK), 0)]

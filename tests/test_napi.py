@@ -64,6 +64,27 @@ def test_js_sample_token_matches_python():
     assert js == py
 
 
+@needs_addon
+def test_js_sample_token_matches_python_random():
+    """Random logits and temperatures that float32 cannot hold (the division happens in JS
+    doubles): the Python restatement picks what the JS sampleToken picks."""
+    from ssmjs_amd import sampleToken
+    r = np.random.default_rng(5)
+    lgs = [(3.0 * r.standard_normal(700)).astype(np.float32).tolist() for _ in range(4)]
+    cases = [(0.7, 50, 0.9), (1.3, 200, 0.95), (0.8, 50, 0.9), (0.33, 7, 0.5)]
+    us = r.random(6).tolist()
+    code = ("const m = require('./ssmjs_amd/napi'); const L = %s; const C = %s; const U = %s;"
+            "const out = []; for (const l of L) { const lg = Float32Array.from(l);"
+            " for (const c of C) for (const u of U) out.push(m.sampleToken(lg, c[0], c[1], c[2], () => u)); }"
+            "console.log(JSON.stringify(out))" % (json.dumps(lgs), json.dumps(cases), json.dumps(us)))
+    res = _node(code)
+    assert res.returncode == 0, res.stderr
+    js = json.loads(res.stdout)
+    py = [sampleToken(np.array(l, np.float32), t, k, p, rng=lambda u_=u_: u_)
+          for l in lgs for t, k, p in cases for u_ in us]
+    assert js == py
+
+
 @pytest.mark.gpu
 @needs_addon
 def test_node_session_path_matches_oracle(tmp_path):
