@@ -183,6 +183,18 @@ ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const float* z, l
  * row). x (rows, n) with row stride ldx; out (rows) uint32. */
 ssm_status ssm_argmax(const float* x, long ldx, int rows, int n, uint32_t* out, void* stream);
 
+/* sampleToken(logits, {temperature, topK, topP}) per row (src/session/streaming.ts:53-97),
+ * with the uniform draw Math.random() (streaming.ts:91) passed in: u (rows) doubles in
+ * [0, 1), device. logits (rows, n) fp32 with row stride ld; out (rows) uint32, device.
+ * Temperature is clamped to >= 1e-7 (streaming.ts:11,61); the division and exp are in
+ * double with float stores; the topK largest exps are taken in a stable descending order
+ * (equal exps: lower index first); the nucleus ends at the first cumulative exp/sumE >=
+ * topP; the pick is the first nucleus entry whose running exp sum reaches u * (nucleus
+ * sum). Needs 1 <= n <= 32768 and min(topK, n) <= 1024 (SSM_ERR_UNSUPPORTED otherwise) and
+ * topK >= 1. Logits must be finite. */
+ssm_status ssm_sample(const float* logits, long ld, int rows, int n, double temperature,
+                      int top_k, double top_p, const double* u, uint32_t* out, void* stream);
+
 /* ------------------------------------------------------------------ model level */
 #define SSM_LAYER_MAMBA1 1
 #define SSM_LAYER_MAMBA2 2
@@ -249,9 +261,19 @@ ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const uint32_t* d_
                                   float* d_logits, uint32_t* d_argmax);
 /* Greedy generation (topK = 1 in sampleToken, streaming.ts:74-75: argmax, lowest index on
  * ties): prefill prompt (B,Lp), then n_new recurrent steps with on-device argmax. out_ids
- * (B,n_new) host. Stops early for all rows only when every row has emitted eos_id. */
+ * (B,n_new) host. All n_new steps run; the caller cuts each row after its eos id
+ * (streaming.ts:47). */
 ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint32_t* prompt, int Lp,
                                int n_new, uint32_t* out_ids);
+/* Sampled generation (the generate loop of streaming.ts:17-49 with sampleToken on the
+ * device, as ssm_sample): prefill prompt (B,Lp) (host), then n_new - 1 recurrent steps;
+ * token k of row b is drawn with u_host[k*B + b] (host, n_new*B doubles in [0, 1), the
+ * Math.random() values of streaming.ts:91 in the order the reference draws them). out_ids
+ * (B,n_new) host. All n_new steps run; the caller cuts each row after its eos id. Same
+ * limits as ssm_sample on the vocabulary size and topK. */
+ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint32_t* prompt, int Lp,
+                               int n_new, double temperature, int top_k, double top_p,
+                               const double* u_host, uint32_t* out_ids);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,8 @@ def _declare(L):
     L.orc_linear.argtypes = [_fp, C.c_long, _fp, _fp, _fp, C.c_long, C.c_int, C.c_int, C.c_int,
                              C.c_int]
     L.orc_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_int, C.c_float]
+    L.orc_sample_token.argtypes = [_fp, C.c_int, C.c_double, C.c_int, C.c_double, C.c_double]
+    L.orc_sample_token.restype = C.c_int
     L.orc_gated_rmsnorm.argtypes = [_fp, C.c_long, _fp, C.c_long, _fp, _fp, C.c_long, C.c_int,
                                     C.c_int, C.c_int, C.c_float]
     L.orc_model_open.argtypes = [C.c_void_p, C.c_size_t, C.c_char_p, C.c_int]
@@ -175,6 +177,16 @@ def linear(x, W, bias=None):
     y = np.empty((M, W.shape[0]), np.float32)
     lib().orc_linear(_f(x), K, _f(W), _f(bias), _f(y), W.shape[0], M, K, W.shape[0], 0)
     return y
+
+
+def sample_token(logits, temperature, topK, topP, u) -> int:
+    """sampleToken (src/session/streaming.ts:53-97) on one row with Math.random() = u."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    r = lib().orc_sample_token(_f(lg), lg.size, float(temperature), int(topK), float(topP),
+                               float(u))
+    if r < 0:
+        raise ValueError("sample_token: needs n >= 1 and topK >= 1")
+    return r
 
 
 def rmsnorm(x, w, eps=1e-5):

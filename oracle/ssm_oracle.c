@@ -302,6 +302,64 @@ void orc_gated_rmsnorm(const float* x, long ldx, const float* z, long ldz, const
     free(v);
 }
 
+/* ------------------------------------------------------------ sampleToken */
+
+typedef struct {
+    float e;
+    int idx;
+} orc_entry;
+
+/* Array.prototype.sort with (a, b) => exps[b] - exps[a] is stable: descending e, and equal e
+ * keep ascending index order (streaming.ts:74-75). */
+static int entry_cmp(const void* pa, const void* pb) {
+    const orc_entry* a = (const orc_entry*)pa;
+    const orc_entry* b = (const orc_entry*)pb;
+    if (a->e != b->e) return a->e > b->e ? -1 : 1;
+    return a->idx < b->idx ? -1 : (a->idx > b->idx);
+}
+
+int orc_sample_token(const float* logits, int n, double temperature, int topK, double topP,
+                     double u) {
+    if (n < 1 || topK < 1) return -1;
+    const double t = temperature > 1e-7 ? temperature : 1e-7;   /* streaming.ts:11,61 */
+    float* scaled = (float*)malloc((size_t)n * sizeof(float));
+    orc_entry* ent = (orc_entry*)malloc((size_t)n * sizeof(orc_entry));
+    for (int i = 0; i < n; ++i) scaled[i] = (float)((double)logits[i] / t);   /* :60-61 */
+    float maxL = -INFINITY;                                                     /* :64-65 */
+    for (int i = 0; i < n; ++i)
+        if (scaled[i] > maxL) maxL = scaled[i];
+    double sumE = 0.0;                                                          /* :66-71 */
+    for (int i = 0; i < n; ++i) {
+        ent[i].e = (float)exp((double)scaled[i] - (double)maxL);
+        ent[i].idx = i;
+        sumE += (double)ent[i].e;
+    }
+    qsort(ent, (size_t)n, sizeof(orc_entry), entry_cmp);                       /* :74-76 */
+    const int K = topK < n ? topK : n;
+    double cum = 0.0;                                                           /* :79-85 */
+    int m = 0;
+    for (int k = 0; k < K; ++k) {
+        cum += (double)ent[k].e / sumE;
+        m = k + 1;
+        if (cum >= topP) break;
+    }
+    double nsum = 0.0;                                                          /* :88-89 */
+    for (int k = 0; k < m; ++k) nsum += (double)ent[k].e;
+    const double thr = u * nsum;                                                /* :90 */
+    double acc = 0.0;
+    int pick = ent[m - 1].idx;                                                  /* :96 */
+    for (int k = 0; k < m; ++k) {                                               /* :91-95 */
+        acc += (double)ent[k].e;
+        if (acc >= thr) {
+            pick = ent[k].idx;
+            break;
+        }
+    }
+    free(scaled);
+    free(ent);
+    return pick;
+}
+
 /* ------------------------------------------------------------ model */
 
 enum { LT_MAMBA1 = 1, LT_MAMBA2 = 2 };

@@ -93,6 +93,15 @@ void orc_rmsnorm(const float* x, const float* w, float* y, int M, int n, float e
 void orc_gated_rmsnorm(const float* x, long ldx, const float* z, long ldz, const float* w,
                        float* y, long ldy, int M, int n, int G, float eps);
 
+/* sampleToken (src/session/streaming.ts:53-97) with Math.random() = u: scaled = float(logit /
+ * max(T, 1e-7)); e = float(exp(scaled - max scaled)) (double arithmetic, float stores);
+ * sumE = sum of e in index order; the topK largest e in a stable descending order; nucleus =
+ * that list up to the first cumulative e/sumE >= topP; returns the first nucleus index whose
+ * running e sum reaches u * (nucleus sum), else the nucleus's last index. -1 if topK < 1 or
+ * n < 1 (the reference then returns undefined). */
+int orc_sample_token(const float* logits, int n, double temperature, int topK, double topP,
+                     double u);
+
 /* ---- model level: weights in the ssmjs_amd checkpoint format (magic "SSMW") ---- */
 typedef struct orc_model orc_model;
 

@@ -68,6 +68,7 @@ _fp = C.c_void_p   # device float* passed as integers / c_void_p
 _l = C.c_long
 _i = C.c_int
 _f = C.c_float
+_d = C.c_double
 _sz = C.c_size_t
 
 # name -> (restype, argtypes). Keep in the order of include/ssm_hip.h.
@@ -105,6 +106,7 @@ PROTOTYPES = {
     "ssm_linear_rows": (_i, [_i, _fp, _l, _fp, _l, _fp, _fp, _fp, _l, _i, _i, _i, _f, _f, _vp, _sz,
                              _vp]),
     "ssm_argmax": (_i, [_fp, _l, _i, _i, _vp, _vp]),
+    "ssm_sample": (_i, [_fp, _l, _i, _i, _d, _i, _d, _vp, _vp, _vp]),
     "ssm_model_create": (_i, [_vp, C.POINTER(ssm_config), C.c_uint64, C.POINTER(_vp)]),
     "ssm_model_destroy": (_i, [_vp]),
     "ssm_model_config": (_i, [_vp, C.POINTER(ssm_config)]),
@@ -124,6 +126,7 @@ PROTOTYPES = {
     "ssm_decode_step": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "ssm_decode_step_device": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "ssm_generate_greedy": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "ssm_generate_sample": (_i, [_vp, _vp, _vp, _i, _i, _d, _i, _d, _vp, _vp]),
 }
 
 _lib = None

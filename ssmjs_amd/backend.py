@@ -14,6 +14,12 @@ import numpy as np
 from . import _lib
 
 
+def sample_supported(n: int, topK: int) -> bool:
+    """Whether the device sampler (ssm_sample / ssm_generate_sample) takes a row of n logits
+    with this topK: n <= 32768 and min(topK, n) <= 1024."""
+    return 1 <= n <= 32768 and topK >= 1 and min(topK, n) <= 1024
+
+
 def _ptr(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
@@ -183,4 +189,17 @@ class State:
         out = np.empty((self.B, n_new), np.uint32)
         _lib.call("ssm_generate_greedy", self.model.handle, self._h, _ptr(prompt),
                   prompt.shape[1], n_new, _ptr(out))
+        return out
+
+    def generate_sample(self, prompt, n_new: int, temperature: float, topK: int, topP: float,
+                        u) -> np.ndarray:
+        """ssm_generate_sample: u (n_new, B) float64 draws, token k of row b uses u[k, b]."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        if prompt.ndim == 1:
+            prompt = prompt[None]
+        u = np.ascontiguousarray(u, dtype=np.float64).reshape(n_new, self.B)
+        out = np.empty((self.B, n_new), np.uint32)
+        _lib.call("ssm_generate_sample", self.model.handle, self._h, _ptr(prompt),
+                  prompt.shape[1], n_new, float(temperature), int(topK), float(topP), _ptr(u),
+                  _ptr(out))
         return out

@@ -412,7 +412,9 @@ struct ssm_state {
     uint32_t* d_gen = nullptr;   // generation ids ring
     size_t gen_cap = 0;
     float* d_logits = nullptr;   // (B, V)
-    uint32_t* d_ping = nullptr;  // (2, B) ids of greedy generation steps
+    uint32_t* d_ping = nullptr;  // (2, B) ids of generation steps
+    double* d_u = nullptr;       // (n_new, B) uniform draws of sampled generation
+    size_t u_cap = 0;
     // Captured one-token steps: a step's kernels depend only on these pointers (the model's
     // weights and workspaces, this state's buffers, the ids / logits / argmax arguments), so a
     // step repeated with the same ones replays a HIP graph instead of launching ~5 kernels per
@@ -1111,7 +1113,7 @@ extern "C" ssm_status ssm_state_destroy(ssm_state* s) {
         for (auto& g : s->graphs)
             if (g.exec) hipGraphExecDestroy(g.exec);
         hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits); hipFree(s->d_gen);
-        hipFree(s->d_ping);
+        hipFree(s->d_ping); hipFree(s->d_u);
     }
     s->graphs.clear();
     s->destroyed = true;
@@ -1321,6 +1323,22 @@ extern "C" ssm_status ssm_decode_step(ssm_model* m, ssm_state* s, const uint32_t
     return finish_host(m, s, logits, argmax, s->d_gen);
 }
 
+namespace {
+
+// Generation ring (n_new, B) on the device -> out_ids (B, n_new) on the host.
+ssm_status gen_to_host(ssm_model* m, ssm_state* s, int n_new, uint32_t* out_ids) {
+    const int B = s->B;
+    std::vector<uint32_t> tmp((size_t)n_new * B);
+    SSM_HIP_TRY(hipMemcpyAsync(tmp.data(), s->d_gen, tmp.size() * 4, hipMemcpyDeviceToHost,
+                               m->ctx->stream));
+    SSM_TRY(check_flag(m));
+    for (int b = 0; b < B; ++b)
+        for (int k = 0; k < n_new; ++k) out_ids[(size_t)b * n_new + k] = tmp[(size_t)k * B + b];
+    return SSM_OK;
+}
+
+}  // namespace
+
 extern "C" ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint32_t* prompt,
                                           int Lp, int n_new, uint32_t* out_ids) {
     SSM_TRY(state_enter(s));
@@ -1346,10 +1364,56 @@ extern "C" ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint
         SSM_HIP_TRY(hipMemcpyAsync(s->d_gen + (size_t)k * B, outp, (size_t)B * 4,
                                    hipMemcpyDeviceToDevice, st));
     }
-    std::vector<uint32_t> tmp((size_t)n_new * B);
-    SSM_HIP_TRY(hipMemcpyAsync(tmp.data(), s->d_gen, tmp.size() * 4, hipMemcpyDeviceToHost, st));
-    SSM_TRY(check_flag(m));
-    for (int b = 0; b < B; ++b)
-        for (int k = 0; k < n_new; ++k) out_ids[(size_t)b * n_new + k] = tmp[(size_t)k * B + b];
-    return SSM_OK;
+    return gen_to_host(m, s, n_new, out_ids);
+}
+
+extern "C" ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint32_t* prompt,
+                                          int Lp, int n_new, double temperature, int top_k,
+                                          double top_p, const double* u_host,
+                                          uint32_t* out_ids) {
+    SSM_TRY(state_enter(s));
+    SSM_REQUIRE(s->m == m && prompt && Lp > 0 && n_new >= 0 &&
+                    ((out_ids && u_host) || n_new == 0),
+                "ssm_generate_sample: bad args");
+    SSM_REQUIRE(top_k >= 1, "ssm_generate_sample: topK must be at least 1");
+    if (!ssm::sample_ok(m->dm.V, top_k))
+        return ssm::fail(SSM_ERR_UNSUPPORTED,
+                         "ssm_generate_sample: vocabulary %d / topK %d beyond the device sampler",
+                         m->dm.V, top_k);
+    if (n_new == 0) return SSM_OK;
+    const int B = s->B;
+    const int V = m->dm.V;
+    const size_t T = (size_t)B * Lp;
+    const size_t nu = (size_t)n_new * B;
+    SSM_TRY(ensure_ids(m, T));
+    SSM_TRY(ensure_gen(s, nu));
+    hipStream_t st = m->ctx->stream;
+    if (nu > s->u_cap) {
+        SSM_HIP_TRY(hipStreamSynchronize(st));
+        if (s->d_u) SSM_HIP_TRY(hipFree(s->d_u));
+        s->d_u = nullptr;
+        SSM_HIP_TRY(hipMalloc((void**)&s->d_u, nu * sizeof(double)));
+        s->u_cap = nu;
+    }
+    SSM_HIP_TRY(hipMemcpyAsync(s->d_u, u_host, nu * sizeof(double), hipMemcpyHostToDevice, st));
+    SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, prompt, T * 4, hipMemcpyHostToDevice, st));
+    SSM_TRY(prefill_device(m, s, m->d_ids, Lp, nullptr));
+    SSM_TRY(ssm::launch_sample(s->d_logits, V, B, V, temperature, top_k, top_p, s->d_u,
+                               s->d_gen, st));
+    // as in greedy generation, steps alternate between two id buffers so that they replay
+    // two captured graphs; the sampler runs after each step, outside the graph (its draws
+    // change every step)
+    if (n_new > 1 && !s->d_ping) SSM_HIP_TRY(hipMalloc((void**)&s->d_ping, (size_t)2 * B * 4));
+    if (n_new > 1)
+        SSM_HIP_TRY(hipMemcpyAsync(s->d_ping, s->d_gen, (size_t)B * 4, hipMemcpyDeviceToDevice, st));
+    for (int k = 1; k < n_new; ++k) {
+        uint32_t* in = s->d_ping + (size_t)((k - 1) & 1) * B;
+        uint32_t* outp = s->d_ping + (size_t)(k & 1) * B;
+        SSM_TRY(ssm_decode_step_device(m, s, in, nullptr, nullptr));
+        SSM_TRY(ssm::launch_sample(s->d_logits, V, B, V, temperature, top_k, top_p,
+                                   s->d_u + (size_t)k * B, outp, st));
+        SSM_HIP_TRY(hipMemcpyAsync(s->d_gen + (size_t)k * B, outp, (size_t)B * 4,
+                                   hipMemcpyDeviceToDevice, st));
+    }
+    return gen_to_host(m, s, n_new, out_ids);
 }

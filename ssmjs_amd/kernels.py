@@ -14,6 +14,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .backend import sample_supported  # noqa: F401  (re-export)
 
 _NULL = None
 
@@ -148,6 +149,19 @@ def argmax(x, out=None):
     rows, n = x.shape
     o = out if out is not None else torch.empty(rows, dtype=torch.int32, device=x.device)
     _lib.call("ssm_argmax", _p(x), x.stride(0), rows, n, _p(o), _stream())
+    return o
+
+
+def sample(x, u, temperature=1.0, topK=50, topP=0.9, out=None):
+    """sampleToken per row on the device (ssm_sample, src/session/streaming.ts:53-97).
+
+    x: (rows, n) fp32 logits; u: (rows,) float64 draws in [0, 1) (Math.random()). Returns
+    (rows,) int32 picks. Raises for n > 32768 or min(topK, n) > 1024."""
+    rows, n = x.shape
+    assert u.dtype == torch.float64 and u.numel() == rows and u.is_contiguous()
+    o = out if out is not None else torch.empty(rows, dtype=torch.int32, device=x.device)
+    _lib.call("ssm_sample", _p(x), x.stride(0), rows, n, float(temperature), int(topK),
+              float(topP), _p(u), _p(o), _stream())
     return o
 
 

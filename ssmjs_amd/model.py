@@ -17,6 +17,7 @@ Every numeric path runs in libssm_hip.so; there is no CPU fallback.
 from __future__ import annotations
 
 import math
+import random
 
 import numpy as np
 
@@ -92,10 +93,24 @@ class HybridMambaModel:
         eos = self.config.get("eosId", -1)
         st = self._m.new_state(1)
         try:
-            if topK == 1:
-                # sampleToken with topK = 1 is the stable argmax of the logits; the device
-                # argmax keeps the lowest index among equal maxima
+            if backend.sample_supported(self.config["vocabSize"], topK):
+                # sampleToken on the device (topK = 1 included: its pick is the lowest index
+                # among f32 exps equal to the largest, which an argmax of the logits misses
+                # when two exps round alike). The draws are taken from rng up front, one per
+                # step in the reference's order (streaming.ts:91), so the tokens up to eos
+                # are those of the host loop below with the same rng; rng is then advanced
+                # max_new_tokens times even when eos comes earlier.
+                draw = rng or random.random
+                u = np.array([draw() for _ in range(max_new_tokens)], np.float64)
+                out = st.generate_sample(np.array([ids], np.uint32), max_new_tokens,
+                                         temperature, topK, topP, u[:, None])[0].tolist()
+            elif topK == 1:
+                # vocabularies beyond the device sampler: device argmax of the logits (lowest
+                # index among equal maxima)
                 out = st.generate_greedy(np.array([ids], np.uint32), max_new_tokens)[0].tolist()
+            else:
+                out = None
+            if out is not None:
                 for t in out:
                     ids.append(int(t))
                     if t == eos:

@@ -146,17 +146,28 @@ class HybridMambaModel {
       const st = a.stateCreate(h, 1);
       const done = (r) => { a.stateDestroy(st); return r; };
       const fail = (e) => { a.stateDestroy(st); throw e; };
+      const keep = (out) => {
+        for (const t of out) {
+          ids.push(t);
+          if (t === eos) break;
+        }
+        return ids;
+      };
+      const V = this.config.vocabSize;
+      if (topK >= 1 && V <= 32768 && Math.min(topK, V) <= 1024) {
+        // sampleToken on the device (ssm_generate_sample), topK 1 included: one draw per
+        // step, taken up front in the order the host loop below takes them
+        const draw = rng || Math.random;
+        const u = new Float64Array(maxNewTokens);
+        for (let k = 0; k < maxNewTokens; k++) u[k] = draw();
+        return a.generateSample(h, st, Uint32Array.from(ids), ids.length, maxNewTokens,
+                                temperature, topK, topP, u).then(keep).then(done, fail);
+      }
       if (topK === 1) {
-        // sampleToken with topK 1 is the stable argmax; the device argmax keeps the lowest
-        // index among equal maxima
+        // beyond the device sampler: device argmax of the logits (lowest index among equal
+        // maxima)
         return a.generateGreedy(h, st, Uint32Array.from(ids), ids.length, maxNewTokens)
-          .then((out) => {
-            for (const t of out) {
-              ids.push(t);
-              if (t === eos) break;
-            }
-            return ids;
-          }).then(done, fail);
+          .then(keep).then(done, fail);
       }
       const step = (logits, k) => {
         const nxt = sampleToken(logits, temperature, topK, topP, rng);

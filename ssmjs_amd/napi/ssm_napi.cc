@@ -84,6 +84,12 @@ int get_int(napi_env env, napi_value v, bool* ok) {
     return x;
 }
 
+double get_double(napi_env env, napi_value v, bool* ok) {
+    double x = 0.0;
+    if (napi_get_value_double(env, v, &x) != napi_ok) *ok = false;
+    return x;
+}
+
 // Copy the bytes of an ArrayBuffer, a TypedArray or a DataView.
 bool copy_bytes(napi_env env, napi_value v, std::vector<uint8_t>& out) {
     bool is = false;
@@ -483,6 +489,50 @@ napi_value GenerateGreedy(napi_env env, napi_callback_info info) {
     return queue(env, j, "ssm_generate_greedy");
 }
 
+// generateSample(model, state, prompt (batch*Lp), Lp, nNew, temperature, topK, topP,
+//                u Float64Array (nNew*batch)) -> Promise<Uint32Array (batch*nNew)>
+// u holds the Math.random() draws, token k of sequence b taking u[k*batch + b].
+napi_value GenerateSample(napi_env env, napi_callback_info info) {
+    napi_value argv[9];
+    if (!get_args(env, info, 9, argv)) return nullptr;
+    Model* m = unwrap<Model>(env, argv[0]);
+    State* s = unwrap<State>(env, argv[1]);
+    if (!m || !s) return nullptr;
+    bool ok = true;
+    const int Lp = get_int(env, argv[3], &ok), n = get_int(env, argv[4], &ok);
+    const double temperature = get_double(env, argv[5], &ok);
+    const int top_k = get_int(env, argv[6], &ok);
+    const double top_p = get_double(env, argv[7], &ok);
+    auto ids = std::make_shared<std::vector<uint32_t>>();
+    if (!copy_ids(env, argv[2], *ids)) return nullptr;
+    if (!ok || Lp <= 0 || n < 0 || (size_t)s->batch * Lp != ids->size()) {
+        napi_throw(env, make_error(env, "UNKNOWN", "generateSample: prompt.length must equal batch * Lp"));
+        return nullptr;
+    }
+    auto u = std::make_shared<std::vector<double>>();
+    {
+        bool is = false;
+        napi_is_typedarray(env, argv[8], &is);
+        napi_typedarray_type tt;
+        size_t len = 0;
+        void* data = nullptr;
+        if (is) napi_get_typedarray_info(env, argv[8], &tt, &len, &data, nullptr, nullptr);
+        if (!is || tt != napi_float64_array || len != (size_t)n * s->batch) {
+            napi_throw(env, make_error(env, "UNKNOWN", "generateSample: u must be a Float64Array of nNew * batch draws"));
+            return nullptr;
+        }
+        u->assign((const double*)data, (const double*)data + len);
+    }
+    auto out = std::make_shared<std::vector<uint32_t>>((size_t)s->batch * n);
+    Job* j = new Job();
+    j->run = [m, s, ids, u, out, Lp, n, temperature, top_k, top_p]() {
+        return ssm_generate_sample(m->m, s->s, ids->data(), Lp, n, temperature, top_k, top_p,
+                                   u->data(), out->data());
+    };
+    j->done = [out](napi_env e) { return typed_from<uint32_t, napi_uint32_array>(e, *out); };
+    return queue(env, j, "ssm_generate_sample");
+}
+
 napi_value Init(napi_env env, napi_value exports) {
     const struct { const char* name; napi_callback fn; } fns[] = {
         {"version", Version},         {"ctxCreate", CtxCreate},       {"ctxDestroy", CtxDestroy},
@@ -490,6 +540,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"loadWeights", LoadWeights}, {"exportWeights", ExportWeights}, {"forward", Forward},
         {"stateCreate", StateCreate}, {"stateDestroy", StateDestroy}, {"prefill", Prefill},
         {"decodeStep", DecodeStep},   {"generateGreedy", GenerateGreedy},
+        {"generateSample", GenerateSample},
     };
     for (const auto& f : fns) {
         napi_value v;

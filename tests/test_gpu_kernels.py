@@ -377,6 +377,66 @@ def test_argmax_ties_nan_and_tails(n, pad):
     assert got.tolist() == [int(np.argmax(x[0])), n // 3, n - 1, 0, 0, n // 2]
 
 
+def _sample_rows(r, rows, n):
+    """Logit rows of several kinds: heavy exact ties, near-ties (small scale: rounded exps
+    collide), wide spread, and one constant row."""
+    x = np.empty((rows, n), np.float32)
+    for i in range(rows):
+        k = i % 4
+        if k == 0:
+            x[i] = r.integers(-3, 3, n) * 0.5
+        elif k == 1:
+            x[i] = r.standard_normal(n) * 0.02
+        elif k == 2:
+            x[i] = r.standard_normal(n) * 3.0
+        else:
+            x[i] = r.standard_normal(n)
+    x[rows - 1] = 0.25
+    return x
+
+
+@pytest.mark.parametrize("n,pad", [(1, 0), (2, 1), (700, 3), (1500, 0), (32000, 0),
+                                   (32768, 0)])
+def test_sample_matches_oracle(n, pad):
+    """sampleToken on the device (ssm_sample) picks exactly the index the restatement of
+    src/session/streaming.ts:53-97 picks, for the same draw u, over temperatures (including
+    the 1e-7 floor), topK (1, ties at the K-th value, K >= n, the 1024 maximum) and topP."""
+    case(f"sample n={n} pad={pad}")
+    r = rng(80 + n)
+    rows = 12
+    xb = np.zeros((rows, n + pad), np.float32)
+    xb[:, :n] = _sample_rows(r, rows, n)
+    x = dev(xb)[:, :n]
+    params = [(1.0, 50, 0.9), (0.8, 1, 0.9), (2.5, 1024, 1.0), (1e-9, 7, 0.5),
+              (1.0, n + 3, 0.95), (0.7, 2, 0.0)]
+    for T, Kk, P in params:
+        if min(Kk, n) > 1024:
+            continue
+        u = r.random(rows)
+        u[0], u[1] = 0.0, 0.9999999999
+        got = K().sample(x, torch.from_numpy(u).to("cuda"), T, Kk, P)
+        torch.cuda.synchronize()
+        got = got.cpu().numpy().astype(np.int64)
+        want = [O.sample_token(xb[i, :n], T, Kk, P, u[i]) for i in range(rows)]
+        assert got.tolist() == want, (T, Kk, P)
+
+
+def test_sample_limits():
+    """Shapes beyond the device sampler are refused (SSM_ERR_UNSUPPORTED), not truncated."""
+    case("sample limits")
+    from ssmjs_amd._lib import SsmError
+    u = torch.zeros(1, dtype=torch.float64, device="cuda")
+    with pytest.raises(SsmError):
+        K().sample(torch.zeros(1, 32769, device="cuda"), u, 1.0, 50, 0.9)
+    with pytest.raises(SsmError):
+        K().sample(torch.zeros(1, 2048, device="cuda"), u, 1.0, 1025, 0.9)
+    with pytest.raises(SsmError):
+        K().sample(torch.zeros(1, 16, device="cuda"), u, 1.0, 0, 0.9)
+    # topK above the cap is fine when the row is shorter than the cap
+    got = K().sample(torch.zeros(1, 16, device="cuda"), u, 1.0, 5000, 0.9)
+    assert int(got.cpu()[0]) == 0
+
+
 def test_m2_state_update_decode_shape():
     """Config-4 shape (64 sequences x 32 heads): the row-split grid (8192 workgroups of two
     rows per thread) over the full (B, H, P, N) state."""

@@ -202,3 +202,64 @@ def test_unsupported_layer_types(device):
                "expand": 2, "nHeads": 4, "layers": [{"type": t}]}
         with pytest.raises(_lib.SsmError):
             backend.Model(device, cfg)
+
+
+@pytest.mark.parametrize("T,topK,topP", [(0.8, 50, 0.9), (1.3, 1024, 1.0), (0.8, 1, 0.9),
+                                         (1.0, 3, 0.5)])
+def test_sampled_generation_matches_oracle_sampler(device, T, topK, topP):
+    """ssm_generate_sample (prefill, then per token one recurrent step and sampleToken on the
+    device) picks, row by row, what the oracle's sampleToken (streaming.ts:53-97) picks on
+    the same device logits with the same draws."""
+    case(f"generate_sample T={T} topK={topK} topP={topP}")
+    m, _ = _model(device, ["mamba2", "mamba1"], N=64, emb_scale=4.0)
+    r = np.random.default_rng(21)
+    B, Lp, n_new = 3, 9, 16
+    prompt = r.integers(0, 512, (B, Lp)).astype(np.uint32)
+    u = r.random((n_new, B))
+    u[0, 0], u[1, 1] = 0.0, 0.9999999999
+    st = m.new_state(B)
+    got = st.generate_sample(prompt, n_new, T, topK, topP, u)
+    st.destroy()
+    st = m.new_state(B)
+    lg, _ = st.prefill(prompt)
+    want = np.zeros((B, n_new), np.uint32)
+    for k in range(n_new):
+        for b in range(B):
+            want[b, k] = O.sample_token(lg[b], T, topK, topP, u[k, b])
+        if k + 1 < n_new:
+            lg, _ = st.decode(want[:, k])
+    st.destroy()
+    print(f"  distinct picks {len(np.unique(want))}")
+    np.testing.assert_array_equal(got, want)
+    m.destroy()
+
+
+def test_model_generate_sampled_equals_host_loop(device):
+    """HybridMambaModel.generate (device sampler) == the host loop of streaming.ts:17-49
+    (prefill, decode, host sampleToken) with the same seeded draws, up to eos."""
+    case("HybridMambaModel.generate sampled vs host loop")
+    import random as _random
+    from ssmjs_amd import model as M
+    from ssmjs_amd.streaming import sample_token
+    dev_ = M.HipDevice(0)
+    cfg = {"vocabSize": 300, "dModel": 128, "numLayers": 2, "dState": 32, "dConv": 4,
+           "expand": 2, "nHeads": 4, "layers": [{"type": "mamba2"}, {"type": "mamba1"}],
+           "eosId": 7}
+    hm = M.HybridMambaModel(dev_, cfg, seed=5)
+    sampling = {"temperature": 0.8, "topK": 50, "topP": 0.9}
+    prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+    got = hm.generate(prompt, 40, sampling, rng=_random.Random(1234).random)
+    rng = _random.Random(1234).random
+    st = hm.native.new_state(1)
+    ids = list(prompt)
+    lg, _ = st.prefill(np.array([ids], np.uint32))
+    for k in range(40):
+        nxt = sample_token(lg[0], 0.8, 50, 0.9, rng)
+        ids.append(nxt)
+        if nxt == 7 or k + 1 == 40:
+            break
+        lg, _ = st.decode(np.array([nxt], np.uint32))
+    st.destroy()
+    assert got == ids
+    hm.destroy()
+    dev_.destroy()

@@ -250,3 +250,85 @@ def test_model_rejects_bad_images(golden):
     bad[4] = 9
     with pytest.raises(ValueError, match="version"):
         O.Model(bytes(bad))
+
+
+# ---------------------------------------------------------------- sampleToken restatement
+# orc_sample_token follows src/session/streaming.ts:53-97. It is pinned by answers the
+# reference's arithmetic fixes (stable sort, nucleus cut, draw order), by the exact-tie rule
+# of the f32 exps, and by agreement with the independent numpy restatement in
+# ssmjs_amd/streaming.py on rows with many ties.
+
+def test_sample_token_known_answers():
+    lg = np.array([0.1, 3.0, -2.0, 3.0, 1.0], np.float32)
+    for u in (0.0, 0.5, 0.999999):                 # topK 1: first of the stable sort
+        assert O.sample_token(lg, 0.8, 1, 0.9, u) == 1
+    p = np.log(np.array([0.5, 0.3, 0.15, 0.05], np.float32))
+    assert O.sample_token(p, 1.0, 50, 0.7, 0.0) == 0      # nucleus [0, 1]
+    assert O.sample_token(p, 1.0, 50, 0.7, 0.99) == 1
+    assert O.sample_token(p, 1.0, 3, 1.0, 0.999) == 2     # topK 3 never reaches index 3
+    assert O.sample_token(p, 1.0, 50, 0.0, 0.999) == 0    # topP 0: nucleus = top entry
+    assert O.sample_token(p, 1.0, 99, 1.0, 0.999) == 3    # topK > n: every index
+    assert O.sample_token(np.zeros(7, np.float32), 1.0, 50, 1.0, 0.999) == 6
+    with pytest.raises(ValueError):
+        O.sample_token(p, 1.0, 0, 0.9, 0.5)
+
+
+def test_sample_token_ties_of_rounded_exps():
+    """Two logits whose exps round to the same f32 tie, and the lower index wins even when
+    its logit is smaller: exp(-7.45e-9) rounds to 1.0f."""
+    a = np.float32(0.1)
+    b = np.nextafter(a, np.float32(1.0))
+    assert b > a
+    assert O.sample_token(np.array([a, b], np.float32), 1.0, 1, 0.9, 0.5) == 0
+    assert O.sample_token(np.array([b, a], np.float32), 1.0, 1, 0.9, 0.5) == 0
+    # far enough apart, the larger logit wins whatever its index
+    c = np.float32(0.1 + 1e-6)
+    assert O.sample_token(np.array([a, c], np.float32), 1.0, 1, 0.9, 0.5) == 1
+    # temperature rounding: adjacent logits whose quotients by 5 collide in f32 tie as well
+    # (ulp 1.19e-7 over 5 is below the quotient's ulp of 2.98e-8)
+    x = np.float32(1.9)
+    for _ in range(64):
+        y = np.nextafter(x, np.float32(2.0))
+        if np.float32(np.float64(x) / 5.0) == np.float32(np.float64(y) / 5.0):
+            break
+        x = y
+    assert np.float32(np.float64(x) / 5.0) == np.float32(np.float64(y) / 5.0)
+    assert O.sample_token(np.array([x, y], np.float32), 5.0, 1, 0.9, 0.5) == 0
+    assert O.sample_token(np.array([y, x], np.float32), 5.0, 1, 0.9, 0.5) == 0
+
+
+def test_sample_token_temperature_floor():
+    lg = np.array([0.0, 1e-6, -1e-6], np.float32)
+    # T <= 1e-7 acts as 1e-7: scaled gaps of 10 make the top entry take the whole nucleus
+    for T in (0.0, -1.0, 1e-9):
+        assert O.sample_token(lg, T, 50, 0.9, 0.999) == 1
+
+
+def test_sample_token_draw_is_renormalised_nucleus():
+    """Over a uniform grid of draws the picks follow e_k / (nucleus sum): the CDF walk."""
+    lg = np.log(np.array([0.4, 0.25, 0.2, 0.1, 0.05], np.float32))
+    M = 2000
+    counts = np.zeros(5)
+    for j in range(M):
+        counts[O.sample_token(lg, 1.0, 4, 0.8, (j + 0.5) / M)] += 1
+    e = np.exp(lg.astype(np.float64) - lg.max())
+    nucleus = e[:3]                                   # 0.4 + 0.25 + 0.2 >= 0.8
+    want = np.zeros(5)
+    want[:3] = nucleus / nucleus.sum()
+    assert np.abs(counts / M - want).max() <= 1.0 / M + 1e-12
+
+
+@pytest.mark.parametrize("n", [1, 2, 700, 5000])
+def test_sample_token_agrees_with_host_restatement(n):
+    from ssmjs_amd.streaming import sample_token as host_sample
+    r = np.random.default_rng(900 + n)
+    for trial in range(12):
+        if trial % 3 == 0:
+            lg = r.integers(-3, 3, n).astype(np.float32) * 0.5   # heavy ties
+        else:
+            lg = (r.standard_normal(n) * (0.05 if trial % 3 == 1 else 3.0)).astype(np.float32)
+        T = [1.0, 0.8, 2.5, 1e-9][trial % 4]
+        K = [1, 2, 50, n, n + 5, 1024][trial % 6]
+        P = [0.9, 1.0, 0.5, 0.0][(trial // 2) % 4]
+        for u in (0.0, 0.3, float(r.random()), 0.9999999):
+            assert O.sample_token(lg, T, K, P, u) == host_sample(lg, T, K, P, rng=lambda: u)
