@@ -191,9 +191,12 @@ ssm_status ssm_argmax(const float* x, long ldx, int rows, int n, uint32_t* out, 
  * (equal exps: lower index first); the nucleus ends at the first cumulative exp/sumE >=
  * topP; the pick is the first nucleus entry whose running exp sum reaches u * (nucleus
  * sum). Needs 1 <= n <= 32768 and min(topK, n) <= 1024 (SSM_ERR_UNSUPPORTED otherwise) and
- * topK >= 1. Logits must be finite. */
+ * topK >= 1. Logits must be finite. workspace: device memory of ssm_sample_workspace(rows,
+ * n) bytes (scaled values, keys, slice maxima and sums), one stream at a time. */
+size_t ssm_sample_workspace(int rows, int n);
 ssm_status ssm_sample(const float* logits, long ld, int rows, int n, double temperature,
-                      int top_k, double top_p, const double* u, uint32_t* out, void* stream);
+                      int top_k, double top_p, const double* u, uint32_t* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ model level */
 #define SSM_LAYER_MAMBA1 1

@@ -20,9 +20,10 @@ ssm_status launch_argmax(const float* x, long ldx, int rows, int n, uint32_t* ou
                          hipStream_t st);
 // sampleToken on the device (sample.hip): sample_ok says whether (n, topK) is supported.
 bool sample_ok(int n, int top_k);
+size_t sample_workspace(int rows, int n);
 ssm_status launch_sample(const float* logits, long ld, int rows, int n, double temperature,
                          int top_k, double top_p, const double* u, uint32_t* out,
-                         hipStream_t st);
+                         void* workspace, hipStream_t st);
 ssm_status launch_init(float* p, long n, int kind, float a0, float a1, uint64_t seed,
                        uint64_t tensor_id, int row, hipStream_t st);
 ssm_status launch_neg_exp(const float* x, float* y, long n, hipStream_t st);

@@ -415,6 +415,7 @@ struct ssm_state {
     uint32_t* d_ping = nullptr;  // (2, B) ids of generation steps
     double* d_u = nullptr;       // (n_new, B) uniform draws of sampled generation
     size_t u_cap = 0;
+    void* d_sws = nullptr;       // sampler workspace (ssm_sample_workspace(B, V) bytes)
     // Captured one-token steps: a step's kernels depend only on these pointers (the model's
     // weights and workspaces, this state's buffers, the ids / logits / argmax arguments), so a
     // step repeated with the same ones replays a HIP graph instead of launching ~5 kernels per
@@ -1113,7 +1114,7 @@ extern "C" ssm_status ssm_state_destroy(ssm_state* s) {
         for (auto& g : s->graphs)
             if (g.exec) hipGraphExecDestroy(g.exec);
         hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits); hipFree(s->d_gen);
-        hipFree(s->d_ping); hipFree(s->d_u);
+        hipFree(s->d_ping); hipFree(s->d_u); hipFree(s->d_sws);
     }
     s->graphs.clear();
     s->destroyed = true;
@@ -1395,11 +1396,12 @@ extern "C" ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint
         SSM_HIP_TRY(hipMalloc((void**)&s->d_u, nu * sizeof(double)));
         s->u_cap = nu;
     }
+    if (!s->d_sws) SSM_HIP_TRY(hipMalloc(&s->d_sws, ssm::sample_workspace(B, V)));
     SSM_HIP_TRY(hipMemcpyAsync(s->d_u, u_host, nu * sizeof(double), hipMemcpyHostToDevice, st));
     SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, prompt, T * 4, hipMemcpyHostToDevice, st));
     SSM_TRY(prefill_device(m, s, m->d_ids, Lp, nullptr));
     SSM_TRY(ssm::launch_sample(s->d_logits, V, B, V, temperature, top_k, top_p, s->d_u,
-                               s->d_gen, st));
+                               s->d_gen, s->d_sws, st));
     // as in greedy generation, steps alternate between two id buffers so that they replay
     // two captured graphs; the sampler runs after each step, outside the graph (its draws
     // change every step)
@@ -1411,7 +1413,7 @@ extern "C" ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint
         uint32_t* outp = s->d_ping + (size_t)(k & 1) * B;
         SSM_TRY(ssm_decode_step_device(m, s, in, nullptr, nullptr));
         SSM_TRY(ssm::launch_sample(s->d_logits, V, B, V, temperature, top_k, top_p,
-                                   s->d_u + (size_t)k * B, outp, st));
+                                   s->d_u + (size_t)k * B, outp, s->d_sws, st));
         SSM_HIP_TRY(hipMemcpyAsync(s->d_gen + (size_t)k * B, outp, (size_t)B * 4,
                                    hipMemcpyDeviceToDevice, st));
     }

@@ -152,7 +152,13 @@ def argmax(x, out=None):
     return o
 
 
-def sample(x, u, temperature=1.0, topK=50, topP=0.9, out=None):
+def sample_workspace(rows, n, device):
+    """Workspace for sample (ssm_sample_workspace bytes)."""
+    return torch.empty(max(1, _lib.lib().ssm_sample_workspace(rows, n)), dtype=torch.uint8,
+                       device=device)
+
+
+def sample(x, u, temperature=1.0, topK=50, topP=0.9, out=None, workspace=None):
     """sampleToken per row on the device (ssm_sample, src/session/streaming.ts:53-97).
 
     x: (rows, n) fp32 logits; u: (rows,) float64 draws in [0, 1) (Math.random()). Returns
@@ -160,8 +166,9 @@ def sample(x, u, temperature=1.0, topK=50, topP=0.9, out=None):
     rows, n = x.shape
     assert u.dtype == torch.float64 and u.numel() == rows and u.is_contiguous()
     o = out if out is not None else torch.empty(rows, dtype=torch.int32, device=x.device)
+    ws = workspace if workspace is not None else sample_workspace(rows, n, x.device)
     _lib.call("ssm_sample", _p(x), x.stride(0), rows, n, float(temperature), int(topK),
-              float(topP), _p(u), _p(o), _stream())
+              float(topP), _p(u), _p(o), _p(ws), ws.numel(), _stream())
     return o
 
 

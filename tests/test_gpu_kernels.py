@@ -378,17 +378,21 @@ def test_argmax_ties_nan_and_tails(n, pad):
 
 
 def _sample_rows(r, rows, n):
-    """Logit rows of several kinds: heavy exact ties, near-ties (small scale: rounded exps
-    collide), wide spread, and one constant row."""
+    """Logit rows of several kinds: heavy exact ties (more equal to the K-th value than the
+    candidate list holds), near-ties (small scale: rounded exps collide), wide spread, a
+    plateau of up to 100 equal maxima (more candidates than topK), and one constant row."""
     x = np.empty((rows, n), np.float32)
     for i in range(rows):
-        k = i % 4
+        k = i % 5
         if k == 0:
             x[i] = r.integers(-3, 3, n) * 0.5
         elif k == 1:
             x[i] = r.standard_normal(n) * 0.02
         elif k == 2:
             x[i] = r.standard_normal(n) * 3.0
+        elif k == 3:
+            x[i] = r.standard_normal(n)
+            x[i, r.choice(n, min(n, 100), replace=False)] = 5.0
         else:
             x[i] = r.standard_normal(n)
     x[rows - 1] = 0.25
