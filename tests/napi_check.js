@@ -14,7 +14,10 @@ async function main() {
   await model.loadWeights(fs.readFileSync(ckpt));
   const prompt = promptCsv.split(',').map(Number);
   const generated = await model.generate(prompt, Number(nNew), { temperature: 0.8, topK: 1, topP: 0.9 });
-  const sampled = await model.generate(prompt, 4, { temperature: 1.0, topK: 5, topP: 0.9, rng: () => 0.5 });
+  const draws = [0.1, 0.7, 0.35, 0.9, 0.5];
+  let nDraw = 0;
+  const sampled = await model.generate(prompt, 8, { temperature: 1.3, topK: 5, topP: 0.9,
+                                                    rng: () => draws[nDraw++ % draws.length] });
   const { logits } = await model.forward(Uint32Array.from(prompt), 1, prompt.length);
   let badCode = null;
   try { await model.loadWeights(Buffer.from('JUNK0000')); } catch (e) { badCode = e.code; }

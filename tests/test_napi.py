@@ -116,7 +116,23 @@ def test_node_session_path_matches_oracle(tmp_path):
     ids, margins = O.greedy(om, np.array([prompt], np.uint32), 16)
     assert margins.min() > 1e-3
     assert out["generated"] == prompt + ids[0].tolist()
-    assert out["sampled"][:len(prompt)] == prompt and len(out["sampled"]) == len(prompt) + 4
+    # sampled generation (device sampler behind generate) == the host loop over the same
+    # device logits with the oracle's sampleToken and the same draws
+    draws = [0.1, 0.7, 0.35, 0.9, 0.5]
+    d = backend.Device(0)
+    m = backend.Model(d, cfg, seed=0)
+    m.load_weights(blob)
+    st = m.new_state(1)
+    want = list(prompt)
+    lg, _ = st.prefill(np.array([prompt], np.uint32))
+    for k in range(8):
+        want.append(O.sample_token(lg[0], 1.3, 5, 0.9, draws[k % 5]))
+        if k + 1 < 8:
+            lg, _ = st.decode(np.array([want[-1]], np.uint32))
+    st.destroy()
+    m.destroy()
+    d.destroy()
+    assert out["sampled"] == want
     ref = om.forward(np.array([prompt], np.uint32))[0]
     lg = np.array(out["logits"], np.float32).reshape(len(prompt), 256)
     assert np.abs(lg - ref).max() / np.abs(ref).max() <= 1e-4
