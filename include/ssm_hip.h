@@ -190,7 +190,7 @@ ssm_status ssm_argmax(const float* x, long ldx, int rows, int n, uint32_t* out, 
  * double with float stores; the topK largest exps are taken in a stable descending order
  * (equal exps: lower index first); the nucleus ends at the first cumulative exp/sumE >=
  * topP; the pick is the first nucleus entry whose running exp sum reaches u * (nucleus
- * sum). Needs 1 <= n <= 32768 and min(topK, n) <= 1024 (SSM_ERR_UNSUPPORTED otherwise) and
+ * sum). Needs 1 <= n <= 262144 and min(topK, n) <= 1024 (SSM_ERR_UNSUPPORTED otherwise) and
  * topK >= 1. Logits must be finite. workspace: device memory of ssm_sample_workspace(rows,
  * n) bytes (scaled values, keys, slice maxima and sums), one stream at a time. */
 size_t ssm_sample_workspace(int rows, int n);

@@ -16,8 +16,8 @@ from . import _lib
 
 def sample_supported(n: int, topK: int) -> bool:
     """Whether the device sampler (ssm_sample / ssm_generate_sample) takes a row of n logits
-    with this topK: n <= 32768 and min(topK, n) <= 1024."""
-    return 1 <= n <= 32768 and topK >= 1 and min(topK, n) <= 1024
+    with this topK: n <= 262144 and min(topK, n) <= 1024."""
+    return 1 <= n <= 262144 and topK >= 1 and min(topK, n) <= 1024
 
 
 def _ptr(a):

@@ -10,9 +10,10 @@
 //   scale  (slices of 2048 logits per workgroup): scaled values to the workspace, slice maxima;
 //   exp    (same slices): e as a sortable key (bits of e + 1: monotonic for e >= 0, and 0
 //          marks padding) over the scaled values, and each slice's sum of e;
-//   pick   (one 1024-thread workgroup per row, keys in registers): the K-th largest key by a
-//          4-pass radix select, the candidates above / equal to it gathered to LDS, sorted
-//          (key descending, index ascending), then one wave walks the nucleus and the draw.
+//   pick   (one 1024-thread workgroup per row; keys in registers up to 32768 per row, read
+//          again from the workspace for longer rows): a bound on the K-th largest key, the
+//          candidates above it gathered to LDS (an exact radix select when too many tie),
+//          sorted (key descending, index ascending), then the nucleus and the draw.
 // The double division and exp are the costly part (about 35 double operations per logit),
 // which is why they are spread over many workgroups instead of the one that owns the row.
 // sumE adds per thread in index order, then over threads, waves and slices in a fixed order:
@@ -23,17 +24,22 @@
 #include "common.hpp"
 #include "glue.hpp"
 
+// The slice loops are unrolled fully for register-held keys (a constant 32 slices) and stay
+// loops for keys read from the workspace; clang warns about the latter.
+#pragma clang diagnostic ignored "-Wpass-failed"
+
 namespace {
 
 constexpr int kSlice = 2048;                    // logits per scale / exp workgroup
 constexpr int kSliceThreads = 256;
 constexpr int kPer = kSlice / kSliceThreads;    // 8 per thread
 constexpr int kThreads = 1024;                  // pick workgroup
-constexpr int kEPT = 32;                        // keys per pick thread: rows up to 32768
-constexpr int kMaxN = kThreads * kEPT;
+constexpr int kEPT = 32;                        // keys per pick thread held in registers
+constexpr int kRegN = kThreads * kEPT;          // rows up to 32768 keep their keys in registers
+constexpr int kMaxN = 262144;                   // longer rows re-read them from the workspace
 constexpr int kMaxK = 1024;                     // topK handled on the device; sort capacity
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxSlices = (kMaxN + kSlice - 1) / kSlice;
+constexpr int kMaxSlices = (kMaxN + kSlice - 1) / kSlice;   // 128
 
 struct Ws {
     uint32_t* keys;   // (rows, n): scaled floats, then keys
@@ -90,17 +96,19 @@ __global__ __launch_bounds__(kSliceThreads) void sample_scale_kernel(
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int i = base + kSliceThreads * j;
-        v[j] = i < n ? x[i] : 0.f;
+        v[j] = x[i < n ? i : n - 1];   // clamped, not branched: all loads in flight at once
     }
+    // every element is computed (past the row's end on a clamped copy) so that the eight
+    // divisions overlap; only the stores and the maximum are masked
+    float sc[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) sc[j] = (float)((double)v[j] / t);
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int i = base + kSliceThreads * j;
-        if (i < n) {
-            const float s = (float)((double)v[j] / t);
-            out[i] = s;
-            mx = fmaxf(mx, s);
-        }
+        if (i < n) out[i] = sc[j];
+        mx = fmaxf(mx, i < n ? sc[j] : -INFINITY);
     }
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -115,26 +123,30 @@ __global__ __launch_bounds__(kSliceThreads) void sample_scale_kernel(
 // e = float(exp(scaled - maxL)) (:66-71) stored as key bits(e) + 1, and the slice's sum of e
 __global__ __launch_bounds__(kSliceThreads) void sample_exp_kernel(int n, Ws ws) {
     __shared__ double red[kSliceThreads / 64];
+    __shared__ float redm[kSliceThreads / 64];
     const int row = blockIdx.y, S = gridDim.x;
-    float mx = ws.smax[(long)row * S];
-    for (int s = 1; s < S; ++s) mx = fmaxf(mx, ws.smax[(long)row * S + s]);
+    float mx = (int)threadIdx.x < S ? ws.smax[(long)row * S + threadIdx.x] : -INFINITY;
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
     uint32_t* keys = ws.keys + (long)row * n;
     const int base = blockIdx.x * kSlice + threadIdx.x;
     float v[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int i = base + kSliceThreads * j;
-        v[j] = i < n ? __uint_as_float(keys[i]) : 0.f;
+        v[j] = __uint_as_float(keys[i < n ? i : n - 1]);   // clamped: loads in flight at once
     }
+    float e[kPer];   // all eight exps overlap, as in the scale kernel
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) e[j] = (float)exp((double)v[j] - (double)mx);
     double part = 0.0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int i = base + kSliceThreads * j;
-        if (i < n) {
-            const float e = (float)exp((double)v[j] - (double)mx);
-            part += (double)e;
-            keys[i] = __float_as_uint(e) + 1u;
-        }
+        if (i < n) keys[i] = __float_as_uint(e[j]) + 1u;
+        part += i < n ? (double)e[j] : 0.0;
     }
     part = wave_sum(part);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
@@ -151,10 +163,50 @@ __device__ __forceinline__ bool before(unsigned ka, unsigned ia, unsigned kb, un
     return ka > kb || (ka == kb && ia < ib);
 }
 
-// The K-th largest key by a 4-pass radix select over the keys in registers: kth, how many
-// elements equal to it belong to the top K (left), and how many equal it in all (eq_total).
-// Padding (key 0) is left out of the counts; there are always at least K real elements.
-__device__ void radix_select(const unsigned (&key)[kEPT], unsigned K, unsigned (*hist)[256],
+// A row's keys as thread tid sees them: slice j holds index tid + 1024 j. Rows up to 32768
+// keep them in registers; longer rows read them from the workspace at every use (the row
+// stays in L2 / the MALL between the passes).
+template <bool REG>
+struct RowKeys;
+
+template <>
+struct RowKeys<true> {
+    unsigned k[kEPT];
+    __device__ void init(const uint32_t* src, int n) {
+#pragma unroll
+        for (int j = 0; j < kEPT; ++j) {
+            const int i = threadIdx.x + kThreads * j;
+            const unsigned v = src[i < n ? i : n - 1];   // clamped, not branched
+            k[j] = i < n ? v : 0u;
+        }
+    }
+    __device__ constexpr int slices() const { return kEPT; }
+    __device__ unsigned get(int j) const { return k[j]; }
+};
+
+template <>
+struct RowKeys<false> {
+    const uint32_t* src;
+    int n;
+    __device__ void init(const uint32_t* s, int nn) {
+        src = s;
+        n = nn;
+    }
+    __device__ int slices() const { return (n + kThreads - 1) / kThreads; }
+    // any j >= 0: past the row's end it reads the last key (in bounds) and returns 0; a
+    // branch around the load instead would wait for each load before issuing the next
+    __device__ unsigned get(int j) const {
+        const int i = threadIdx.x + kThreads * j;
+        const unsigned v = src[i < n ? i : n - 1];
+        return i < n ? v : 0u;
+    }
+};
+
+// The K-th largest key by a 4-pass radix select: kth, how many elements equal to it belong
+// to the top K (left), and how many equal it in all (eq_total). Padding (key 0) is left out
+// of the counts; there are always at least K real elements.
+template <bool REG>
+__device__ void radix_select(const RowKeys<REG>& ks, unsigned K, unsigned (*hist)[256],
                              unsigned* wtot, unsigned* sel, unsigned& kth, unsigned& left,
                              unsigned& eq_total) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -165,9 +217,11 @@ __device__ void radix_select(const unsigned (&key)[kEPT], unsigned K, unsigned (
         for (int b = lane; b < 256; b += 64) hist[w][b] = 0u;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < kEPT; ++j)
-            if (key[j] != 0u && (key[j] & pmask) == prefix)
-                atomicAdd(&hist[w][(key[j] >> shift) & 255u], 1u);
+        for (int j = 0; j < ks.slices(); ++j) {
+            const unsigned key = ks.get(j);
+            if (key != 0u && (key & pmask) == prefix)
+                atomicAdd(&hist[w][(key >> shift) & 255u], 1u);
+        }
         __syncthreads();
         // thread t < 256 owns bin 255 - t: an inclusive scan over t counts the elements in
         // this bin and every higher one
@@ -203,17 +257,18 @@ __device__ void radix_select(const unsigned (&key)[kEPT], unsigned K, unsigned (
     kth = prefix;
 }
 
-// Positions for the lanes' flagged entries of kEPT ballots, with one LDS atomic per wave on
-// the list's count (which keeps counting past the list's capacity).
-__device__ __forceinline__ void append_all(const bool (&flag)[kEPT], const unsigned (&key)[kEPT],
-                                           unsigned* count, unsigned* ckey, unsigned* cidx,
-                                           unsigned cap) {
+// Appends the lanes' flagged entries of G slices (starting at slice j0) to the LDS list, with
+// one LDS atomic per wave on the list's count (which keeps counting past the capacity).
+template <int G>
+__device__ __forceinline__ void append(const bool (&flag)[G], const unsigned (&key)[G], int j0,
+                                       unsigned* count, unsigned* ckey, unsigned* cidx,
+                                       unsigned cap) {
     const int tid = threadIdx.x, lane = tid & 63;
     const unsigned long long below = (1ull << lane) - 1ull;
-    unsigned long long bal[kEPT];
+    unsigned long long bal[G];
     unsigned total = 0u;
 #pragma unroll
-    for (int j = 0; j < kEPT; ++j) {
+    for (int j = 0; j < G; ++j) {
         bal[j] = __ballot(flag[j]);
         total += (unsigned)__popcll(bal[j]);
     }
@@ -222,16 +277,33 @@ __device__ __forceinline__ void append_all(const bool (&flag)[kEPT], const unsig
     if (lane == 0) base = atomicAdd(count, total);
     base = (unsigned)__builtin_amdgcn_readfirstlane((int)base);
 #pragma unroll
-    for (int j = 0; j < kEPT; ++j) {
+    for (int j = 0; j < G; ++j) {
         const unsigned pos = base + (unsigned)__popcll(bal[j] & below);
         if (flag[j] && pos < cap) {
             ckey[pos] = key[j];
-            cidx[pos] = (unsigned)(tid + kThreads * j);
+            cidx[pos] = (unsigned)(tid + kThreads * (j0 + j));
         }
         base += (unsigned)__popcll(bal[j]);
     }
 }
 
+// Every key in [lo, hi) (lo <= key < hi, key != 0) to the list, in groups of 16 slices.
+template <bool REG>
+__device__ __forceinline__ void append_range(const RowKeys<REG>& ks, unsigned lo, unsigned hi,
+                                             unsigned* count, unsigned* ckey, unsigned* cidx) {
+#pragma unroll
+    for (int j0 = 0; j0 < ks.slices(); j0 += 16) {
+        bool f[16];
+        unsigned k[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) k[q] = ks.get(REG ? (j0 + q) % kEPT : j0 + q);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) f[q] = k[q] != 0u && k[q] >= lo && k[q] < hi;
+        append<16>(f, k, j0, count, ckey, cidx, (unsigned)kMaxK);
+    }
+}
+
+template <bool REG>
 __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int K, double top_p,
                                                                const double* __restrict__ u,
                                                                Ws ws,
@@ -241,7 +313,7 @@ __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int
     __shared__ unsigned cidx[kMaxK];
     __shared__ double acc[kMaxK];   // running sums of e along the sorted candidates
     __shared__ double pd[kMaxK];    // e / sumE of the sorted candidates
-    __shared__ double ssum[kMaxSlices];
+    __shared__ double sum_s;
     __shared__ unsigned wtot[4];
     __shared__ unsigned sel[3];
     __shared__ unsigned gcount;
@@ -249,17 +321,27 @@ __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int
     __shared__ unsigned flags[2][kWaves];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int row = blockIdx.x;
-    const uint32_t* keys = ws.keys + (long)row * n;
 
-    unsigned key[kEPT];
+    RowKeys<REG> ks;
+    ks.init(ws.keys + (long)row * n, n);
     unsigned tmax = 0u;
 #pragma unroll
-    for (int j = 0; j < kEPT; ++j) {
-        const int i = tid + kThreads * j;
-        key[j] = i < n ? keys[i] : 0u;
-        tmax = key[j] > tmax ? key[j] : tmax;
+    for (int j0 = 0; j0 < ks.slices(); j0 += 16) {   // 16 loads in flight per group
+        unsigned k[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) k[q] = ks.get(REG ? (j0 + q) % kEPT : j0 + q);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) tmax = k[q] > tmax ? k[q] : tmax;
     }
-    if (tid < S) ssum[tid] = ws.ssum[(long)row * S + tid];
+    // sumE from the slice sums: lane l of wave 0 adds slices l, l + 64 (S <= 128), then a
+    // fixed butterfly over the lanes
+    if (w == 0) {
+        const long b = (long)row * S;
+        double part = lane < S ? ws.ssum[b + lane] : 0.0;
+        if (lane + 64 < S) part += ws.ssum[b + lane + 64];
+        part = wave_sum(part);
+        if (lane == 0) sum_s = part;
+    }
     const double ur = u[row];
 
     // 1. a lower bound tau for the K-th largest key: the K-th largest of the 1024 thread
@@ -293,37 +375,27 @@ __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int
     }
 
     // 2. candidates: every key >= tau (they include the top K, ties and all), when they fit
-    {
-        bool take[kEPT];
-#pragma unroll
-        for (int j = 0; j < kEPT; ++j) take[j] = key[j] >= tau && key[j] != 0u;
-        append_all(take, key, &gcount, ckey, cidx, (unsigned)kMaxK);
-    }
+    append_range(ks, tau, 0xffffffffu, &gcount, ckey, cidx);
     __syncthreads();
     unsigned C = gcount;
     if (C > (unsigned)kMaxK) {
         // too many (ties at the bound, or K near the list's capacity): select the K-th key
         // exactly, then take every key above it and the lowest-index ones equal to it
         unsigned kth, left, eq_total;
-        radix_select(key, (unsigned)K, hist, wtot, sel, kth, left, eq_total);
+        radix_select(ks, (unsigned)K, hist, wtot, sel, kth, left, eq_total);
         const unsigned above = (unsigned)K - left;
         if (tid == 0) gcount = 0u;
         __syncthreads();
         const bool all_eq = above + eq_total <= (unsigned)kMaxK;
-        {
-            bool take[kEPT];
-#pragma unroll
-            for (int j = 0; j < kEPT; ++j) take[j] = all_eq ? key[j] >= kth : key[j] > kth;
-            append_all(take, key, &gcount, ckey, cidx, (unsigned)kMaxK);
-        }
+        append_range(ks, all_eq ? kth : kth + 1u, 0xffffffffu, &gcount, ckey, cidx);
         C = all_eq ? above + eq_total : (unsigned)K;
         if (!all_eq) {
             // index order is slice j, then thread
             unsigned taken = 0u;   // equal elements placed so far (the same in every thread)
 #pragma unroll
-            for (int j = 0; j < kEPT; ++j) {
+            for (int j = 0; j < ks.slices(); ++j) {
                 if (taken < left) {   // uniform over the workgroup
-                    const bool eq = key[j] == kth;
+                    const bool eq = ks.get(j) == kth;
                     const unsigned long long bal = __ballot(eq);
                     const unsigned below_in_wave = __popcll(bal & ((1ull << lane) - 1ull));
                     if (lane == 0) wcount[w] = (unsigned)__popcll(bal);
@@ -335,7 +407,7 @@ __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int
                     }
                     const unsigned rank = taken + pre + below_in_wave;
                     if (eq && rank < left) {
-                        ckey[above + rank] = key[j];
+                        ckey[above + rank] = kth;
                         cidx[above + rank] = (unsigned)(tid + kThreads * j);
                     }
                     taken += total;
@@ -345,6 +417,7 @@ __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int
         }
         __syncthreads();
     }
+    const double sum_e = sum_s;
 
     // 3. sort the C candidates (padded to a power of two with key 0, which sorts last)
     unsigned S2 = 64u;
@@ -401,8 +474,7 @@ __global__ __launch_bounds__(kThreads) void sample_pick_kernel(int n, int S, int
     // adds them eight entries at a time (adding 0.0 past the end changes neither sum) before
     // looking for the cut among the eight; the draw is then a parallel search.
     {
-        double sumE = 0.0;
-        for (int s2 = 0; s2 < S; ++s2) sumE += ssum[s2];
+        const double sumE = sum_e;
         const int Kp = (K + 7) & ~7;
         for (int t = tid; t < Kp; t += kThreads) {
             const double ev = t < K ? (double)__uint_as_float(ckey[t] - 1u) : 0.0;
@@ -482,13 +554,18 @@ ssm_status launch_sample(const float* logits, long ld, int rows, int n, double t
     sample_exp_kernel<<<dim3(S, rows), kSliceThreads, 0, st>>>(n, w);
     r = check_launch("sample exp");
     if (r != SSM_OK) return r;
-    sample_pick_kernel<<<rows, kThreads, 0, st>>>(n, S, K, top_p, u, w, out);
+    if (n <= kRegN)
+        sample_pick_kernel<true><<<rows, kThreads, 0, st>>>(n, S, K, top_p, u, w, out);
+    else
+        sample_pick_kernel<false><<<rows, kThreads, 0, st>>>(n, S, K, top_p, u, w, out);
     return check_launch("sample pick");
 }
 
 }  // namespace ssm
 
-static_assert(kMaxSlices <= 16, "slice maxima and sums are read serially");
+static_assert(kMaxSlices <= 128, "the pick kernel adds at most two slice sums per lane");
+static_assert(kEPT % 16 == 0, "register keys are visited in groups of 16 slices");
+static_assert(kMaxSlices <= kSliceThreads, "one slice maximum per exp-kernel thread");
 
 extern "C" size_t ssm_sample_workspace(int rows, int n) { return ssm::sample_workspace(rows, n); }
 

@@ -162,7 +162,7 @@ def sample(x, u, temperature=1.0, topK=50, topP=0.9, out=None, workspace=None):
     """sampleToken per row on the device (ssm_sample, src/session/streaming.ts:53-97).
 
     x: (rows, n) fp32 logits; u: (rows,) float64 draws in [0, 1) (Math.random()). Returns
-    (rows,) int32 picks. Raises for n > 32768 or min(topK, n) > 1024."""
+    (rows,) int32 picks. Raises for n > 262144 or min(topK, n) > 1024."""
     rows, n = x.shape
     assert u.dtype == torch.float64 and u.numel() == rows and u.is_contiguous()
     o = out if out is not None else torch.empty(rows, dtype=torch.int32, device=x.device)

@@ -154,7 +154,7 @@ class HybridMambaModel {
         return ids;
       };
       const V = this.config.vocabSize;
-      if (topK >= 1 && V <= 32768 && Math.min(topK, V) <= 1024) {
+      if (topK >= 1 && V <= 262144 && Math.min(topK, V) <= 1024) {
         // sampleToken on the device (ssm_generate_sample), topK 1 included: one draw per
         // step, taken up front in the order the host loop below takes them
         const draw = rng || Math.random;

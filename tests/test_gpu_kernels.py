@@ -400,11 +400,13 @@ def _sample_rows(r, rows, n):
 
 
 @pytest.mark.parametrize("n,pad", [(1, 0), (2, 1), (700, 3), (1500, 0), (32000, 0),
-                                   (32768, 0)])
+                                   (32768, 0), (32769, 0), (151936, 5), (262144, 0)])
 def test_sample_matches_oracle(n, pad):
     """sampleToken on the device (ssm_sample) picks exactly the index the restatement of
     src/session/streaming.ts:53-97 picks, for the same draw u, over temperatures (including
-    the 1e-7 floor), topK (1, ties at the K-th value, K >= n, the 1024 maximum) and topP."""
+    the 1e-7 floor), topK (1, ties at the K-th value, K >= n, the 1024 maximum) and topP.
+    Rows above 32768 (the reference's default tokenizer has 151,665 entries) read their keys
+    from the workspace instead of registers."""
     case(f"sample n={n} pad={pad}")
     r = rng(80 + n)
     rows = 12
@@ -431,7 +433,7 @@ def test_sample_limits():
     from ssmjs_amd._lib import SsmError
     u = torch.zeros(1, dtype=torch.float64, device="cuda")
     with pytest.raises(SsmError):
-        K().sample(torch.zeros(1, 32769, device="cuda"), u, 1.0, 50, 0.9)
+        K().sample(torch.zeros(1, 262145, device="cuda"), u, 1.0, 50, 0.9)
     with pytest.raises(SsmError):
         K().sample(torch.zeros(1, 2048, device="cuda"), u, 1.0, 1025, 0.9)
     with pytest.raises(SsmError):
