@@ -137,20 +137,39 @@ __global__ void conv1d_state_out(const float* __restrict__ x, long ldx, int B, i
 }
 
 // One decode token: thread per (b, c).
+// One-token update, a thread per (b, c): the window is the (K-1)-deep state plus x. KC is
+// the width when known at compile time (every load is then issued before the first use);
+// KC = 0 takes it from K at run time.
+template <int KC>
 __global__ void conv1d_update_kernel(const float* __restrict__ x, long ldx,
                                      const float* __restrict__ w, const float* __restrict__ bias,
                                      float* __restrict__ y, long ldy, float* __restrict__ state,
-                                     int B, int C, int K, int silu) {
+                                     int B, int C, int Kr, int silu) {
+    const int K = KC > 0 ? KC : Kr;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)B * C) return;
     const int b = (int)(i / C), c = (int)(i % C);
     float* st = state + i * (K - 1);
     const float xn = x[(long)b * ldx + c];
     float acc = bias ? bias[c] : 0.f;
-    for (int k = 0; k < K - 1; ++k) acc = fmaf(w[(long)c * K + k], st[k], acc);
-    acc = fmaf(w[(long)c * K + K - 1], xn, acc);
-    for (int k = 0; k + 1 < K - 1; ++k) st[k] = st[k + 1];
-    if (K > 1) st[K - 2] = xn;
+    if (KC > 0) {
+        float wv[KC > 0 ? KC : 1], sv[KC > 1 ? KC - 1 : 1];
+#pragma unroll
+        for (int k = 0; k < KC; ++k) wv[k] = w[(long)c * KC + k];
+#pragma unroll
+        for (int k = 0; k < KC - 1; ++k) sv[k] = st[k];
+#pragma unroll
+        for (int k = 0; k < KC - 1; ++k) acc = fmaf(wv[k], sv[k], acc);
+        acc = fmaf(wv[KC - 1], xn, acc);
+#pragma unroll
+        for (int k = 0; k + 1 < KC - 1; ++k) st[k] = sv[k + 1];
+        if (KC > 1) st[KC - 2] = xn;
+    } else {
+        for (int k = 0; k < K - 1; ++k) acc = fmaf(w[(long)c * K + k], st[k], acc);
+        acc = fmaf(w[(long)c * K + K - 1], xn, acc);
+        for (int k = 0; k + 1 < K - 1; ++k) st[k] = st[k + 1];
+        if (K > 1) st[K - 2] = xn;
+    }
     y[(long)b * ldy + c] = silu ? ssm::silu_fast(acc) : acc;
 }
 
@@ -214,7 +233,13 @@ extern "C" ssm_status ssm_conv1d_update(const float* x, long ldx, const float* w
                 "ssm_conv1d_update: bad shape");
     if (B == 0 || C == 0) return SSM_OK;
     const long n = (long)B * C;
-    conv1d_update_kernel<<<(unsigned)ssm::cdiv(n, 256), 256, 0, (hipStream_t)stream>>>(
-        x, ldx, w, bias, y, ldy, state, B, C, K, silu);
+    const unsigned grid = (unsigned)ssm::cdiv(n, 256);
+    hipStream_t st = (hipStream_t)stream;
+    switch (K) {
+        case 2: conv1d_update_kernel<2><<<grid, 256, 0, st>>>(x, ldx, w, bias, y, ldy, state, B, C, K, silu); break;
+        case 3: conv1d_update_kernel<3><<<grid, 256, 0, st>>>(x, ldx, w, bias, y, ldy, state, B, C, K, silu); break;
+        case 4: conv1d_update_kernel<4><<<grid, 256, 0, st>>>(x, ldx, w, bias, y, ldy, state, B, C, K, silu); break;
+        default: conv1d_update_kernel<0><<<grid, 256, 0, st>>>(x, ldx, w, bias, y, ldy, state, B, C, K, silu); break;
+    }
     return ssm::check_launch("conv1d_update");
 }

@@ -79,7 +79,7 @@ __global__ void gather_rows_kernel(const float* __restrict__ x, long row_stride,
 
 // Greedy pick: largest logit, lowest index among equal maxima (the order a stable
 // descending sort gives, src/session/streaming.ts:74-75). NaN never wins. One 1024-thread
-// workgroup per row: float4 loads unrolled 8 deep keep a whole vocabulary row (32000 logits
+// workgroup per row: groups of eight float4 loads keep a whole vocabulary row (32000 logits
 // = 128 KB) in flight at once; each thread scans ascending indices, then wave shuffles and
 // LDS combine (value, index) pairs.
 constexpr int kArgBlock = 1024;
@@ -100,16 +100,28 @@ __global__ __launch_bounds__(kArgBlock) void argmax_kernel(const float* __restri
     float best = -INFINITY;
     int bi = n;
     int tail = 0;
-    if (vec) {
+    if (vec && n >= 4) {
         const int n4 = n / 4;
         const float4* x4 = reinterpret_cast<const float4*>(xr);
-#pragma unroll 8
-        for (int i = threadIdx.x; i < n4; i += kArgBlock) {
-            const float4 v = x4[i];
-            arg_take(v.x, 4 * i, best, bi, n);
-            arg_take(v.y, 4 * i + 1, best, bi, n);
-            arg_take(v.z, 4 * i + 2, best, bi, n);
-            arg_take(v.w, 4 * i + 3, best, bi, n);
+        // eight loads per group from clamped (in-bounds) addresses, all in flight before the
+        // first is used; a branch around each load would wait for it before the next
+        for (int g = threadIdx.x; g < n4; g += 8 * kArgBlock) {
+            float4 v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int i = g + q * kArgBlock;
+                v[q] = x4[i < n4 ? i : n4 - 1];
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int i = g + q * kArgBlock;
+                if (i < n4) {
+                    arg_take(v[q].x, 4 * i, best, bi, n);
+                    arg_take(v[q].y, 4 * i + 1, best, bi, n);
+                    arg_take(v[q].z, 4 * i + 2, best, bi, n);
+                    arg_take(v[q].w, 4 * i + 3, best, bi, n);
+                }
+            }
         }
         tail = 4 * n4;
     }

@@ -38,6 +38,9 @@ constexpr int kTileN = 64;       // output columns per workgroup
 constexpr int kKB = 32;          // K per block
 constexpr int kPitch = kKB + 4;  // LDS row pitch (floats)
 constexpr int kMaxSplit = 16;
+// The finishing kernels read all kMaxSplit slots from clamped (in-bounds) slice indices and
+// mask the unused ones afterwards: with `s < S ? load : 0` the compiler put each load behind
+// its own branch and waited for it before issuing the next.
 constexpr int kTargetWG = 256;   // (tile, slice) workgroups worth splitting K for
 
 enum { MODE_PLAIN = 0, MODE_RMS = 1, MODE_GATED = 2 };
@@ -397,10 +400,10 @@ __global__ __launch_bounds__(256) void rowgemm_direct_reduce(RgArgs a) {
     const float* pm = a.part + (long)m * a.N + n;
     float pv[kMaxSplit];
 #pragma unroll
-    for (int s = 0; s < kMaxSplit; ++s) pv[s] = s < a.S ? pm[s * MN] : 0.f;
+    for (int s = 0; s < kMaxSplit; ++s) pv[s] = pm[(s < a.S ? s : 0) * MN];   // clamped
     float v = 0.f;
 #pragma unroll
-    for (int s = 0; s < kMaxSplit; ++s) v += pv[s];
+    for (int s = 0; s < kMaxSplit; ++s) v += s < a.S ? pv[s] : 0.f;
     v *= rs;
     float* yp = a.Y + (long)m * a.ldy + n;
     if (a.beta != 0.f) v = fmaf(a.beta, *yp, v);
@@ -418,14 +421,15 @@ __global__ __launch_bounds__(256) void rowgemm_reduce(RgArgs a) {
     float pv[kMaxSplit], tv[kMaxSplit];
 #pragma unroll
     for (int s = 0; s < kMaxSplit; ++s) {
-        pv[s] = s < a.S ? a.part[s * MN + i] : 0.f;
-        tv[s] = (MODE != MODE_PLAIN && s < a.S) ? a.ssqp[(long)s * a.M + m] : 0.f;
+        const int sc = s < a.S ? s : 0;   // clamped, not branched
+        pv[s] = a.part[sc * MN + i];
+        tv[s] = MODE != MODE_PLAIN ? a.ssqp[(long)sc * a.M + m] : 0.f;
     }
     float v = 0.f, t = 0.f;
 #pragma unroll
     for (int s = 0; s < kMaxSplit; ++s) {
-        v += pv[s];
-        t += tv[s];
+        v += s < a.S ? pv[s] : 0.f;
+        t += s < a.S ? tv[s] : 0.f;
     }
     if (MODE != MODE_PLAIN) v *= rsqrtf(t / (float)a.K + a.eps);
     float* yp = a.Y + (long)m * a.ldy + n;
@@ -454,10 +458,10 @@ __global__ __launch_bounds__(1024) void rowgemm_reduce_norm(RgArgs a, const floa
     } else if (MODE != MODE_PLAIN) {
         float tv[kMaxSplit];
 #pragma unroll
-        for (int s = 0; s < kMaxSplit; ++s) tv[s] = s < a.S ? a.ssqp[(long)s * a.M + m] : 0.f;
+        for (int s = 0; s < kMaxSplit; ++s) tv[s] = a.ssqp[(long)(s < a.S ? s : 0) * a.M + m];
         float t = 0.f;
 #pragma unroll
-        for (int s = 0; s < kMaxSplit; ++s) t += tv[s];
+        for (int s = 0; s < kMaxSplit; ++s) t += s < a.S ? tv[s] : 0.f;
         rs = rsqrtf(t / (float)a.K + a.eps);
     }
     const float* pm = a.part + (long)m * a.N;
@@ -466,10 +470,10 @@ __global__ __launch_bounds__(1024) void rowgemm_reduce_norm(RgArgs a, const floa
     for (int n = tid; n < a.N; n += 1024) {
         float pv[kMaxSplit];
 #pragma unroll
-        for (int s = 0; s < kMaxSplit; ++s) pv[s] = s < a.S ? pm[s * MN + n] : 0.f;
+        for (int s = 0; s < kMaxSplit; ++s) pv[s] = pm[(s < a.S ? s : 0) * MN + n];   // clamped
         float v = 0.f;
 #pragma unroll
-        for (int s = 0; s < kMaxSplit; ++s) v += pv[s];
+        for (int s = 0; s < kMaxSplit; ++s) v += s < a.S ? pv[s] : 0.f;
         v *= rs;
         if (a.beta != 0.f) v = fmaf(a.beta, ym[n], v);
         ym[n] = v;
