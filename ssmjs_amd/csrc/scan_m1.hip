@@ -260,15 +260,31 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
     const float xx = x[(long)b * ldx + d];
     const float du = dl * xx;
     float* hp = h + i * Nr;
+    // per group of up to 16 states: all loads first, from clamped (in-bounds) indices, then
+    // the arithmetic; loads behind a per-n branch were each waited for before the next
+    constexpr int G = N < 16 ? N : 16;
     float acc = 0.f;
 #pragma unroll
-    for (int n = 0; n < N; ++n)
-        if (n < Nr) {
-            const float v = fmaf(ssm::ex2(dl * A[(long)d * Nr + n] * ssm::kLog2e), hp[n],
-                                 du * Bm[(long)b * ldb + n]);
-            hp[n] = v;
-            acc = fmaf(v, Cm[(long)b * ldc + n], acc);
+    for (int n0 = 0; n0 < N; n0 += G) {
+        if (n0 >= Nr) break;
+        float hv[G], av[G], bv[G], cv[G];
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            const int nn = n0 + q < Nr ? n0 + q : Nr - 1;
+            hv[q] = hp[nn];
+            av[q] = A[(long)d * Nr + nn];
+            bv[q] = Bm[(long)b * ldb + nn];
+            cv[q] = Cm[(long)b * ldc + nn];
         }
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            const float v = fmaf(ssm::ex2(dl * av[q] * ssm::kLog2e), hv[q], du * bv[q]);
+            if (n0 + q < Nr) {
+                hp[n0 + q] = v;
+                acc = fmaf(v, cv[q], acc);
+            }
+        }
+    }
     if (Dsk) acc = fmaf(Dsk[d], xx, acc);
     if (z) acc *= ssm::silu_fast(z[(long)b * ldz + d]);
     y[(long)b * ldy + d] = acc;
