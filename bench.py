@@ -9,7 +9,8 @@ Workloads (--workload picks one, default cfg2):
         conv/SiLU -> x_proj/dt_proj -> scan (D skip, SiLU(z) gate) -> out_proj)
   cfg3  Mamba-2 SSD prefill core, B=8 L=4096 H=64 P=64 N=128 G=1; --dtype f32|bf16
   cfg4  Mamba-2 24-layer decode, d=1024 H=32 P=64 N=128 V=32000, 64 cached sequences,
-        one greedy step (24 layers + LM head + argmax) per bench step, fp32
+        one greedy step (24 layers + LM head + argmax) per bench step, fp32; --sampling
+        draws the token with sampleToken on the device instead (T 0.8, topK 50, topP 0.9)
   cfg5  Mamba-2 SSD long-context prefill core, B=1 L=65536 H=32 P=64 N=128, bf16
 A step is one pass of the path over one batch of synthetic input that is already resident in
 HBM. Timing: W untimed warmup steps, then K steps between HIP events on the stream the
@@ -60,6 +61,9 @@ def parse():
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "copy"])
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sampling", action="store_true",
+                    help="cfg4: draw each token with sampleToken on the device (temperature "
+                         "0.8, topK 50, topP 0.9) instead of the greedy argmax")
     return ap.parse_args()
 
 
@@ -346,13 +350,25 @@ def w_cfg4(torch, np, dev, args):
     nxt = torch.empty(Bsz, dtype=torch.int32, device="cuda")
     bufs = [ids, nxt]
     k = [0]
+    steps, warm = args.steps or 256, args.warmup if args.warmup is not None else 8
+    samp = (0.8, 50, 0.9)   # the reference's default sampling (session.ts complete())
+    if args.sampling:
+        from ssmjs_amd import kernels
+        logits = torch.empty(Bsz, V, device="cuda")
+        draws = torch.from_numpy(r.random((steps + warm + 64, Bsz))).cuda()
+        sws = kernels.sample_workspace(Bsz, V, "cuda")
 
     def step():
         a, b = bufs[k[0] % 2], bufs[(k[0] + 1) % 2]
-        _lib.call("ssm_decode_step_device", m.handle, st._h, a.data_ptr(), None, b.data_ptr())
+        if args.sampling:
+            _lib.call("ssm_decode_step_device", m.handle, st._h, a.data_ptr(),
+                      logits.data_ptr(), None)
+            kernels.sample(logits, draws[k[0] % draws.shape[0]], *samp, out=b, workspace=sws)
+        else:
+            _lib.call("ssm_decode_step_device", m.handle, st._h, a.data_ptr(), None,
+                      b.data_ptr())
         k[0] += 1
 
-    steps, warm = args.steps or 256, args.warmup if args.warmup is not None else 8
     ms = timed(torch, step, steps, warm)
     stg = profiled_stages(dev, torch, step, min(steps, 32))
     D, P = 2 * d, 64
@@ -378,8 +394,10 @@ def w_cfg4(torch, np, dev, args):
     dom = max(stages.values(), key=lambda r_: r_["avg_ms"])
     out = {"value": Bsz / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
            "dtype": "f32",
-           "config": {"workload": "cfg4: Mamba-2 24-layer recurrent decode, one greedy token "
-                                  "for each of 64 cached sequences per step",
+           "config": {"workload": "cfg4: Mamba-2 24-layer recurrent decode, one "
+                                  + ("sampled (device sampleToken, T 0.8 topK 50 topP 0.9)"
+                                     if args.sampling else "greedy")
+                                  + " token for each of 64 cached sequences per step",
                       "batch": Bsz, "d_model": d, "layers": nl, "heads": H, "head_dim": P,
                       "d_state": N, "vocab": V, "tokens_per_step": Bsz},
            "roofline": dom, "stages": stages,
