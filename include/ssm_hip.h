@@ -191,7 +191,8 @@ ssm_status ssm_argmax(const float* x, long ldx, int rows, int n, uint32_t* out, 
  * (equal exps: lower index first); the nucleus ends at the first cumulative exp/sumE >=
  * topP; the pick is the first nucleus entry whose running exp sum reaches u * (nucleus
  * sum). Needs 1 <= n <= 262144 and min(topK, n) <= 1024 (SSM_ERR_UNSUPPORTED otherwise) and
- * topK >= 1. Logits must be finite. workspace: device memory of ssm_sample_workspace(rows,
+ * topK >= 1. Logits may be -inf (e = 0, as in the reference) but not NaN or +inf, and a
+ * row needs one finite logit. workspace: device memory of ssm_sample_workspace(rows,
  * n) bytes (scaled values, keys, slice maxima and sums), one stream at a time. */
 size_t ssm_sample_workspace(int rows, int n);
 ssm_status ssm_sample(const float* logits, long ld, int rows, int n, double temperature,

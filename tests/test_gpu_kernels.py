@@ -380,7 +380,8 @@ def test_argmax_ties_nan_and_tails(n, pad):
 def _sample_rows(r, rows, n):
     """Logit rows of several kinds: heavy exact ties (more equal to the K-th value than the
     candidate list holds), near-ties (small scale: rounded exps collide), wide spread, a
-    plateau of up to 100 equal maxima (more candidates than topK), and one constant row."""
+    plateau of up to 100 equal maxima (more candidates than topK), rows with -inf (masked)
+    logits, and one constant row."""
     x = np.empty((rows, n), np.float32)
     for i in range(rows):
         k = i % 5
@@ -395,6 +396,8 @@ def _sample_rows(r, rows, n):
             x[i, r.choice(n, min(n, 100), replace=False)] = 5.0
         else:
             x[i] = r.standard_normal(n)
+            x[i, r.random(n) < 0.3] = -np.inf   # masked tokens: e = 0
+            x[i, 0] = 1.0                        # at least one finite logit
     x[rows - 1] = 0.25
     return x
 

@@ -327,6 +327,9 @@ def test_sample_token_agrees_with_host_restatement(n):
             lg = r.integers(-3, 3, n).astype(np.float32) * 0.5   # heavy ties
         else:
             lg = (r.standard_normal(n) * (0.05 if trial % 3 == 1 else 3.0)).astype(np.float32)
+        if trial % 4 == 3 and n > 1:
+            lg[r.random(n) < 0.3] = -np.inf     # masked tokens: e = 0
+            lg[0] = 0.5
         T = [1.0, 0.8, 2.5, 1e-9][trial % 4]
         K = [1, 2, 50, n, n + 5, 1024][trial % 6]
         P = [0.9, 1.0, 0.5, 0.0][(trial // 2) % 4]
