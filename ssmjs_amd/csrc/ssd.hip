@@ -802,22 +802,41 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
     }
 }
 
+constexpr int kSeqT = 64;         // most time steps per LDS round of the sequential kernel
+constexpr int kSeqItems = 4096;   // most x (and B, C) values per round: 16 per thread
+
+__host__ __device__ inline int seq_steps(int Pd, int N) {
+    const int w = Pd > N ? Pd : N;
+    const int t = kSeqItems / w;
+    return t < kSeqT ? (t > 0 ? t : 1) : kSeqT;
+}
+
 // Sequential SSD for shapes outside the MFMA kernel (head dim != 64 or d_state not 64/128):
 // the one-token update above run over the L steps of a (b, h) sequence with the state in
-// registers. Each thread owns RPT rows of the state (RPT <= 8) in float4 columns.
+// registers. Each thread owns RPT rows of the state (RPT <= 8) in float4 columns. The
+// steps' inputs come through LDS, kSeqT steps per round, fetched one round ahead.
 template <typename TIN, int LPR>
 __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, int Pd) {
     constexpr int RPP = 256 / LPR;
     constexpr int MAXR = 8;
+    constexpr int MAXX = kSeqItems / 256;    // x values per thread and round
+    constexpr int MAXBC = kSeqItems / 256;   // B (and C) values per thread and round
+    extern __shared__ float seq_smem[];
     const int bh = blockIdx.x;
     const int h = bh % a.H, b = bh / a.H, g = h / (a.H / a.G);
     const int tid = threadIdx.x, c4 = tid % LPR, rsub = tid / LPR;
-    const int N = a.N;
+    const int N = a.N, L = a.L;
+    const int T = seq_steps(Pd, N);   // time steps staged per round
     const bool col_ok = 4 * c4 < N;
-    const TIN* X = reinterpret_cast<const TIN*>(a.x);
+    const TIN* X = reinterpret_cast<const TIN*>(a.x) + (long)h * Pd;
     const TIN* Bp = reinterpret_cast<const TIN*>(a.Bm) + (long)g * N;
     const TIN* Cp = reinterpret_cast<const TIN*>(a.Cm) + (long)g * N;
     const float Ah = a.A[h], dtb = a.dt_bias ? a.dt_bias[h] : 0.f, Dh = a.Dsk ? a.Dsk[h] : 0.f;
+    const long rb = (long)b * L;
+    float* xs = seq_smem;          // [T][Pd]
+    float* bs = xs + T * Pd;       // [T][N]
+    float* cs = bs + T * N;        // [T][N]
+    float* ds = cs + T * N;        // [T]: dt'
     float4 st[MAXR];
 #pragma unroll
     for (int k = 0; k < MAXR; ++k) {
@@ -828,35 +847,86 @@ __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, int Pd) {
             st[k] = make_float4(src[0], src[1], src[2], src[3]);
         }
     }
-    for (int t = 0; t < a.L; ++t) {
-        const long r = (long)b * a.L + t;
-        float dl = a.dt[r * a.lddt + h] + dtb;
-        if (a.softplus) dl = ssm::softplus(dl);
-        dl = fminf(fmaxf(dl, a.dt_min), a.dt_max);
-        const float dA = ssm::ex2(dl * Ah * ssm::kLog2e);
-        float bv[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (col_ok)
+
+    // The inputs of T steps are fetched into registers by the whole workgroup (clamped
+    // indices, no branches, so every load is in flight at once), then staged in LDS; the
+    // sequential steps read LDS while the next round's loads are in flight.
+    float px[MAXX], pb[MAXBC], pc[MAXBC], pdt = 0.f;
+    auto fetch = [&](int t0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                bv[i] = ld1<TIN>(Bp + r * a.ldb + 4 * c4 + i);
-                cv[i] = ld1<TIN>(Cp + r * a.ldc + 4 * c4 + i);
-            }
-#pragma unroll
-        for (int k = 0; k < MAXR; ++k) {
-            const int p = rsub + k * RPP;
-            if (p >= Pd) break;
-            const float xp = ld1<TIN>(X + r * a.ldx + (long)h * Pd + p);
-            const float dx = dl * xp;
-            float4& v = st[k];
-            v.x = fmaf(dA, v.x, dx * bv[0]);
-            v.y = fmaf(dA, v.y, dx * bv[1]);
-            v.z = fmaf(dA, v.z, dx * bv[2]);
-            v.w = fmaf(dA, v.w, dx * bv[3]);
-            float acc = v.x * cv[0] + v.y * cv[1] + v.z * cv[2] + v.w * cv[3];
-#pragma unroll
-            for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
-            if (c4 == 0) a.y[r * a.ldy + (long)h * Pd + p] = fmaf(Dh, xp, acc);
+        for (int i = 0; i < MAXX; ++i) {
+            int e = tid + 256 * i;
+            e = e < T * Pd ? e : T * Pd - 1;
+            const int t = min(t0 + e / Pd, L - 1);
+            px[i] = ld1<TIN>(X + (rb + t) * a.ldx + e % Pd);
         }
+#pragma unroll
+        for (int i = 0; i < MAXBC; ++i) {
+            int e = tid + 256 * i;
+            e = e < T * N ? e : T * N - 1;
+            const int t = min(t0 + e / N, L - 1);
+            pb[i] = ld1<TIN>(Bp + (rb + t) * a.ldb + e % N);
+            pc[i] = ld1<TIN>(Cp + (rb + t) * a.ldc + e % N);
+        }
+        pdt = a.dt[(rb + min(t0 + (tid < T ? tid : 0), L - 1)) * a.lddt + h];
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < MAXX; ++i)
+            if (tid + 256 * i < T * Pd) xs[tid + 256 * i] = px[i];
+#pragma unroll
+        for (int i = 0; i < MAXBC; ++i)
+            if (tid + 256 * i < T * N) {
+                bs[tid + 256 * i] = pb[i];
+                cs[tid + 256 * i] = pc[i];
+            }
+        if (tid < T) {
+            float dl = pdt + dtb;
+            if (a.softplus) dl = ssm::softplus(dl);
+            ds[tid] = fminf(fmaxf(dl, a.dt_min), a.dt_max);
+        }
+    };
+    if (L > 0) {   // (L = 0 passes h0 through to hT)
+        fetch(0);
+        stage();
+        __syncthreads();
+    }
+    const int cb = col_ok ? 4 * c4 : 0;
+    for (int t0 = 0; t0 < L; t0 += T) {
+        fetch(t0 + T < L ? t0 + T : t0);   // the last round refetches its own inputs
+        const int tn = min(T, L - t0);
+        // unrolled so that the LDS reads, exp2 and output reductions of neighbouring steps
+        // overlap; only the state update chains from step to step
+#pragma unroll 4
+        for (int tt = 0; tt < tn; ++tt) {
+            const float dl = ds[tt];
+            const float dA = ssm::ex2(dl * Ah * ssm::kLog2e);
+            const float4 bq = *reinterpret_cast<const float4*>(bs + tt * N + cb);
+            const float4 cq = *reinterpret_cast<const float4*>(cs + tt * N + cb);
+            const float bv[4] = {col_ok ? bq.x : 0.f, col_ok ? bq.y : 0.f, col_ok ? bq.z : 0.f,
+                                 col_ok ? bq.w : 0.f};
+            const float cv[4] = {cq.x, cq.y, cq.z, cq.w};
+            const long r = rb + t0 + tt;
+#pragma unroll
+            for (int k = 0; k < MAXR; ++k) {
+                const int p = rsub + k * RPP;
+                if (p >= Pd) break;
+                const float xp = xs[tt * Pd + p];
+                const float dx = dl * xp;
+                float4& v = st[k];
+                v.x = fmaf(dA, v.x, dx * bv[0]);
+                v.y = fmaf(dA, v.y, dx * bv[1]);
+                v.z = fmaf(dA, v.z, dx * bv[2]);
+                v.w = fmaf(dA, v.w, dx * bv[3]);
+                float acc = v.x * cv[0] + v.y * cv[1] + v.z * cv[2] + v.w * cv[3];
+#pragma unroll
+                for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+                if (c4 == 0) a.y[r * a.ldy + (long)h * Pd + p] = fmaf(Dh, xp, acc);
+            }
+        }
+        __syncthreads();
+        stage();
+        __syncthreads();
     }
     if (a.hT) {
 #pragma unroll
@@ -881,14 +951,15 @@ ssm_status launch_ssd_seq(SsdArgs& a, int Pd, hipStream_t st) {
         return ssm::fail(SSM_ERR_UNSUPPORTED, "ssd: head dim %d with d_state %d is too large", Pd,
                          a.N);
     const unsigned grid = (unsigned)(a.B * a.H);
+    const size_t smem = sizeof(float) * (size_t)seq_steps(Pd, a.N) * (Pd + 2 * a.N + 1);
     switch (L2) {
-        case 1: ssd_seq_kernel<TIN, 1><<<grid, 256, 0, st>>>(a, Pd); break;
-        case 2: ssd_seq_kernel<TIN, 2><<<grid, 256, 0, st>>>(a, Pd); break;
-        case 4: ssd_seq_kernel<TIN, 4><<<grid, 256, 0, st>>>(a, Pd); break;
-        case 8: ssd_seq_kernel<TIN, 8><<<grid, 256, 0, st>>>(a, Pd); break;
-        case 16: ssd_seq_kernel<TIN, 16><<<grid, 256, 0, st>>>(a, Pd); break;
-        case 32: ssd_seq_kernel<TIN, 32><<<grid, 256, 0, st>>>(a, Pd); break;
-        default: ssd_seq_kernel<TIN, 64><<<grid, 256, 0, st>>>(a, Pd); break;
+        case 1: ssd_seq_kernel<TIN, 1><<<grid, 256, smem, st>>>(a, Pd); break;
+        case 2: ssd_seq_kernel<TIN, 2><<<grid, 256, smem, st>>>(a, Pd); break;
+        case 4: ssd_seq_kernel<TIN, 4><<<grid, 256, smem, st>>>(a, Pd); break;
+        case 8: ssd_seq_kernel<TIN, 8><<<grid, 256, smem, st>>>(a, Pd); break;
+        case 16: ssd_seq_kernel<TIN, 16><<<grid, 256, smem, st>>>(a, Pd); break;
+        case 32: ssd_seq_kernel<TIN, 32><<<grid, 256, smem, st>>>(a, Pd); break;
+        default: ssd_seq_kernel<TIN, 64><<<grid, 256, smem, st>>>(a, Pd); break;
     }
     return ssm::check_launch("ssd_seq");
 }
