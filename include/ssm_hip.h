@@ -131,9 +131,12 @@ ssm_status ssm_m1_state_update(const float* x, long ldx, const float* dt, long l
  *   S_t = exp(dt'_t A_h) S_{t-1} + dt'_t x_t B_t^T  (P x N);  y_t = S_t C_t + Dsk_h x_t.
  * x: (B,L,H,P) elements of `in_dtype` with row stride ldx; dt: (B,L,H) float, row stride
  * lddt; Bm, Cm: (B,L,G,N) of `in_dtype`, row strides ldb/ldc; y: (B,L,H,P) float, ldy;
- * h0/hT: (B,H,P,N) float (may be NULL). P = 64 and N in {64, 128} on this backend.
- * The chunk length of the reference config (chunkLen) does not change the result; the
- * kernel uses its own internal chunk. `workspace` holds ssm_ssd_workspace(...) bytes. */
+ * h0/hT: (B,H,P,N) float (may be NULL). P = 64 with N in {64, 128} runs the fused MFMA
+ * kernel. Other shapes: with G = 1, N <= 64, float inputs, a dt clamp that cannot bind and
+ * the workspace, the Mamba-1 chunked scan over H*P channels; otherwise a sequential kernel
+ * (no workspace needed). The chunk length of the reference config (chunkLen) does not change
+ * the result; the kernel uses its own internal chunk. `workspace` holds
+ * ssm_ssd_workspace(...) bytes. */
 size_t ssm_ssd_workspace(int B, int L, int H, int P, int G, int N);
 ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, const float* dt, long lddt,
                               const float* dt_bias, int softplus, float dt_min, float dt_max,

@@ -895,9 +895,6 @@ __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, int Pd) {
     for (int t0 = 0; t0 < L; t0 += T) {
         fetch(t0 + T < L ? t0 + T : t0);   // the last round refetches its own inputs
         const int tn = min(T, L - t0);
-        // unrolled so that the LDS reads, exp2 and output reductions of neighbouring steps
-        // overlap; only the state update chains from step to step
-#pragma unroll 4
         for (int tt = 0; tt < tn; ++tt) {
             const float dl = ds[tt];
             const float dA = ssm::ex2(dl * Ah * ssm::kLog2e);
@@ -964,11 +961,51 @@ ssm_status launch_ssd_seq(SsdArgs& a, int Pd, hipStream_t st) {
     return ssm::check_launch("ssd_seq");
 }
 
+// Shapes outside the MFMA kernel with one group, d_state <= 64 and fp32 inputs run as the
+// Mamba-1 chunked scan over D = H*P channels: channel h*P + p has dt[b, t, h], A[h] for every
+// state, dt_bias[h] and D[h], and every channel reads the same B and C. This kernel writes
+// those per-channel copies to the workspace (dt: (B, L, D); A: (D, N); bias, D: (D)).
+__global__ void ssd_expand_kernel(const float* __restrict__ dt, long lddt,
+                                  const float* __restrict__ dt_bias, const float* __restrict__ A,
+                                  const float* __restrict__ Dsk, int B, int L, int H, int Pd,
+                                  int N, float* __restrict__ dte, float* __restrict__ Ae,
+                                  float* __restrict__ be, float* __restrict__ De) {
+    const long D = (long)H * Pd;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long nt = (long)B * L * D;
+    if (i < nt) {
+        const long r = i / D;
+        const int h = (int)((i % D) / Pd);
+        dte[i] = dt[r * lddt + h];
+    } else if (i < nt + D * N) {
+        const long k = i - nt;
+        Ae[k] = A[(k / N) / Pd];
+    } else if (i < nt + D * N + D) {
+        const long d = i - nt - D * N;
+        be[d] = dt_bias ? dt_bias[d / Pd] : 0.f;
+        De[d] = Dsk ? Dsk[d / Pd] : 0.f;
+    }
+}
+
+size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace of the chunked fallback: the copies above, then the scan's own workspace.
+size_t chunked_fallback_bytes(int B, int L, int H, int Pd, int N) {
+    const size_t D = (size_t)H * Pd;
+    return up256(sizeof(float) * (size_t)B * L * D) + up256(sizeof(float) * D * N) +
+           2 * up256(sizeof(float) * D) + ssm_selective_scan_workspace(B, L, (int)D, N);
+}
+
+bool chunked_fallback_shape(int Pd, int G, int N) {
+    return !(Pd == P && (N == 64 || N == 128)) && G == 1 && N <= 64;
+}
+
 }  // namespace
 
 extern "C" size_t ssm_ssd_workspace(int B, int L, int H, int Pd, int G, int N) {
-    (void)G;
-    if (B <= 0 || L <= 0 || H <= 0 || Pd != P || (N != 64 && N != 128)) return 0;
+    if (B <= 0 || L <= 0 || H <= 0 || Pd <= 0 || N <= 0) return 0;
+    if (chunked_fallback_shape(Pd, G, N)) return chunked_fallback_bytes(B, L, H, Pd, N);
+    if (Pd != P || (N != 64 && N != 128)) return 0;
     int nchunks, nseg, per;
     plan(B, L, H, nchunks, nseg, per);
     if (nseg <= 1) return 0;
@@ -1005,7 +1042,7 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
     if (B == 0) return SSM_OK;
     if (L == 0) {
         if (hT) {
-            const size_t bytes = sizeof(float) * (size_t)B * H * P * N;
+            const size_t bytes = sizeof(float) * (size_t)B * H * Pd * N;
             if (h0) SSM_HIP_TRY(hipMemcpyAsync(hT, h0, bytes, hipMemcpyDeviceToDevice,
                                                (hipStream_t)stream));
             else SSM_HIP_TRY(hipMemsetAsync(hT, 0, bytes, (hipStream_t)stream));
@@ -1018,6 +1055,30 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
     a.ldc = ldc; a.Dsk = Dsk; a.y = y; a.ldy = ldy; a.B = B; a.L = L; a.H = H; a.G = G; a.N = N;
     a.h0 = h0; a.hT = hT;
     hipStream_t st = (hipStream_t)stream;
+    // the Mamba-1 scan has no dt clamp: it stands in when the clamp cannot bind
+    const bool no_clamp = (softplus && dt_min <= 0.f && dt_max == INFINITY) ||
+                          (dt_min == -INFINITY && dt_max == INFINITY);
+    if (!mfma_path && in_dtype == SSM_F32 && no_clamp && chunked_fallback_shape(Pd, G, N) &&
+        workspace && workspace_bytes >= chunked_fallback_bytes(B, L, H, Pd, N)) {
+        const long D = (long)H * Pd;
+        char* p = (char*)workspace;
+        float* dte = (float*)p;
+        p += up256(sizeof(float) * (size_t)B * L * D);
+        float* Ae = (float*)p;
+        p += up256(sizeof(float) * (size_t)D * N);
+        float* be = (float*)p;
+        p += up256(sizeof(float) * (size_t)D);
+        float* De = (float*)p;
+        p += up256(sizeof(float) * (size_t)D);
+        const long n = (long)B * L * D + D * N + D;
+        ssd_expand_kernel<<<(unsigned)ssm::cdiv(n, 256), 256, 0, st>>>(
+            dt, lddt, dt_bias, A, Dsk, B, L, H, Pd, N, dte, Ae, be, De);
+        SSM_HIP_TRY(hipGetLastError());
+        const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+        return ssm_selective_scan((const float*)x, ldx, dte, D, be, softplus, Ae,
+                                  (const float*)Bm, ldb, (const float*)Cm, ldc, Dsk ? De : nullptr,
+                                  nullptr, 0, y, ldy, B, L, (int)D, N, h0, hT, p, rest, stream);
+    }
     if (!mfma_path)
         return in_dtype == SSM_F32 ? launch_ssd_seq<float>(a, Pd, st)
                                    : launch_ssd_seq<__bf16>(a, Pd, st);

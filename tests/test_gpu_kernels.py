@@ -257,17 +257,28 @@ def test_ssd_long_sequence_segments(dtype, H, L):
     assert e1 <= tol and e2 <= tol
 
 
-def test_ssd_sequential_fallback_shapes():
-    """head dim 16, d_state 16 (outside the MFMA kernel) -> sequential kernel."""
-    case("ssd fallback P=16 N=16")
-    r = rng(11)
-    B, L, H, G, N, P = 2, 45, 4, 1, 16, 16
+@pytest.mark.parametrize("B,L,H,G,N,P,path", [
+    (2, 45, 4, 1, 16, 16, "chunked"),      # one group, d_state <= 64: Mamba-1 chunked scan
+    (1, 700, 4, 1, 16, 64, "chunked"),     # the presets' Mamba-2 shape, many scan chunks
+    (2, 45, 4, 1, 16, 16, "sequential"),   # no workspace: the sequential kernel
+    (2, 50, 4, 2, 16, 32, "sequential"),   # two groups: the sequential kernel
+    (1, 40, 2, 1, 8, 128, "dtclamp"),      # dt clamp that binds: the sequential kernel
+])
+def test_ssd_fallback_shapes(B, L, H, G, N, P, path):
+    """Shapes outside the MFMA kernel (head dim != 64 or d_state not 64/128). With one group,
+    d_state <= 64, fp32 and a dt clamp that cannot bind they run as the Mamba-1 chunked scan
+    over H*P channels (given the workspace); otherwise the sequential kernel."""
+    case(f"ssd fallback B={B} L={L} H={H} G={G} N={N} P={P} {path}")
+    r = rng(11 + L)
     x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
     h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32)
-    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, h0=h0a, return_state=True)
+    lim = (0.05, 0.2) if path == "dtclamp" else (0.0, float("inf"))
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, h0=h0a, return_state=True, dt_min=lim[0],
+                    dt_max=lim[1])
     hd = torch.zeros(B, H, P, N, device="cuda")
+    ws = torch.empty(1, dtype=torch.uint8, device="cuda") if path == "sequential" else None
     y = K().ssd_chunk_scan(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), None, True,
-                           h0=dev(h0a), hT=hd)
+                           dt_min=lim[0], dt_max=lim[1], h0=dev(h0a), hT=hd, workspace=ws)
     assert err(host(y), ref) <= F32_TOL
     assert err(host(hd), hT) <= F32_TOL
 
