@@ -124,10 +124,9 @@ __global__ void scan_chunk_prefix(const float* __restrict__ A, int L, int D, int
         float he[kPre], sd[kPre];
 #pragma unroll
         for (int u = 0; u < kPre; ++u) {
-            // clamped (in bounds) rather than branched, so that the loads issue together
-            const int cu = c0 + u < NC ? c0 + u : NC - 1;
-            he[u] = p0[(long)cu * cstride];
-            sd[u] = s0[(long)cu * D];
+            const bool live = c0 + u < NC;
+            he[u] = live ? p0[(long)(c0 + u) * cstride] : 0.f;
+            sd[u] = live ? s0[(long)(c0 + u) * D] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < kPre; ++u) {
