@@ -252,7 +252,7 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
                                  long ldb, const float* __restrict__ Cm, long ldc,
                                  const float* __restrict__ Dsk, const float* __restrict__ z,
                                  long ldz, float* __restrict__ y, long ldy,
-                                 float* __restrict__ h, int B, int D, int Nr) {
+                                 float* __restrict__ h, int B, int D, int Nr, int vec) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)B * D) return;
     const int b = (int)(i / D), d = (int)(i % D);
@@ -260,10 +260,43 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
     const float xx = x[(long)b * ldx + d];
     const float du = dl * xx;
     float* hp = h + i * Nr;
-    // per group of up to 16 states: all loads first, from clamped (in-bounds) indices, then
-    // the arithmetic; loads behind a per-n branch were each waited for before the next
+    // per group of up to 16 states: all loads first, then the arithmetic. When the state
+    // count is the template's and the rows are 16-byte aligned (vec), h and A come in float4
+    // loads; otherwise from clamped (in-bounds) scalar indices. (Loads behind a per-n branch
+    // were each waited for before the next.)
     constexpr int G = N < 16 ? N : 16;
     float acc = 0.f;
+    if (Nr == N && vec) {
+#pragma unroll
+        for (int n0 = 0; n0 < N; n0 += G) {
+            float hv[G], av[G], bv[G], cv[G];
+#pragma unroll
+            for (int q = 0; q < G; q += 4) {
+                const float4 h4 = *reinterpret_cast<const float4*>(hp + n0 + q);
+                const float4 a4 = *reinterpret_cast<const float4*>(A + (long)d * N + n0 + q);
+                hv[q] = h4.x; hv[q + 1] = h4.y; hv[q + 2] = h4.z; hv[q + 3] = h4.w;
+                av[q] = a4.x; av[q + 1] = a4.y; av[q + 2] = a4.z; av[q + 3] = a4.w;
+            }
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+                bv[q] = Bm[(long)b * ldb + n0 + q];
+                cv[q] = Cm[(long)b * ldc + n0 + q];
+            }
+#pragma unroll
+            for (int q = 0; q < G; q += 4) {
+                float4 v;
+                v.x = fmaf(ssm::ex2(dl * av[q] * ssm::kLog2e), hv[q], du * bv[q]);
+                v.y = fmaf(ssm::ex2(dl * av[q + 1] * ssm::kLog2e), hv[q + 1], du * bv[q + 1]);
+                v.z = fmaf(ssm::ex2(dl * av[q + 2] * ssm::kLog2e), hv[q + 2], du * bv[q + 2]);
+                v.w = fmaf(ssm::ex2(dl * av[q + 3] * ssm::kLog2e), hv[q + 3], du * bv[q + 3]);
+                *reinterpret_cast<float4*>(hp + n0 + q) = v;
+                acc = fmaf(v.x, cv[q], acc);
+                acc = fmaf(v.y, cv[q + 1], acc);
+                acc = fmaf(v.z, cv[q + 2], acc);
+                acc = fmaf(v.w, cv[q + 3], acc);
+            }
+        }
+    } else
 #pragma unroll
     for (int n0 = 0; n0 < N; n0 += G) {
         if (n0 >= Nr) break;
@@ -362,9 +395,12 @@ extern "C" ssm_status ssm_m1_state_update(const float* x, long ldx, const float*
     const long n = (long)B * D;
     const unsigned g = (unsigned)ssm::cdiv(n, 256);
     hipStream_t st = (hipStream_t)stream;
+    // float4 access to h and A rows when N is a template size and the rows are aligned
+    const int vec = (N == 8 || N == 16 || N == 32 || N == 64) && (uintptr_t)h % 16 == 0 &&
+                    (uintptr_t)A % 16 == 0;
 #define M1U(NS)                                                                              \
     m1_update_kernel<NS><<<g, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus, A, Bm, ldb, \
-                                            Cm, ldc, Dsk, z, ldz, y, ldy, h, B, D, N)
+                                            Cm, ldc, Dsk, z, ldz, y, ldy, h, B, D, N, vec)
     if (N <= 8) M1U(8);
     else if (N <= 16) M1U(16);
     else if (N <= 32) M1U(32);
