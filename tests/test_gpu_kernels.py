@@ -283,6 +283,30 @@ def test_ssd_fallback_shapes(B, L, H, G, N, P, path):
     assert err(host(hd), hT) <= F32_TOL
 
 
+@pytest.mark.parametrize("P,N", [(64, 128), (16, 16), (128, 16)])
+def test_ssd_empty_sequence_passes_state_through(P, N):
+    """L = 0: hT is h0 (zeros without h0), for every head dim."""
+    case(f"ssd L=0 P={P} N={N}")
+    from ssmjs_amd import _lib
+    r = rng(14)
+    B, H, G = 2, 4, 1
+    dummy = torch.zeros(H * P + G * N, device="cuda")   # non-null, never read for L = 0
+    A, D = dev(-np.ones(H)), dev(np.ones(H))
+    h0 = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32)
+    hT = torch.full((B, H, P, N), 7.0, device="cuda")
+    for h0p in (dev(h0), None):
+        p = dummy.data_ptr()
+        _lib.call("ssm_ssd_chunk_scan", _lib.SSM_F32, p, H * P, p, H, None, 1, 0.0,
+                  float("inf"), A.data_ptr(), p, G * N, p, G * N, D.data_ptr(), p, H * P, B, 0,
+                  H, P, G, N, h0p.data_ptr() if h0p is not None else None, hT.data_ptr(), None,
+                  0, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        if h0p is not None:
+            assert np.array_equal(host(hT), h0)
+        else:
+            assert not host(hT).any()
+
+
 def test_ssd_chunk_equals_decode_steps():
     """Final state of a prefill == state reached by one-token updates (state passing)."""
     case("ssd prefill vs m2 updates")
