@@ -80,6 +80,12 @@ def _declare(L):
     L.orc_state_floats.restype = C.c_size_t
     L.orc_state_read.argtypes = [C.c_void_p, C.c_void_p, _fp]
     L.orc_state_write.argtypes = [C.c_void_p, C.c_void_p, _fp]
+    L.orc_num_threads.restype = C.c_int
+
+
+def num_threads() -> int:
+    """Threads of the oracle's OpenMP loops (OMP_NUM_THREADS, else every host core)."""
+    return int(lib().orc_num_threads())
 
 
 def _f(a):

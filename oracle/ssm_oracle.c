@@ -11,6 +11,19 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Threads the parallel loops use (1 without OpenMP). Every output element is computed by one
+ * thread in a fixed order, so results do not depend on the thread count. */
+int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
 
 static double softplus_d(double x) { return x > 20.0 ? x : log1p(exp(x)); }
 static double silu_d(double x) { return x / (1.0 + exp(-x)); }
@@ -23,6 +36,7 @@ void orc_causal_conv1d(const float* x, long ldx, const float* w, const float* bi
     for (int b = 0; b < B; ++b) {
         const float* xb = x + (long)b * L * ldx;
         float* yb = y + (long)b * L * ldy;
+#pragma omp parallel for schedule(static)
         for (int t = 0; t < L; ++t) {
             for (int c = 0; c < C; ++c) {
                 double acc = bias ? bias[c] : 0.0;
@@ -72,7 +86,10 @@ void orc_selective_scan(const float* u, long ldu, const float* dt, long lddt,
                         const float* Bm, long ldb, const float* Cm, long ldc,
                         const float* Dsk, const float* z, long ldz, float* y, long ldy,
                         int B, int L, int D, int N, const float* h0, float* hT) {
+#pragma omp parallel
+    {
     double* h = (double*)malloc(sizeof(double) * N);
+#pragma omp for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int d = 0; d < D; ++d) {
             for (int n = 0; n < N; ++n) h[n] = h0 ? h0[((long)b * D + d) * N + n] : 0.0;
@@ -95,11 +112,13 @@ void orc_selective_scan(const float* u, long ldu, const float* dt, long lddt,
                 for (int n = 0; n < N; ++n) hT[((long)b * D + d) * N + n] = (float)h[n];
         }
     free(h);
+    }
 }
 
 void orc_m1_state_update(const float* x, const float* dt, const float* dt_bias, int softplus,
                          const float* A, const float* Bm, const float* Cm, const float* Dsk,
                          const float* z, float* y, float* h, int B, int D, int N) {
+#pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int d = 0; d < D; ++d) {
             double delta = dt[(long)b * D + d] + (dt_bias ? dt_bias[d] : 0.0);
@@ -135,7 +154,10 @@ void orc_ssd_sequential(const float* x, long ldx, const float* dt, long lddt,
                         int B, int L, int H, int P, int G, int N,
                         const float* h0, float* hT) {
     int hpg = H / G;
+#pragma omp parallel
+    {
     double* h = (double*)malloc(sizeof(double) * (size_t)P * N);
+#pragma omp for collapse(2) schedule(dynamic)
     for (int b = 0; b < B; ++b)
         for (int hh = 0; hh < H; ++hh) {
             int g = hh / hpg;
@@ -164,6 +186,7 @@ void orc_ssd_sequential(const float* x, long ldx, const float* dt, long lddt,
                 for (long i = 0; i < (long)P * N; ++i) hT[sbase + i] = (float)h[i];
         }
     free(h);
+    }
 }
 
 void orc_ssd_chunked(const float* x, long ldx, const float* dt, long lddt,
@@ -173,10 +196,13 @@ void orc_ssd_chunked(const float* x, long ldx, const float* dt, long lddt,
                      int B, int L, int H, int P, int G, int N, int Q,
                      const float* h0, float* hT) {
     int hpg = H / G;
+#pragma omp parallel
+    {
     double* S = (double*)malloc(sizeof(double) * (size_t)P * N);     /* state entering chunk */
     double* Sc = (double*)malloc(sizeof(double) * (size_t)P * N);    /* chunk-local state */
     double* acum = (double*)malloc(sizeof(double) * Q);
     double* dlt = (double*)malloc(sizeof(double) * Q);
+#pragma omp for collapse(2) schedule(dynamic)
     for (int b = 0; b < B; ++b)
         for (int hh = 0; hh < H; ++hh) {
             int g = hh / hpg;
@@ -231,6 +257,7 @@ void orc_ssd_chunked(const float* x, long ldx, const float* dt, long lddt,
                 for (long i = 0; i < (long)P * N; ++i) hT[sbase + i] = (float)S[i];
         }
     free(S); free(Sc); free(acum); free(dlt);
+    }
 }
 
 void orc_m2_state_update(const float* x, const float* dt, const float* dt_bias, int softplus,
@@ -238,6 +265,7 @@ void orc_m2_state_update(const float* x, const float* dt, const float* dt_bias, 
                          const float* Cm, const float* Dsk, const float* z, float* y, float* h,
                          int B, int H, int P, int G, int N) {
     int hpg = H / G;
+#pragma omp parallel for collapse(2) schedule(static)
     for (int b = 0; b < B; ++b)
         for (int hh = 0; hh < H; ++hh) {
             int g = hh / hpg;
@@ -265,6 +293,7 @@ void orc_m2_state_update(const float* x, const float* dt, const float* dt_bias, 
 
 void orc_linear(const float* x, long ldx, const float* W, const float* bias, float* y, long ldy,
                 int M, int K, int Nout, int acc) {
+#pragma omp parallel for collapse(2) schedule(static)
     for (int m = 0; m < M; ++m)
         for (int o = 0; o < Nout; ++o) {
             double s = bias ? bias[o] : 0.0;
@@ -277,6 +306,7 @@ void orc_linear(const float* x, long ldx, const float* W, const float* bias, flo
 }
 
 void orc_rmsnorm(const float* x, const float* w, float* y, int M, int n, float eps) {
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m) {
         double ss = 0.0;
         for (int i = 0; i < n; ++i) ss += (double)x[(long)m * n + i] * x[(long)m * n + i];
@@ -288,7 +318,10 @@ void orc_rmsnorm(const float* x, const float* w, float* y, int M, int n, float e
 void orc_gated_rmsnorm(const float* x, long ldx, const float* z, long ldz, const float* w,
                        float* y, long ldy, int M, int n, int G, float eps) {
     int gs = n / G;
+#pragma omp parallel
+    {
     double* v = (double*)malloc(sizeof(double) * n);
+#pragma omp for schedule(static)
     for (int m = 0; m < M; ++m) {
         for (int i = 0; i < n; ++i)
             v[i] = (double)x[(long)m * ldx + i] * silu_d(z[(long)m * ldz + i]);
@@ -300,6 +333,7 @@ void orc_gated_rmsnorm(const float* x, long ldx, const float* z, long ldz, const
         }
     }
     free(v);
+    }
 }
 
 /* ------------------------------------------------------------ sampleToken */

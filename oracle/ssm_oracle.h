@@ -28,6 +28,9 @@
 extern "C" {
 #endif
 
+/* Threads the OpenMP loops use; outputs are independent of it. */
+int orc_num_threads(void);
+
 /* y[b,t,c] = act(bias[c] + sum_k w[c,k] * x[b,t-K+1+k,c]); x at t<0 is state_in[b,c,K-1+t]
  * (zero when state_in is NULL). state_out[b,c,:] receives the last K-1 inputs. */
 void orc_causal_conv1d(const float* x, long ldx, const float* w, const float* bias,

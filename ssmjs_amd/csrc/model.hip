@@ -107,6 +107,13 @@ struct ssm_ctx {
     };
     std::map<std::tuple<int, int, int, long, long>, LtPlan> lt_plans;
     bool destroyed = false;
+    // Held by every entry point that uses the context (its stream, BLAS handles, plan cache,
+    // profiler record, and the workspaces and graphs of models and states made on it) for the
+    // whole call, including host synchronisation and graph capture. Calls from several
+    // threads on one device (the Node-API addon runs each Promise on a pool thread) are
+    // therefore serialised, a capture never records another caller's launches, and
+    // ssm_ctx_destroy waits for the call in flight. Recursive: entry points call each other.
+    std::recursive_mutex mu;
     char arch[64] = {0};
     int cus = 0;
     size_t mem = 0;
@@ -140,11 +147,20 @@ ssm_status blas_status(rocblas_status s, const char* what) {
     return ssm::fail(SSM_ERR_HIP, "%s: rocBLAS status %d", what, (int)s);
 }
 
-ssm_status ctx_enter(ssm_ctx* c) {
-    if (!c) return ssm::fail(SSM_ERR_INVALID_ARG, "null context");
+using CtxLock = std::unique_lock<std::recursive_mutex>;
+
+// Checks run with the context lock held.
+ssm_status ctx_live(ssm_ctx* c) {
     if (c->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "context has been destroyed");
     SSM_HIP_TRY(hipSetDevice(c->device));
     return SSM_OK;
+}
+
+// Takes the context lock into `lk` (kept until the caller returns), then checks the context.
+ssm_status ctx_enter(ssm_ctx* c, CtxLock& lk) {
+    if (!c) return ssm::fail(SSM_ERR_INVALID_ARG, "null context");
+    lk = CtxLock(c->mu);
+    return ctx_live(c);
 }
 
 // The hipBLASLt plan of a shape: Y^T (Nout x M, column-major, ld ldy) = op(A) B with A = W
@@ -255,6 +271,7 @@ extern "C" ssm_status ssm_ctx_create(int device_ordinal, ssm_ctx** out) {
 
 extern "C" ssm_status ssm_ctx_destroy(ssm_ctx* c) {
     if (!c) return SSM_OK;
+    CtxLock lk(c->mu);   // waits for a call in flight on another thread
     if (!c->destroyed) {
         hipSetDevice(c->device);
         hipStreamSynchronize(c->stream);
@@ -276,7 +293,8 @@ extern "C" ssm_status ssm_ctx_destroy(ssm_ctx* c) {
 }
 
 extern "C" ssm_status ssm_ctx_set_stream(ssm_ctx* c, void* stream) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     c->stream = stream ? (hipStream_t)stream : c->own;
     return blas_status(rocblas_set_stream(c->blas, c->stream), "rocblas_set_stream");
 }
@@ -284,13 +302,15 @@ extern "C" ssm_status ssm_ctx_set_stream(ssm_ctx* c, void* stream) {
 extern "C" void* ssm_ctx_stream(ssm_ctx* c) { return c ? (void*)c->stream : nullptr; }
 
 extern "C" ssm_status ssm_ctx_profile(ssm_ctx* c, int enable) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     c->prof = enable != 0;
     return SSM_OK;
 }
 
 extern "C" ssm_status ssm_ctx_profile_report(ssm_ctx* c, char* buf, size_t cap) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     SSM_HIP_TRY(hipStreamSynchronize(c->stream));
     std::vector<std::string> names;
     std::vector<double> tot;
@@ -318,14 +338,16 @@ extern "C" ssm_status ssm_ctx_profile_report(ssm_ctx* c, char* buf, size_t cap) 
 }
 
 extern "C" ssm_status ssm_ctx_synchronize(ssm_ctx* c) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     SSM_HIP_TRY(hipStreamSynchronize(c->stream));
     return SSM_OK;
 }
 
 extern "C" ssm_status ssm_ctx_info(ssm_ctx* c, char* arch, int arch_len, int* cus,
                                    size_t* mem) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     if (arch && arch_len > 0) std::snprintf(arch, arch_len, "%s", c->arch);
     if (cus) *cus = c->cus;
     if (mem) *mem = c->mem;
@@ -333,25 +355,29 @@ extern "C" ssm_status ssm_ctx_info(ssm_ctx* c, char* arch, int arch_len, int* cu
 }
 
 extern "C" ssm_status ssm_malloc(ssm_ctx* c, size_t bytes, void** dptr) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     SSM_REQUIRE(dptr, "ssm_malloc: null out");
     SSM_HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
     return SSM_OK;
 }
 extern "C" ssm_status ssm_free(ssm_ctx* c, void* p) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     SSM_HIP_TRY(hipStreamSynchronize(c->stream));
     SSM_HIP_TRY(hipFree(p));
     return SSM_OK;
 }
 extern "C" ssm_status ssm_memcpy_h2d(ssm_ctx* c, void* dst, const void* src, size_t n) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     SSM_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
     SSM_HIP_TRY(hipStreamSynchronize(c->stream));
     return SSM_OK;
 }
 extern "C" ssm_status ssm_memcpy_d2h(ssm_ctx* c, void* dst, const void* src, size_t n) {
-    SSM_TRY(ctx_enter(c));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(c, lk));
     SSM_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
     SSM_HIP_TRY(hipStreamSynchronize(c->stream));
     return SSM_OK;
@@ -436,16 +462,21 @@ struct ssm_state {
 
 namespace {
 
-ssm_status model_enter(ssm_model* m) {
+// Model and state structs outlive their destroy calls (their flags answer later calls with
+// SESSION_DESTROYED), so m->ctx and s->m stay readable; the flags are read under the lock.
+ssm_status model_enter(ssm_model* m, CtxLock& lk) {
     if (!m) return ssm::fail(SSM_ERR_INVALID_ARG, "null model");
+    lk = CtxLock(m->ctx->mu);
     if (m->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "model has been destroyed");
-    return ctx_enter(m->ctx);
+    return ctx_live(m->ctx);
 }
 
-ssm_status state_enter(ssm_state* s) {
+ssm_status state_enter(ssm_state* s, CtxLock& lk) {
     if (!s) return ssm::fail(SSM_ERR_INVALID_ARG, "null state");
+    lk = CtxLock(s->m->ctx->mu);
     if (s->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "state has been destroyed");
-    return model_enter(s->m);
+    if (s->m->destroyed) return ssm::fail(SSM_ERR_DESTROYED, "model has been destroyed");
+    return ctx_live(s->m->ctx);
 }
 
 void build_layout(ssm_model* m) {
@@ -850,7 +881,8 @@ extern "C" ssm_status ssm_model_create(ssm_ctx* ctx, const ssm_config* cfg, uint
                                        ssm_model** out) {
     SSM_REQUIRE(out, "ssm_model_create: null out");
     *out = nullptr;
-    SSM_TRY(ctx_enter(ctx));
+    CtxLock lk;
+    SSM_TRY(ctx_enter(ctx, lk));
     ssm_model* m = new ssm_model();
     m->ctx = ctx;
     ssm_status s = validate_config(cfg, &m->dm, &m->types);
@@ -880,7 +912,9 @@ extern "C" ssm_status ssm_model_create(ssm_ctx* ctx, const ssm_config* cfg, uint
 }
 
 extern "C" ssm_status ssm_model_destroy(ssm_model* m) {
-    if (!m || m->destroyed) return SSM_OK;
+    if (!m) return SSM_OK;
+    CtxLock lk(m->ctx->mu);
+    if (m->destroyed) return SSM_OK;
     if (!m->ctx->destroyed) {
         hipSetDevice(m->ctx->device);
         hipStreamSynchronize(m->ctx->stream);
@@ -892,7 +926,8 @@ extern "C" ssm_status ssm_model_destroy(ssm_model* m) {
 }
 
 extern "C" ssm_status ssm_model_config(ssm_model* m, ssm_config* out) {
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     SSM_REQUIRE(out, "null out");
     const Dims& d = m->dm;
     out->vocab_size = d.V; out->d_model = d.d; out->n_layers = d.nl; out->d_state = d.N;
@@ -951,7 +986,8 @@ float h2f(uint16_t h) {
 
 extern "C" ssm_status ssm_model_export_weights(ssm_model* m, int f16, void* buf, size_t cap,
                                                size_t* bytes) {
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     const size_t hb = header_bytes(m->dm.nl);
     const size_t total = hb + m->nfloats * (f16 ? 2 : 4);
     if (bytes) *bytes = total;
@@ -977,7 +1013,8 @@ extern "C" ssm_status ssm_model_export_weights(ssm_model* m, int f16, void* buf,
 }
 
 extern "C" ssm_status ssm_model_load_weights(ssm_model* m, const void* buf, size_t bytes) {
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     const unsigned char* p = (const unsigned char*)buf;
     auto bad = [](const char* why) { return ssm::fail(SSM_ERR_CHECKPOINT_INVALID, "%s", why); };
     if (!p || bytes < 80 || std::memcmp(p, "SSMW", 4) != 0) return bad("bad magic");
@@ -1023,7 +1060,8 @@ extern "C" ssm_status ssm_model_load_weights(ssm_model* m, const void* buf, size
 
 extern "C" ssm_status ssm_forward_device(ssm_model* m, const uint32_t* d_ids, int B, int L,
                                          float* d_logits) {
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     SSM_REQUIRE(d_ids && d_logits && B >= 0 && L >= 0, "ssm_forward_device: bad args");
     if (B == 0 || L == 0) return SSM_OK;
     Ws w;
@@ -1035,7 +1073,8 @@ extern "C" ssm_status ssm_forward_device(ssm_model* m, const uint32_t* d_ids, in
 
 extern "C" ssm_status ssm_forward(ssm_model* m, const uint32_t* ids, int B, int L,
                                   float* logits) {
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     SSM_REQUIRE(ids && logits && B >= 0 && L >= 0, "ssm_forward: bad args");
     if (B == 0 || L == 0) return SSM_OK;
     const size_t T = (size_t)B * L;
@@ -1053,7 +1092,8 @@ extern "C" ssm_status ssm_forward(ssm_model* m, const uint32_t* ids, int B, int 
 
 extern "C" ssm_status ssm_mixer_forward_device(ssm_model* m, int layer, const float* d_x,
                                                float* d_y, int B, int L) {
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     SSM_REQUIRE(layer >= 0 && layer < m->dm.nl && d_x && d_y && B >= 0 && L >= 0,
                 "ssm_mixer_forward_device: bad args");
     if (B == 0 || L == 0) return SSM_OK;
@@ -1066,7 +1106,8 @@ extern "C" ssm_status ssm_mixer_forward_device(ssm_model* m, int layer, const fl
 extern "C" ssm_status ssm_state_create(ssm_model* m, int B, ssm_state** out) {
     SSM_REQUIRE(out, "ssm_state_create: null out");
     *out = nullptr;
-    SSM_TRY(model_enter(m));
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
     SSM_REQUIRE(B > 0, "ssm_state_create: batch must be positive");
     const Dims& d = m->dm;
     ssm_state* s = new ssm_state();
@@ -1107,7 +1148,9 @@ extern "C" ssm_status ssm_state_create(ssm_model* m, int B, ssm_state** out) {
 }
 
 extern "C" ssm_status ssm_state_destroy(ssm_state* s) {
-    if (!s || s->destroyed) return SSM_OK;
+    if (!s) return SSM_OK;
+    CtxLock lk(s->m->ctx->mu);
+    if (s->destroyed) return SSM_OK;
     if (!s->m->destroyed && !s->m->ctx->destroyed) {
         hipSetDevice(s->m->ctx->device);
         hipStreamSynchronize(s->m->ctx->stream);
@@ -1122,7 +1165,8 @@ extern "C" ssm_status ssm_state_destroy(ssm_state* s) {
 }
 
 extern "C" ssm_status ssm_state_reset(ssm_state* s) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     for (size_t i = 0; i < s->ssm.size(); ++i) {
         SSM_HIP_TRY(hipMemsetAsync(s->ssm[i], 0, s->ssm_n[i] * 4, s->m->ctx->stream));
         SSM_HIP_TRY(hipMemsetAsync(s->conv[i], 0, s->conv_n[i] * 4, s->m->ctx->stream));
@@ -1134,7 +1178,8 @@ extern "C" ssm_status ssm_state_reset(ssm_state* s) {
 extern "C" size_t ssm_state_floats(ssm_state* s) { return s ? s->floats : 0; }
 
 extern "C" ssm_status ssm_state_read(ssm_state* s, float* out) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(out, "null out");
     size_t off = 0;
     for (size_t i = 0; i < s->ssm.size(); ++i) {
@@ -1150,7 +1195,8 @@ extern "C" ssm_status ssm_state_read(ssm_state* s, float* out) {
 }
 
 extern "C" ssm_status ssm_state_write(ssm_state* s, const float* in) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(in, "null in");
     size_t off = 0;
     for (size_t i = 0; i < s->ssm.size(); ++i) {
@@ -1166,7 +1212,8 @@ extern "C" ssm_status ssm_state_write(ssm_state* s, const float* in) {
 }
 
 extern "C" ssm_status ssm_state_layer(ssm_state* s, int layer, float** ssm_p, float** conv_p) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(layer >= 0 && layer < (int)s->ssm.size(), "layer out of range");
     if (ssm_p) *ssm_p = s->ssm[layer];
     if (conv_p) *conv_p = s->conv[layer];
@@ -1214,7 +1261,8 @@ ssm_status ensure_gen(ssm_state* s, size_t n) {
 
 extern "C" ssm_status ssm_prefill(ssm_model* m, ssm_state* s, const uint32_t* ids, int L,
                                   float* last_logits, uint32_t* argmax) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(s->m == m, "state belongs to another model");
     SSM_REQUIRE(ids && L > 0, "ssm_prefill: need at least one token");
     const size_t T = (size_t)s->B * L;
@@ -1306,7 +1354,8 @@ ssm_status decode_graphed(ssm_model* m, ssm_state* s, const uint32_t* d_ids, flo
 
 extern "C" ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const uint32_t* d_ids,
                                              float* d_logits, uint32_t* d_argmax) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(s->m == m && d_ids, "ssm_decode_step_device: bad args");
     float* lg = d_logits ? d_logits : s->d_logits;
     if (!graphs_on(m->ctx)) return decode_body(m, s, d_ids, lg, d_argmax);
@@ -1315,7 +1364,8 @@ extern "C" ssm_status ssm_decode_step_device(ssm_model* m, ssm_state* s, const u
 
 extern "C" ssm_status ssm_decode_step(ssm_model* m, ssm_state* s, const uint32_t* ids,
                                       float* logits, uint32_t* argmax) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(s->m == m && ids, "ssm_decode_step: bad args");
     SSM_TRY(ensure_gen(s, (size_t)s->B));
     SSM_HIP_TRY(hipMemcpyAsync(s->d_tok, ids, (size_t)s->B * 4, hipMemcpyHostToDevice,
@@ -1342,7 +1392,8 @@ ssm_status gen_to_host(ssm_model* m, ssm_state* s, int n_new, uint32_t* out_ids)
 
 extern "C" ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint32_t* prompt,
                                           int Lp, int n_new, uint32_t* out_ids) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(s->m == m && prompt && Lp > 0 && n_new >= 0 && (out_ids || n_new == 0),
                 "ssm_generate_greedy: bad args");
     if (n_new == 0) return SSM_OK;
@@ -1372,7 +1423,8 @@ extern "C" ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint
                                           int Lp, int n_new, double temperature, int top_k,
                                           double top_p, const double* u_host,
                                           uint32_t* out_ids) {
-    SSM_TRY(state_enter(s));
+    CtxLock lk;
+    SSM_TRY(state_enter(s, lk));
     SSM_REQUIRE(s->m == m && prompt && Lp > 0 && n_new >= 0 &&
                     ((out_ids && u_host) || n_new == 0),
                 "ssm_generate_sample: bad args");

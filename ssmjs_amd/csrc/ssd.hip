@@ -1,23 +1,22 @@
 // K3-K6: Mamba-2 SSD prefill (Dao & Gu 2024, section 6) for gfx950, and K7: the one-token
 // Mamba-2 state update.
 //
-// One workgroup owns one (batch, segment) and HPW heads of one group (4 waves per head; two
-// heads for bf16 inputs, one for fp32) and walks the segment's chunks in order with each
-// head's P x N state held in MFMA accumulator registers, so the chunk-state tensor is never
-// written to HBM. Per chunk of Q = 64 steps:
+// This file: bf16 inputs (x, B, C; dt and y fp32). fp32 inputs run the fp32 matrix-core
+// kernel of ssd_f32.hip. One workgroup owns one (batch, segment) and HPW heads of one group (4
+// waves per head; two heads when heads pair up in a group) and walks the segment's chunks in
+// order with each head's P x N state held in MFMA accumulator registers, so the chunk-state
+// tensor is never written to HBM. Per chunk of Q = 64 steps:
 //   dt/decay  every wave computes dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix
 //             sum of dt' * A_h over the chunk with a 64-lane DPP scan.
-//   staging   X, X * w with w_j = exp(acum_end - acum_j) dt'_j, and B go to LDS as bf16 (hi,
-//             plus lo when SPLIT). C goes to LDS too when two heads share it; with one head
-//             each wave keeps its 16 rows of C in registers.
+//   staging   X, X * w with w_j = exp(acum_end - acum_j) dt'_j, and B go to LDS as bf16. C
+//             goes to LDS too when two heads share it; with one head each wave keeps its 16
+//             rows of C in registers.
 //   Y_off     Y^T[p,i] = exp(acum_i) * sum_n S[p,n] C[i,n]              (MFMA, K = N)
 //   Y_diag    S^T[j,i] = sum_n B[j,n] C[i,n]; mask j <= i; * exp(acum_i - acum_j) dt'_j;
 //             Y^T[p,i] += sum_j X^T[p,j] S^T[j,i]                          (MFMA, K = N, Q)
 //             with D_h added on the diagonal j == i, so Y^T is y^T
 //   state     S = exp(acum_end) S + (X w)^T B                             (MFMA, K = Q)
-// MFMA is v_mfma_f32_16x16x32_bf16 with fp32 accumulation. SPLIT (float inputs) writes each
-// operand as hi = bf16(v), lo = bf16(v - hi) and accumulates hi*hi + hi*lo + lo*hi, which keeps
-// about 16 mantissa bits of every product.
+// MFMA is v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
 //
 // The internal chunk (Q = 64) is independent of the model's chunkLen: the chunked algorithm
 // is exact for any chunk length. Long single sequences are cut into segments so that
@@ -28,6 +27,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "ssd.hpp"
 
 namespace {
 
@@ -69,30 +69,7 @@ __device__ __forceinline__ float ld1<float>(const float* p) { return *p; }
 template <>
 __device__ __forceinline__ float ld1<__bf16>(const __bf16* p) { return (float)*p; }
 
-// Load n (4 or 8) consecutive elements as floats.
-template <typename T, int n>
-__device__ __forceinline__ void ldv(const T* p, float* out) {
-    if constexpr (sizeof(T) == 4) {
-#pragma unroll
-        for (int i = 0; i < n; i += 4) {
-            float4 v = *reinterpret_cast<const float4*>(p + i);
-            out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
-        }
-    } else {
-        if constexpr (n == 8) {
-            bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) out[i] = (float)v[i];
-        } else {
-            bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) out[i] = (float)v[i];
-        }
-    }
-}
-
 __device__ __forceinline__ __bf16 hi_of(float v) { return (__bf16)v; }
-__device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v - (float)h); }
 
 // LDS tiles, all in natural row-major layout (rows = time steps j, or p for the state). The
 // operands an MFMA needs with K = j (X^T, (X w)^T, B^T) are read with ds_read_b64_tr_b16:
@@ -103,21 +80,20 @@ __device__ __forceinline__ __bf16 lo_of(float v, __bf16 h) { return (__bf16)(v -
 // are conflict-free at pitch 144; the transposed reads over rows j0 + 8 q4 (+4) meet 2-way
 // bank conflicts at every pitch (SQ_LDS_BANK_CONFLICT). A layout without them (k-slot rows
 // 4 q4 apart, pitches of 16 mod 32) ran no faster: LDS is not what bounds this kernel.
-template <bool SPLIT, int NN, bool FULL, int HPW>
+template <int NN, bool FULL, int HPW>
 struct Smem {
-    static constexpr int NS = SPLIT ? 2 : 1;
     static constexpr int XP = P + 8;                   // X / Xw row pitch (bf16)
     static constexpr int BP = NN + 16;                 // B / C row pitch
     // 16-byte alignment lets the compiler use ds_read_b128 / ds_write_b128 for the 8-wide
     // bf16 rows (every pitch is a multiple of 8 elements). B and C belong to the group and
     // are staged once for the HPW heads of the workgroup; the other tiles are per head.
-    alignas(16) __bf16 xw[HPW][NS][Q][XP];             // X * w_j   (j, p)
-    alignas(16) __bf16 b[NS][Q][BP];                   // B         (j, n)
+    alignas(16) __bf16 xw[HPW][Q][XP];                 // X * w_j   (j, p)
+    alignas(16) __bf16 b[Q][BP];                       // B         (j, n)
     static constexpr bool CST = FULL && HPW > 1;       // C staged (shared by two heads)
-    alignas(16) __bf16 c[CST ? NS : 1][CST ? Q : 1][BP];              // C   (i, n)
-    alignas(16) __bf16 x[HPW][FULL ? NS : 1][FULL ? Q : 1][XP];       // X   (j, p)
-    alignas(16) __bf16 s[HPW][FULL ? NS : 1][FULL ? NN : 1][XP];      // state^T (n, p)
-    alignas(16) float g[HPW][Q];    // acum_j log2(e) - log2(dt'_j): the decay weight exponent
+    alignas(16) __bf16 c[CST ? Q : 1][BP];             // C   (i, n)
+    alignas(16) __bf16 x[HPW][FULL ? Q : 1][XP];       // X   (j, p)
+    alignas(16) __bf16 s[HPW][FULL ? NN : 1][XP];      // state^T (n, p)
+    alignas(16) float dv[HPW][Q];   // dt'_j
     alignas(16) float ac[HPW][Q];   // acum_j log2(e)
 };
 
@@ -142,21 +118,20 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
 // workgroup's heads): thread t of the workgroup reads rows t / (NN/8) + BR k, 8 elements at
 // 8 (t % (NN/8)). dt: time step lane. With one head per workgroup each wave loads its own C
 // rows as MFMA fragments instead (no staging).
-template <typename TIN, int NN, bool FULL, int HPW>
+template <int NN, bool FULL, int HPW>
 struct Raw {
     static constexpr int KS = NN / 32;
     static constexpr int BL = NN / 8;                // lanes per B / C row
     static constexpr int BR = 256 * HPW / BL;        // B / C rows per pass
     static constexpr int BPASS = Q / BR;
-    using v8 = typename std::conditional<sizeof(TIN) == 4, float4, bf16x8>::type;
-    static constexpr int V8N = sizeof(TIN) == 4 ? 2 : 1;   // 16-byte units per 8 elements
-    static constexpr int XE = 16 / (int)sizeof(TIN);       // X elements per 16-byte load
-    static constexpr int XL = P / XE;                      // lanes per X row
-    static constexpr int XR = 64 / XL;                     // X rows per load
-    static constexpr int XK = 16 / XR;                     // X loads per wave
+    using v8 = bf16x8;
+    static constexpr int XE = 8;                     // X elements per 16-byte load
+    static constexpr int XL = P / XE;                // lanes per X row
+    static constexpr int XR = 64 / XL;               // X rows per load
+    static constexpr int XK = 16 / XR;               // X loads per wave
     v8 x[XK];
-    v8 b[BPASS][V8N];
-    v8 c[FULL && HPW > 1 ? BPASS : 1][V8N];
+    v8 b[BPASS];
+    v8 c[FULL && HPW > 1 ? BPASS : 1];
     float dt;
 };
 
@@ -207,18 +182,17 @@ __device__ __forceinline__ V vzero() {
     return v;
 }
 
-// Launch shape: HPW heads of one group per workgroup (4 waves per head). bf16 inputs run two
-// heads per workgroup (8 waves, 111 KB LDS, one workgroup per CU): B and C are loaded and
-// staged once for both heads, which halves their share of the memory instructions. fp32
-// inputs (SPLIT) keep one head and one workgroup per CU (hi and lo tiles).
-template <typename TIN, bool SPLIT, int NN, bool FULL, int HPW>
-__global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void ssd_kernel(SsdArgs a) {
-    __shared__ __attribute__((aligned(16))) Smem<SPLIT, NN, FULL, HPW> sm;
-    using SM = Smem<SPLIT, NN, FULL, HPW>;
+// Launch shape: HPW heads of one group per workgroup (4 waves per head). When heads pair up
+// in a group, two heads per workgroup (8 waves, one workgroup per CU): B and C are loaded and
+// staged once for both heads, which halves their share of the memory instructions.
+template <int NN, bool FULL, int HPW>
+__global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kernel(SsdArgs a) {
+    using TIN = __bf16;
+    __shared__ __attribute__((aligned(16))) Smem<NN, FULL, HPW> sm;
+    using SM = Smem<NN, FULL, HPW>;
     constexpr int NB = NN / 16;   // state n-blocks per wave
     constexpr int KS = NN / 32;   // k-steps over n
-    using RW = Raw<TIN, NN, FULL, HPW>;
-    constexpr int L1 = SPLIT ? 1 : 0;   // index of the lo copy (aliases hi when unused)
+    using RW = Raw<NN, FULL, HPW>;
     constexpr bool CST = SM::CST;       // C staged in LDS (two heads) or loaded per wave
 
     int wg = blockIdx.x;
@@ -277,7 +251,6 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
     // instruction moves whole lines of 8 rows. A DPP swap between the two lanes puts every
     // value where the MFMA layout has it.
     const int podd = l16 & 1;
-    const unsigned oc = (unsigned)(ic * a.ldc + 8 * q4) * SZ;
     const unsigned oc2 = (unsigned)((16 * wl + l16 - podd) * a.ldc + 32 * podd + 8 * q4) * SZ;
     // rows of chunk c that exist; 0 past the segment, so a prefetch there reads nothing
     auto rows_of = [&](int c) { return c < c_end ? min(Q, a.L - c * Q) : 0; };
@@ -297,58 +270,32 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
 #pragma unroll
         for (int k = 0; k < RW::XK; ++k) raw.x[k] = bload16<v8>(rx, ox + k * oxk);
 #pragma unroll
-        for (int k = 0; k < RW::BPASS; ++k)
-#pragma unroll
-            for (int u = 0; u < RW::V8N; ++u) raw.b[k][u] = bload16<v8>(rb, ob + k * obk + 4 * u * SZ);
+        for (int k = 0; k < RW::BPASS; ++k) raw.b[k] = bload16<v8>(rb, ob + k * obk);
         if constexpr (CST) {
             const auto rc = rsrc(cm0 + r0 * a.ldc, span(qv, a.ldc, NN, SZ));
 #pragma unroll
-            for (int k = 0; k < RW::BPASS; ++k)
-#pragma unroll
-                for (int u = 0; u < RW::V8N; ++u) raw.c[k][u] = bload16<v8>(rc, occ + k * occk + 4 * u * SZ);
+            for (int k = 0; k < RW::BPASS; ++k) raw.c[k] = bload16<v8>(rc, occ + k * occk);
         }
     };
     // Without C staging: C rows of the wave's strip, row ic, n = 32ks + 8q4 + 0..7 (MFMA
     // B-operand fragments), prefetched after their last use in the previous chunk
-    v8 craw[FULL && !CST ? KS : 1][RW::V8N];
+    v8 craw[FULL && !CST ? KS : 1];
     auto load_c = [&](int c) {
         if constexpr (FULL && !CST) {
             const int qv = rows_of(c);
             const auto rc = rsrc(cm0 + (long)c * Q * a.ldc, span(qv, a.ldc, NN, SZ));
-            if constexpr (sizeof(TIN) == 2) {
-                // craw[2h + sel]: row 16wl + (l16 & ~1) + sel, n = 64h + 32 (l16 & 1) + 8 q4 + 0..7
+            // craw[2h + sel]: row 16wl + (l16 & ~1) + sel, n = 64h + 32 (l16 & 1) + 8 q4 + 0..7
 #pragma unroll
-                for (int hh = 0; hh < KS / 2; ++hh)
+            for (int hh = 0; hh < KS / 2; ++hh)
 #pragma unroll
-                    for (int sel = 0; sel < 2; ++sel)
-                        craw[2 * hh + sel][0] =
-                            bload16<v8>(rc, oc2 + (unsigned)(sel * a.ldc * SZ) + 128u * hh);
-            } else {
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-                    for (int u = 0; u < RW::V8N; ++u) craw[ks][u] = bload16<v8>(rc, oc + (32 * ks + 4 * u) * SZ);
-            }
+                for (int sel = 0; sel < 2; ++sel)
+                    craw[2 * hh + sel] =
+                        bload16<v8>(rc, oc2 + (unsigned)(sel * a.ldc * SZ) + 128u * hh);
         }
     };
-    // 8 elements of B or C to LDS (hi, plus lo when SPLIT)
-    auto stage8 = [&](__bf16 (*tile)[Q][SM::BP], int j, const v8* src) {
-        if constexpr (sizeof(TIN) == 2) {
-            *reinterpret_cast<bf16x8*>(&tile[0][j][bc]) = src[0];
-        } else {
-            bf16x8 hh, ll;
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const float e4[4] = {src[u].x, src[u].y, src[u].z, src[u].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    hh[4 * u + e] = hi_of(e4[e]);
-                    ll[4 * u + e] = lo_of(e4[e], hh[4 * u + e]);
-                }
-            }
-            *reinterpret_cast<bf16x8*>(&tile[0][j][bc]) = hh;
-            if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(&tile[L1][j][bc]) = ll;
-        }
+    // 8 elements of B or C to LDS
+    auto stage8 = [&](__bf16 (*tile)[SM::BP], int j, const v8& src) {
+        *reinterpret_cast<bf16x8*>(&tile[j][bc]) = src;
     };
 
     // ---- entering state -> accumulators (wave wl: rows p = 16wl + 4*q4 + r, cols 16nb + l16)
@@ -371,14 +318,10 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
     auto write_state_lds = [&]() {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            bf16x4 hv, lv;
+            bf16x4 hv;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                hv[r] = hi_of(S[nb][r]);
-                lv[r] = lo_of(S[nb][r], hv[r]);
-            }
-            *reinterpret_cast<bf16x4*>(&sm.s[hw][0][16 * nb + l16][16 * wl + 4 * q4]) = hv;
-            if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(&sm.s[hw][L1][16 * nb + l16][16 * wl + 4 * q4]) = lv;
+            for (int r = 0; r < 4; ++r) hv[r] = hi_of(S[nb][r]);
+            *reinterpret_cast<bf16x4*>(&sm.s[hw][16 * nb + l16][16 * wl + 4 * q4]) = hv;
         }
     };
     if (FULL && state_live) write_state_lds();
@@ -408,9 +351,10 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
         decay_sum += acend;
         if (wl == 0) {
-            // exp(acum_i - acum_j) dt'_j = exp2(ac_i - g_j); dt'_j = 0 gives g_j = +inf, weight 0
+            // decay weight exp(acum_i - acum_j) dt'_j = exp2(ac_i - ac_j) dt'_j: dt' keeps its
+            // sign (softplus off with no lower clamp allows dt' < 0)
             const float sl = sc * ssm::kLog2e;
-            sm.g[hw][lane] = sl - __builtin_amdgcn_logf(dv);
+            sm.dv[hw][lane] = dv;
             sm.ac[hw][lane] = sl;
         }
         const float wl_ = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
@@ -422,37 +366,11 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
             const int j = 16 * wl + RW::XR * k + xr;
             const float wj = __builtin_bit_cast(
                 float, __builtin_amdgcn_ds_bpermute(4 * j, __builtin_bit_cast(int, wl_)));
-            float xv[E];
-            if constexpr (sizeof(TIN) == 4) {
-                xv[0] = raw.x[k].x; xv[1] = raw.x[k].y; xv[2] = raw.x[k].z; xv[3] = raw.x[k].w;
-            } else {
+            bf16x8 wh;
 #pragma unroll
-                for (int e = 0; e < E; ++e) xv[e] = (float)raw.x[k][e];
-            }
-            using bfE = typename std::conditional<E == 8, bf16x8, bf16x4>::type;
-            bfE wh, wlo;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const float u = xv[e] * wj;
-                wh[e] = hi_of(u);
-                wlo[e] = lo_of(u, wh[e]);
-            }
-            *reinterpret_cast<bfE*>(&sm.xw[hw][0][j][xc]) = wh;
-            if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.xw[hw][L1][j][xc]) = wlo;
-            if constexpr (FULL) {
-                if constexpr (sizeof(TIN) == 2) {
-                    *reinterpret_cast<bf16x8*>(&sm.x[hw][0][j][xc]) = raw.x[k];
-                } else {
-                    bfE hh, ll;
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        hh[e] = hi_of(xv[e]);
-                        ll[e] = lo_of(xv[e], hh[e]);
-                    }
-                    *reinterpret_cast<bfE*>(&sm.x[hw][0][j][xc]) = hh;
-                    if constexpr (SPLIT) *reinterpret_cast<bfE*>(&sm.x[hw][L1][j][xc]) = ll;
-                }
-            }
+            for (int e = 0; e < E; ++e) wh[e] = hi_of((float)raw.x[k][e] * wj);
+            *reinterpret_cast<bf16x8*>(&sm.xw[hw][j][xc]) = wh;
+            if constexpr (FULL) *reinterpret_cast<bf16x8*>(&sm.x[hw][j][xc]) = raw.x[k];
         }
         // ---- stage B and C (shared by the workgroup's heads)
 #pragma unroll
@@ -462,31 +380,16 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
         }
         // ---- C rows of this wave's strip as MFMA fragments: row ic, n = 32ks + 8q4 + 0..7
         // (from registers here without C staging, from LDS after the barrier with it)
-        bf16x8 cfh[FULL ? KS : 1], cfl[FULL ? KS : 1];
+        bf16x8 cfh[FULL ? KS : 1];
         if constexpr (FULL && !CST) {
+            // fragment ks = 2h + e of row ic: the own load (h, sel = l16 & 1) holds e = l16 & 1,
+            // the neighbour's load (h, sel = l16 & 1) the other one
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                if constexpr (sizeof(TIN) == 2) {
-                    // fragment ks = 2h + e of row ic: the own load (h, sel = l16 & 1) holds
-                    // e = l16 & 1, the neighbour's load (h, sel = l16 & 1) the other one
-                    if (ks % 2 == 0) {
-                        const int hh = ks / 2;
-                        const bf16x8 s0 = swap_pair(craw[2 * hh][0]);
-                        const bf16x8 s1 = swap_pair(craw[2 * hh + 1][0]);
-                        cfh[ks] = podd ? s1 : craw[2 * hh][0];
-                        cfh[ks + 1] = podd ? craw[2 * hh + 1][0] : s0;
-                    }
-                } else {
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const float e4[4] = {craw[ks][u].x, craw[ks][u].y, craw[ks][u].z, craw[ks][u].w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            cfh[ks][4 * u + e] = hi_of(e4[e]);
-                            cfl[ks][4 * u + e] = lo_of(e4[e], cfh[ks][4 * u + e]);
-                        }
-                    }
-                }
+            for (int hh = 0; hh < KS / 2; ++hh) {
+                const bf16x8 s0 = swap_pair(craw[2 * hh]);
+                const bf16x8 s1 = swap_pair(craw[2 * hh + 1]);
+                cfh[2 * hh] = podd ? s1 : craw[2 * hh];
+                cfh[2 * hh + 1] = podd ? craw[2 * hh + 1] : s0;
             }
         }
         __syncthreads();   // staging (and the state LDS copy) visible to every wave
@@ -498,10 +401,8 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
         if constexpr (FULL) {
             if constexpr (CST) {
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    cfh[ks] = *reinterpret_cast<const bf16x8*>(&sm.c[0][ic][32 * ks + 8 * q4]);
-                    if constexpr (SPLIT) cfl[ks] = *reinterpret_cast<const bf16x8*>(&sm.c[L1][ic][32 * ks + 8 * q4]);
-                }
+                for (int ks = 0; ks < KS; ++ks)
+                    cfh[ks] = *reinterpret_cast<const bf16x8*>(&sm.c[ic][32 * ks + 8 * q4]);
             }
             const float aci = sm.ac[hw][ic];
             floatx4 Y[P / 16];
@@ -516,15 +417,9 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
                     for (int ks = 0; ks < KS; ++ks) {
                         // S[p = 16pb + l16][n = 32ks + 8q4 + 0..7] from the state^T tile
                         const int n0 = 32 * ks + 8 * q4;
-                        const bf16x8 ah = cat(tr_read<SM::XP>(&sm.s[hw][0][0][0], n0, 16 * pb, l16),
-                                              tr_read<SM::XP>(&sm.s[hw][0][0][0], n0 + 4, 16 * pb, l16));
+                        const bf16x8 ah = cat(tr_read<SM::XP>(&sm.s[hw][0][0], n0, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.s[hw][0][0], n0 + 4, 16 * pb, l16));
                         Y[pb] = mfma(ah, cfh[ks], Y[pb]);
-                        if constexpr (SPLIT) {
-                            const bf16x8 al = cat(tr_read<SM::XP>(&sm.s[hw][L1][0][0], n0, 16 * pb, l16),
-                                                  tr_read<SM::XP>(&sm.s[hw][L1][0][0], n0 + 4, 16 * pb, l16));
-                            Y[pb] = mfma(ah, cfl[ks], Y[pb]);
-                            Y[pb] = mfma(al, cfh[ks], Y[pb]);
-                        }
                     }
                 }
                 const float e = ssm::ex2(aci);
@@ -546,14 +441,8 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
 #pragma unroll
                     for (int jb = 0; jb <= W; ++jb) {
                         const bf16x8 bh_ = *reinterpret_cast<const bf16x8*>(
-                            &sm.b[0][16 * jb + l16][32 * ks + 8 * q4]);
+                            &sm.b[16 * jb + l16][32 * ks + 8 * q4]);
                         st[jb] = mfma(bh_, cfh[ks], st[jb]);
-                        if constexpr (SPLIT) {
-                            const bf16x8 bl_ = *reinterpret_cast<const bf16x8*>(
-                                &sm.b[L1][16 * jb + l16][32 * ks + 8 * q4]);
-                            st[jb] = mfma(bh_, cfl[ks], st[jb]);
-                            st[jb] = mfma(bl_, cfh[ks], st[jb]);
-                        }
                     }
                 // S^T[j, i] * exp(acum_i - acum_j) dt'_j for this lane's rows j = 16jb + 4q4 + r;
                 // below the diagonal block every j < i, on it j > i is masked by a select (the
@@ -566,11 +455,13 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
                         for (int r = 0; r < 4; ++r) sv[jb][r] = 0.f;
                         continue;
                     }
-                    const float4 gj = *reinterpret_cast<const float4*>(&sm.g[hw][16 * jb + 4 * q4]);
-                    const float gjr[4] = {gj.x, gj.y, gj.z, gj.w};
+                    const float4 aj = *reinterpret_cast<const float4*>(&sm.ac[hw][16 * jb + 4 * q4]);
+                    const float4 dj = *reinterpret_cast<const float4*>(&sm.dv[hw][16 * jb + 4 * q4]);
+                    const float ajr[4] = {aj.x, aj.y, aj.z, aj.w};
+                    const float djr[4] = {dj.x, dj.y, dj.z, dj.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float f = st[jb][r] * ssm::ex2(aci - gjr[r]);
+                        const float f = st[jb][r] * (ssm::ex2(aci - ajr[r]) * djr[r]);
                         if (jb < W) {
                             sv[jb][r] = f;
                         } else {
@@ -582,25 +473,17 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
                 // X^T fragment: k-slots 0..3 <-> j = 32 jb2 + 4 q4 + 0..3, 4..7 <-> +16
 #pragma unroll
                 for (int jb2 = 0; jb2 <= W / 2; ++jb2) {
-                    bf16x8 sfh, sfl;
+                    bf16x8 sfh;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         sfh[r] = hi_of(sv[2 * jb2][r]);
                         sfh[4 + r] = hi_of(sv[2 * jb2 + 1][r]);
-                        sfl[r] = lo_of(sv[2 * jb2][r], sfh[r]);
-                        sfl[4 + r] = lo_of(sv[2 * jb2 + 1][r], sfh[4 + r]);
                     }
 #pragma unroll
                     for (int pb = 0; pb < P / 16; ++pb) {
-                        const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[hw][0][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
-                                              tr_read<SM::XP>(&sm.x[hw][0][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
+                        const bf16x8 xh = cat(tr_read<SM::XP>(&sm.x[hw][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
+                                              tr_read<SM::XP>(&sm.x[hw][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
                         Y[pb] = mfma(xh, sfh, Y[pb]);
-                        if constexpr (SPLIT) {
-                            const bf16x8 xl = cat(tr_read<SM::XP>(&sm.x[hw][L1][0][0], 32 * jb2 + 4 * q4, 16 * pb, l16),
-                                                  tr_read<SM::XP>(&sm.x[hw][L1][0][0], 32 * jb2 + 16 + 4 * q4, 16 * pb, l16));
-                            Y[pb] = mfma(xh, sfl, Y[pb]);
-                            Y[pb] = mfma(xl, sfh, Y[pb]);
-                        }
                     }
                 }
             };
@@ -640,23 +523,13 @@ __global__ __launch_bounds__(256 * HPW, SPLIT || (FULL && HPW > 1) ? 1 : 2) void
 #pragma unroll
             for (int ks = 0; ks < Q / 32; ++ks) {
                 const int j0 = 32 * ks + 8 * q4;
-                const bf16x8 xh = cat(tr_read<SM::XP>(&sm.xw[hw][0][0][0], j0, 16 * wl, l16),
-                                      tr_read<SM::XP>(&sm.xw[hw][0][0][0], j0 + 4, 16 * wl, l16));
-                bf16x8 xl;
-                if constexpr (SPLIT)
-                    xl = cat(tr_read<SM::XP>(&sm.xw[hw][L1][0][0], j0, 16 * wl, l16),
-                             tr_read<SM::XP>(&sm.xw[hw][L1][0][0], j0 + 4, 16 * wl, l16));
+                const bf16x8 xh = cat(tr_read<SM::XP>(&sm.xw[hw][0][0], j0, 16 * wl, l16),
+                                      tr_read<SM::XP>(&sm.xw[hw][0][0], j0 + 4, 16 * wl, l16));
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    const bf16x8 bh_ = cat(tr_read<SM::BP>(&sm.b[0][0][0], j0, 16 * nb, l16),
-                                           tr_read<SM::BP>(&sm.b[0][0][0], j0 + 4, 16 * nb, l16));
+                    const bf16x8 bh_ = cat(tr_read<SM::BP>(&sm.b[0][0], j0, 16 * nb, l16),
+                                           tr_read<SM::BP>(&sm.b[0][0], j0 + 4, 16 * nb, l16));
                     S[nb] = mfma(xh, bh_, S[nb]);
-                    if constexpr (SPLIT) {
-                        const bf16x8 bl_ = cat(tr_read<SM::BP>(&sm.b[L1][0][0], j0, 16 * nb, l16),
-                                               tr_read<SM::BP>(&sm.b[L1][0][0], j0 + 4, 16 * nb, l16));
-                        S[nb] = mfma(xh, bl_, S[nb]);
-                        S[nb] = mfma(xl, bh_, S[nb]);
-                    }
                 }
             }
         }
@@ -697,7 +570,7 @@ __global__ void ssd_seg_prefix(SsdArgs a, int PN) {
     }
 }
 
-template <typename TIN, bool SPLIT, int NN, int HPW>
+template <int NN, int HPW>
 ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
     if (a.nseg > 1) {
         // the state-only pass runs one head per workgroup: with no Y work its B tile is a
@@ -708,7 +581,7 @@ ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
         SsdArgs s1 = a;
         const int nwg1 = a.B * a.H * (a.nseg - 1);
         s1.remap = (nwg1 % 8 == 0) ? 1 : 0;
-        ssd_kernel<TIN, SPLIT, NN, false, 1><<<nwg1, 256, 0, st>>>(s1);
+        ssd_kernel<NN, false, 1><<<nwg1, 256, 0, st>>>(s1);
         ssm_status e = ssm::check_launch("ssd_state_pass");
         if (e != SSM_OK) return e;
         const long n = (long)a.B * a.H * P * NN;
@@ -718,7 +591,7 @@ ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
     }
     const int nwg = a.B * (a.H / HPW) * a.nseg;
     a.remap = (nwg % 8 == 0) ? 1 : 0;
-    ssd_kernel<TIN, SPLIT, NN, true, HPW><<<nwg, 256 * HPW, 0, st>>>(a);
+    ssd_kernel<NN, true, HPW><<<nwg, 256 * HPW, 0, st>>>(a);
     return ssm::check_launch("ssd_chunk_scan");
 }
 
@@ -833,8 +706,8 @@ __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, int Pd) {
     const TIN* Cp = reinterpret_cast<const TIN*>(a.Cm) + (long)g * N;
     const float Ah = a.A[h], dtb = a.dt_bias ? a.dt_bias[h] : 0.f, Dh = a.Dsk ? a.Dsk[h] : 0.f;
     const long rb = (long)b * L;
-    float* xs = seq_smem;          // [T][Pd]
-    float* bs = xs + T * Pd;       // [T][N]
+    float* xs = seq_smem;                          // [T][Pd]
+    float* bs = xs + ((T * Pd + 3) & ~3);          // [T][N], 16-byte aligned for float4 reads
     float* cs = bs + T * N;        // [T][N]
     float* ds = cs + T * N;        // [T]: dt'
     float4 st[MAXR];
@@ -948,7 +821,8 @@ ssm_status launch_ssd_seq(SsdArgs& a, int Pd, hipStream_t st) {
         return ssm::fail(SSM_ERR_UNSUPPORTED, "ssd: head dim %d with d_state %d is too large", Pd,
                          a.N);
     const unsigned grid = (unsigned)(a.B * a.H);
-    const size_t smem = sizeof(float) * (size_t)seq_steps(Pd, a.N) * (Pd + 2 * a.N + 1);
+    const int T = seq_steps(Pd, a.N);
+    const size_t smem = sizeof(float) * ((((size_t)T * Pd + 3) & ~(size_t)3) + (size_t)T * (2 * a.N + 1));
     switch (L2) {
         case 1: ssd_seq_kernel<TIN, 1><<<grid, 256, smem, st>>>(a, Pd); break;
         case 2: ssd_seq_kernel<TIN, 2><<<grid, 256, smem, st>>>(a, Pd); break;
@@ -1006,10 +880,12 @@ extern "C" size_t ssm_ssd_workspace(int B, int L, int H, int Pd, int G, int N) {
     if (B <= 0 || L <= 0 || H <= 0 || Pd <= 0 || N <= 0) return 0;
     if (chunked_fallback_shape(Pd, G, N)) return chunked_fallback_bytes(B, L, H, Pd, N);
     if (Pd != P || (N != 64 && N != 128)) return 0;
+    // the larger of the bf16 kernel's and the fp32 kernel's segment states (the size does
+    // not depend on the element type the caller will pass)
     int nchunks, nseg, per;
     plan(B, L, H, nchunks, nseg, per);
-    if (nseg <= 1) return 0;
-    return sizeof(float) * (size_t)B * H * nseg * ((size_t)Pd * N + 1);
+    const size_t bf = nseg <= 1 ? 0 : sizeof(float) * (size_t)B * H * nseg * ((size_t)Pd * N + 1);
+    return std::max(bf, ssm::ssd_f32_workspace(B, L, H, Pd, N));
 }
 
 extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, const float* dt,
@@ -1082,6 +958,10 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
     if (!mfma_path)
         return in_dtype == SSM_F32 ? launch_ssd_seq<float>(a, Pd, st)
                                    : launch_ssd_seq<__bf16>(a, Pd, st);
+    if (in_dtype == SSM_F32)
+        return ssm::ssd_f32((const float*)x, ldx, dt, lddt, dt_bias, softplus, dt_min, dt_max, A,
+                            (const float*)Bm, ldb, (const float*)Cm, ldc, Dsk, y, ldy, B, L, H, G,
+                            N, h0, hT, workspace, workspace_bytes, st);
     plan(B, L, H, a.nchunks, a.nseg, a.chunks_per_seg);
     if (a.nseg > 1) {
         const size_t need = ssm_ssd_workspace(B, L, H, Pd, G, N);
@@ -1090,12 +970,10 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
         a.seg_state = (float*)workspace;
         a.seg_decay = a.seg_state + (size_t)B * H * a.nseg * P * N;
     }
-    if (in_dtype == SSM_F32)
-        return N == 128 ? launch_ssd<float, true, 128, 1>(a, st) : launch_ssd<float, true, 64, 1>(a, st);
-    // bf16: two heads per workgroup when head pairs share a group
+    // two heads per workgroup when head pairs share a group
     if ((H / G) % 2 == 0)
-        return N == 128 ? launch_ssd<__bf16, false, 128, 2>(a, st) : launch_ssd<__bf16, false, 64, 2>(a, st);
-    return N == 128 ? launch_ssd<__bf16, false, 128, 1>(a, st) : launch_ssd<__bf16, false, 64, 1>(a, st);
+        return N == 128 ? launch_ssd<128, 2>(a, st) : launch_ssd<64, 2>(a, st);
+    return N == 128 ? launch_ssd<128, 1>(a, st) : launch_ssd<64, 1>(a, st);
 }
 
 extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float* dt, long lddt,

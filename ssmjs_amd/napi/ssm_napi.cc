@@ -214,6 +214,9 @@ napi_value CtxCreate(napi_env env, napi_callback_info info) {
 }
 
 // ctxDestroy(ctx)                        (device.destroy(), session.ts:592)
+// Runs on the main thread. The library takes the context's lock, so it waits for a job of
+// this device that a pool thread is running, and frees nothing under it. The handle is kept:
+// jobs queued later reach the library, which answers SESSION_DESTROYED.
 napi_value CtxDestroy(napi_env env, napi_callback_info info) {
     napi_value argv[1];
     if (!get_args(env, info, 1, argv)) return nullptr;
@@ -221,7 +224,6 @@ napi_value CtxDestroy(napi_env env, napi_callback_info info) {
     if (!c) return nullptr;
     if (c->c) {
         const ssm_status st = ssm_ctx_destroy(c->c);
-        c->c = nullptr;
         if (st != SSM_OK) throw_status(env, st);
     }
     return nullptr;

@@ -232,12 +232,72 @@ def test_ssd_matches_oracle(B, L, H, G, N, h0, dtype):
     assert e2 <= tol
 
 
+def check_elementwise(got, ref, what, rtol=1e-4, atol_frac=1e-6):
+    """Per element: |got - ref| <= rtol |ref| + atol_frac max|ref| (north_star: max rel err
+    <= 1e-4 fp32; the floor holds elements near zero to a millionth of the tensor's scale)."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    scale = float(np.abs(ref).max())
+    ratio = float((np.abs(got - ref) / (rtol * np.abs(ref) + atol_frac * scale)).max())
+    print(f"  {what}: worst |err|/bound {ratio:.3f}, "
+          f"max|err|/max|ref| {float(np.abs(got - ref).max()) / scale:.2e}", flush=True)
+    assert ratio <= 1.0, f"{what}: beyond {rtol} |ref| + {atol_frac} max|ref|"
+
+
+@pytest.mark.parametrize("B,L,H,h0", [(2, 1000, 8, True), (1, 4096, 4, False)])
+def test_ssd_f32_elementwise_cfg3_dims(B, L, H, h0):
+    """The fp32 SSD at config 3's head dim, d_state and input distributions (x, B, C ~ N(0,1),
+    dt = softplus(N(0,1) - 3), A ~ -U(1,16)): every element of y and of the final state within
+    1e-4 relative plus a 1e-6 floor of the largest magnitude, against the fp64 oracle. A bf16
+    rounding of any operand (about 2^-9 relative) or a bf16 hi/lo split (about 2^-17) fails
+    this bound; fp32 products and sums pass it."""
+    case(f"ssd f32 elementwise B={B} L={L} H={H} h0={h0}")
+    r = rng(5000 + L)
+    P, G, N = 64, 1, 128
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
+    db = (0.1 * r.standard_normal(H)).astype(np.float32)
+    h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32) if h0 else None
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, dt_bias=db, h0=h0a, return_state=True)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(db), True,
+                           h0=dev(h0a) if h0 else None, hT=hd)
+    check_elementwise(host(y), ref, "y")
+    check_elementwise(host(hd), hT, "final state")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ssd_negative_dt_without_softplus(dtype):
+    """softplus off and no lower clamp (dt_min = -inf): dt' keeps the raw, partly negative
+    values. The decay weights exp(acum_i - acum_j) dt'_j then carry dt'_j's sign; the MFMA
+    kernels must give the oracle's finite values (a log of dt' would give NaN)."""
+    case(f"ssd negative dt {dtype}")
+    r = rng(77)
+    B, L, H, G, N, P = 1, 150, 4, 1, 128, 64
+    x, _, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
+    dt = (0.02 * r.standard_normal((B, L, H))).astype(np.float32)   # about half negative
+    A = -r.uniform(0.5, 2.0, H).astype(np.float32)
+    tdt = torch.float32
+    if dtype == "bf16":
+        x, Bm, Cm = _bf(x), _bf(Bm), _bf(Cm)
+        tdt = torch.bfloat16
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, softplus=False, dt_min=-np.inf, return_state=True)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x, tdt), dev(dt), dev(A), dev(Bm, tdt), dev(Cm, tdt), dev(Dk),
+                           None, False, dt_min=-float("inf"), hT=hd)
+    yh = host(y)
+    assert np.isfinite(yh).all()
+    tol = F32_TOL if dtype == "f32" else BF16_TOL
+    assert err(yh, ref) <= tol
+    assert err(host(hd), hT) <= tol
+
+
 @pytest.mark.parametrize("H,L", [(2, 64 * 40 + 17), (32, 64 * 48 + 5), (64, 64 * 24)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_ssd_long_sequence_segments(dtype, H, L):
     """B*H small -> the sequence is cut into segments (state pass + combine + full pass). With
-    512 (batch, head, segment) units per launch the three shapes give 41 segments of one chunk,
-    13 segments of 4 chunks (the last segment and chunk partial) and 8 segments of 3 chunks."""
+    512 (batch, head, segment) units per launch and the bf16 kernel's 64-step chunks the three
+    shapes give 41 segments of one chunk, 13 segments of 4 chunks (the last segment and chunk
+    partial) and 8 segments of 3 chunks; the fp32 kernel's 32-step chunks give 81 segments of
+    one chunk, 14 of 7 and 8 of 6."""
     case(f"ssd segmented {dtype} H={H} L={L}")
     r = rng(4000 + H)
     B, G, N, P = 1, 1, 128, 64
@@ -263,6 +323,8 @@ def test_ssd_long_sequence_segments(dtype, H, L):
     (2, 45, 4, 1, 16, 16, "sequential"),   # no workspace: the sequential kernel
     (2, 50, 4, 2, 16, 32, "sequential"),   # two groups: the sequential kernel
     (1, 40, 2, 1, 8, 128, "dtclamp"),      # dt clamp that binds: the sequential kernel
+    (1, 70, 2, 1, 8, 65, "sequential"),    # odd head dim: x rows of 63*65 floats in LDS
+    (2, 33, 3, 1, 96, 5, "sequential"),    # d_state 96 > 64, head dim 5
 ])
 def test_ssd_fallback_shapes(B, L, H, G, N, P, path):
     """Shapes outside the MFMA kernel (head dim != 64 or d_state not 64/128). With one group,

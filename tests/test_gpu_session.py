@@ -40,9 +40,20 @@ def _checkpoint(version, emb_scale=40.0, seed=11):
     return cfg, checkpoint.pack(dims, T)
 
 
+class Latin1Tokenizer:
+    """Ids 0..255 <-> the characters U+0000..U+00FF, one character per id, so the pieces that
+    completeStream decodes token by token join to exactly the text of the whole sequence."""
+    vocabSize = 256
+
+    def encode(self, text):
+        return [ord(ch) for ch in text]
+
+    def decode(self, tokens):
+        return "".join(chr(t) for t in tokens if 0 <= t < 256)
+
+
 def _options(cfg, blob, **extra):
-    from ssmjs_amd import ByteTokenizer
-    o = {"tokenizer": ByteTokenizer(256), "modelSize": "custom",
+    o = {"tokenizer": Latin1Tokenizer(), "modelSize": "custom",
          "modelConfig": {k: cfg[k] for k in ("dModel", "numLayers", "dState", "nHeads")},
          "mambaVersion": cfg["layers"][0]["type"], "checkpointUrl": "mem://ckpt",
          "fetch": lambda url: blob}
@@ -58,13 +69,16 @@ def test_runtime_generate_greedy_matches_oracle(version):
     rt = SSM.create({"session": _options(cfg, blob)})
     prompt = "Mamba on MI355X"
     text = rt.generate(prompt, {"topK": 1, "maxNewTokens": 20})
-    ids, margins = O.greedy(O.Model(blob), np.array([list(prompt.encode())], np.uint32), 20)
+    ids, margins = O.greedy(O.Model(blob), np.array([Latin1Tokenizer().encode(prompt)],
+                                                    np.uint32), 20)
     assert margins.min() > 1e-3
-    from ssmjs_amd import ByteTokenizer
-    assert text == ByteTokenizer(256).decode(ids[0].tolist())
-    # completeStream (full re-prefill per token, streaming.ts) gives the same tokens
+    assert text == Latin1Tokenizer().decode(ids[0].tolist())
+    # completeStream (full re-prefill per token, streaming.ts:17-49) yields one piece per
+    # token: the same 20 tokens as the recurrent generate and as the oracle's greedy decode
     pieces = list(rt.stream(prompt, {"topK": 1, "maxNewTokens": 20}))
-    assert "".join(pieces) == text or len(pieces) == 20
+    assert len(pieces) == 20
+    assert [Latin1Tokenizer().encode(p_) for p_ in pieces] == [[int(i)] for i in ids[0]]
+    assert "".join(pieces) == text
     rt.destroy()
 
 

@@ -147,3 +147,57 @@ def test_node_session_path_matches_oracle(tmp_path):
     # mean NLL moves by at most twice the logits' error (1e-4 of their range)
     assert abs(np.log(out["ppl"]) - nll) <= 2e-4 * np.abs(lgt).max()
     sys.stdout.flush()
+
+
+@pytest.mark.gpu
+@needs_addon
+def test_node_two_models_one_device(tmp_path):
+    """Two HybridMambaModels on one initWebGPU device driven with Promise.all (their calls
+    run on libuv pool threads at the same time, serialised by the library's context lock):
+    each model's greedy ids and logits match the oracle. Then device.destroy() while a
+    generate is in flight: the generate either completes or rejects with SESSION_DESTROYED,
+    the process does not crash, and later calls reject with SESSION_DESTROYED (the reference
+    keeps one model per session and device, session.ts:359,589-592)."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    print("[case] node: two models on one device, destroy while pending", flush=True)
+    from oracle import oracle as O
+    from ssmjs_amd import backend, checkpoint
+    cfgs = [{"vocabSize": 256, "dModel": 128, "numLayers": 2, "dState": 64, "dConv": 4,
+             "expand": 2, "nHeads": 2, "nGroups": 1, "layers": [{"type": "mamba2"}] * 2},
+            {"vocabSize": 256, "dModel": 96, "numLayers": 3, "dState": 16, "dConv": 4,
+             "expand": 2, "nHeads": 2, "layers": [{"type": "mamba1"}] * 3}]
+    blobs, args = [], []
+    d = backend.Device(0)
+    for i, cfg in enumerate(cfgs):
+        m = backend.Model(d, cfg, seed=31 + i)
+        dims, T = checkpoint.unpack(m.export_weights())
+        m.destroy()
+        T["embedding"] = T["embedding"] * 40.0
+        blob = checkpoint.pack(dims, T)
+        blobs.append(blob)
+        ck, cj = tmp_path / f"w{i}.ssmw", tmp_path / f"cfg{i}.json"
+        ck.write_bytes(blob)
+        cj.write_text(json.dumps(cfg))
+        args += [str(ck), str(cj)]
+    d.destroy()
+    prompt = list(b"two models")
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "napi_concurrent.js"), *args,
+                        ",".join(map(str, prompt)), "12"],
+                       capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout)
+    for key, fkey, blob in (("genA", "fwdA", blobs[0]), ("genB", "fwdB", blobs[1])):
+        om = O.Model(blob)
+        ids, margins = O.greedy(om, np.array([prompt], np.uint32), 12)
+        assert margins.min() > 1e-3
+        assert out[key] == prompt + ids[0].tolist()
+        ref = om.forward(np.array([prompt], np.uint32))[0]
+        lg = np.array(out[fkey], np.float32).reshape(len(prompt), 256)
+        assert np.abs(lg - ref).max() / np.abs(ref).max() <= 1e-4
+    assert out["genA2"] == out["genA"]
+    assert out["during"]["ok"] or out["during"]["code"] == "SESSION_DESTROYED", out["during"]
+    if out["during"]["ok"]:
+        assert out["during"]["len"] == len(prompt) + 400
+    assert out["after"] == "SESSION_DESTROYED"
