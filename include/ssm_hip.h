@@ -201,6 +201,18 @@ size_t ssm_sample_workspace(int rows, int n);
 ssm_status ssm_sample(const float* logits, long ld, int rows, int n, double temperature,
                       int top_k, double top_p, const double* u, uint32_t* out, void* workspace,
                       size_t workspace_bytes, void* stream);
+/* ssm_sample without a workspace argument and without any device allocation. No counterpart
+ * in the reference: it is for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The workspace is a static 32 MiB
+ * device array per GPU (the library holds it until the process ends), so rows and n must
+ * satisfy ssm_sample_workspace(rows, n) <= 32 MiB (e.g. 64 rows of 128000 logits);
+ * larger calls return SSM_ERR_UNSUPPORTED. Its device address is resolved by ssm_ctx_create
+ * (else on the first call on a device, for the device current on the calling thread). Calls
+ * that overlap on one GPU share the array and race: serialise them. Results are identical to
+ * ssm_sample's. */
+ssm_status ssm_sample_noalloc(const float* logits, long ld, int rows, int n, double temperature,
+                              int top_k, double top_p, const double* u, uint32_t* out,
+                              void* stream);
 
 /* ------------------------------------------------------------------ model level */
 #define SSM_LAYER_MAMBA1 1

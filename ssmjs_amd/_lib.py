@@ -108,6 +108,7 @@ PROTOTYPES = {
     "ssm_argmax": (_i, [_fp, _l, _i, _i, _vp, _vp]),
     "ssm_sample_workspace": (_sz, [_i, _i]),
     "ssm_sample": (_i, [_fp, _l, _i, _i, _d, _i, _d, _vp, _vp, _vp, _sz, _vp]),
+    "ssm_sample_noalloc": (_i, [_fp, _l, _i, _i, _d, _i, _d, _vp, _vp, _vp]),
     "ssm_model_create": (_i, [_vp, C.POINTER(ssm_config), C.c_uint64, C.POINTER(_vp)]),
     "ssm_model_destroy": (_i, [_vp]),
     "ssm_model_config": (_i, [_vp, C.POINTER(ssm_config)]),

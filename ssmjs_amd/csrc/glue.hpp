@@ -21,6 +21,8 @@ ssm_status launch_argmax(const float* x, long ldx, int rows, int n, uint32_t* ou
 // sampleToken on the device (sample.hip): sample_ok says whether (n, topK) is supported.
 bool sample_ok(int n, int top_k);
 size_t sample_workspace(int rows, int n);
+// Device address of ssm_sample_noalloc's static scratch on the current device.
+ssm_status sample_scratch(void** out);
 ssm_status launch_sample(const float* logits, long ld, int rows, int n, double temperature,
                          int top_k, double top_p, const double* u, uint32_t* out,
                          void* workspace, hipStream_t st);

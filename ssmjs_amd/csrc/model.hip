@@ -248,6 +248,17 @@ extern "C" ssm_status ssm_ctx_create(int device_ordinal, ssm_ctx** out) {
         delete c;
         return ssm::from_hip(e, "ssm_ctx_create");
     }
+    // the allocation-free sampler's scratch address on this device, resolved here so that a
+    // caller's first ssm_sample_noalloc (possibly under graph capture) makes no runtime lookup
+    {
+        void* scratch = nullptr;
+        const ssm_status sr = ssm::sample_scratch(&scratch);
+        if (sr != SSM_OK) {
+            hipStreamDestroy(c->own);
+            delete c;
+            return sr;
+        }
+    }
     std::snprintf(c->arch, sizeof c->arch, "%s", prop.gcnArchName);
     c->cus = prop.multiProcessorCount;
     c->mem = prop.totalGlobalMem;

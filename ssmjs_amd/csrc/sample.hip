@@ -21,6 +21,8 @@
 // the nucleus cut only if a cumulative probability lies within ~1e-15 of topP.
 #include <cstdint>
 
+#include <mutex>
+
 #include "common.hpp"
 #include "glue.hpp"
 
@@ -568,6 +570,71 @@ static_assert(kEPT % 16 == 0, "register keys are visited in groups of 16 slices"
 static_assert(kMaxSlices <= kSliceThreads, "one slice maximum per exp-kernel thread");
 
 extern "C" size_t ssm_sample_workspace(int rows, int n) { return ssm::sample_workspace(rows, n); }
+
+// ---------------------------------------------------------------- allocation-free variant
+// ssm_sample_noalloc runs the kernels of ssm_sample with their workspace in `scratch`, a
+// file-scope device array of kScratchBytes that each GPU holds from the library's load until
+// the process ends. Host code never passes the array's name to a kernel (on the host it is
+// only a stand-in symbol): its device address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and kept in g_scratch. Every call on a GPU
+// shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race on it.
+// The kernels write every workspace slot before they read it, so nothing is cleared.
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)32 << 20;   // 32 MiB per GPU
+constexpr int kMaxDevices = 64;
+
+__device__ __attribute__((aligned(256))) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+}  // namespace
+
+namespace ssm {
+
+// Device address of `scratch` on the current device (looked up on the first call per device).
+ssm_status sample_scratch(void** out) {
+    int dev = 0;
+    SSM_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(SSM_ERR_INVALID_ARG, "sample scratch: device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return from_hip(e, "hipGetSymbolAddress(sample scratch)");
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return SSM_OK;
+}
+
+}  // namespace ssm
+
+extern "C" ssm_status ssm_sample_noalloc(const float* logits, long ld, int rows, int n,
+                                         double temperature, int top_k, double top_p,
+                                         const double* u, uint32_t* out, void* stream) {
+    SSM_REQUIRE(logits && u && out, "ssm_sample_noalloc: null logits/u/out");
+    SSM_REQUIRE(rows >= 0 && n >= 1 && ld >= n, "ssm_sample_noalloc: bad shape");
+    SSM_REQUIRE(top_k >= 1, "ssm_sample_noalloc: topK must be at least 1");
+    if (!ssm::sample_ok(n, top_k))
+        return ssm::fail(SSM_ERR_UNSUPPORTED,
+                         "ssm_sample_noalloc: needs n <= %d and topK <= %d (n=%d topK=%d)", kMaxN,
+                         kMaxK, n, top_k);
+    const size_t need = ssm::sample_workspace(rows, n);
+    if (need > kScratchBytes)
+        return ssm::fail(SSM_ERR_UNSUPPORTED,
+                         "ssm_sample_noalloc: %d rows of %d logits need %zu bytes of scratch; the "
+                         "static scratch holds %zu (use ssm_sample with a workspace)",
+                         rows, n, need, kScratchBytes);
+    if (rows == 0) return SSM_OK;
+    void* ws = nullptr;
+    ssm_status r = ssm::sample_scratch(&ws);
+    if (r != SSM_OK) return r;
+    return ssm::launch_sample(logits, ld, rows, n, temperature, top_k, top_p, u, out, ws,
+                              (hipStream_t)stream);
+}
 
 extern "C" ssm_status ssm_sample(const float* logits, long ld, int rows, int n,
                                  double temperature, int top_k, double top_p, const double* u,
