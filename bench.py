@@ -3,11 +3,20 @@
 
 Metric: SSM tokens/s on 1xMI355X (prefill + decode) + % of HBM/MFMA roofline.
 
-Workloads (--workload picks one, default cfg2):
+The headline line is config 3 at the reference's precision: the Mamba-2 SSD layer prefill
+(B=8, L=4096, 64 heads x 64, d_state 128, one group, chunkLen 256) in fp32, the largest of
+BASELINE.json's configurations that runs on one GPU. Its `value` is the SSD core's tokens/s;
+its `roofline` is the SSD kernel against the fp32 matrix-core peak with the SURVEY 8(d)
+algorithmic FLOP count. The default run also reports, under "extra": the whole cfg3 layer
+(in_proj -> conv -> SSD -> gated RMSNorm -> out_proj) timed per stage, the SSD with bf16
+inputs, the cfg2 Mamba-1 block, the cfg4 decode step and the cfg5 long-context SSD.
+
+Workloads (--workload picks one line; the default is cfg3 with the extras):
   cfg1  Mamba-1 causal conv1d + selective scan, fp32, B=1 L=256 D=512 N=16 (parity case)
   cfg2  Mamba-1 block forward, fp32, d=768 D=1536 N=16 R=48 K=4, B=4 L=2048 (in_proj ->
         conv/SiLU -> x_proj/dt_proj -> scan (D skip, SiLU(z) gate) -> out_proj)
-  cfg3  Mamba-2 SSD prefill core, B=8 L=4096 H=64 P=64 N=128 G=1; --dtype f32|bf16
+  cfg3  Mamba-2 SSD prefill core, B=8 L=4096 H=64 P=64 N=128 G=1; --dtype f32 (default) | bf16
+  cfg3layer  the whole fp32 Mamba-2 layer at cfg3's dimensions (d_model 2048), per stage
   cfg4  Mamba-2 24-layer decode, d=1024 H=32 P=64 N=128 V=32000, 64 cached sequences,
         one greedy step (24 layers + LM head + argmax) per bench step, fp32; --sampling
         draws the token with sampleToken on the device instead (T 0.8, topK 50, topP 0.9)
@@ -17,11 +26,13 @@ HBM. Timing: W untimed warmup steps, then K steps between HIP events on the stre
 library launches on (torch's current stream, handed to the library context).
 
 The roofline object names the dominant kernel (stage) of the step, its algorithmic FLOPs or
-bytes per launch, and its average duration from HIP events recorded around it inside the
-library during a second, profiled pass of K steps (cfg4: the state update is timed on its own,
-back to back over the 24 layers' states, since the per-stage events of the profiled pass add
-their own overhead to a 25 us kernel). The cpu_baseline object times the CPU restatement
-(oracle/) single-threaded on a bounded slice of the same workload.
+bytes per launch, and its average duration from HIP events on that stream (for multi-stage
+workloads, events the library records around each stage during a second, profiled pass of K
+steps; cfg4's state update is timed on its own, back to back over the 24 layers' states).
+The cpu_baseline object times the restatements of the reference path on the host: the C
+oracle (oracle/) with OpenMP on every host core, and a single-threaded JavaScript
+restatement (oracle/ssm_ref.js, the reference's own execution model), on a bounded slice of
+the same workload.
 """
 from __future__ import annotations
 
@@ -46,10 +57,15 @@ METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 TRAFFIC = {
     ("cfg2", "m1.in_proj"): 339_224_576,               # hipBLASLt sgemm (tile re-reads)
     ("cfg3", "bf16"): 848_125_952,                     # ssd_kernel (two heads per workgroup)
-    ("cfg3", "f32"): 1_166_376_960,                    # ssd_kernel (fp32 inputs)
+    ("cfg3", "f32"): 1_165_402_958,                    # ssd_f32_kernel
     ("cfg4", "m2.step.state_update"): 136_517_632,     # m2_update_kernel
-    ("cfg5", "bf16"): 1_209_127_936,                   # state pass + combine + full pass
+    ("cfg5", "bf16"): 1_200_675_840,                   # state pass + combine + full pass
 }
+# The commit of the kernels each TRAFFIC entry was measured on (profiles/hbm_traffic.md);
+# an entry goes stale when its kernel changes after that commit.
+TRAFFIC_MEASURED_AT = {k: "e7034fa" for k in TRAFFIC}
+TRAFFIC_MEASURED_AT.update({("cfg3", "f32"): "805df87", ("cfg3", "bf16"): "805df87",
+                            ("cfg5", "bf16"): "805df87"})
 
 
 def parse():
@@ -57,10 +73,13 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="cfg2",
-                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "copy"])
+    ap.add_argument("--workload", default=None,
+                    choices=["cfg1", "cfg2", "cfg3", "cfg3layer", "cfg4", "cfg5", "copy"],
+                    help="one line for this workload only (default: cfg3 fp32 plus extras)")
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default run: skip the extra workloads after the cfg3 line")
     ap.add_argument("--sampling", action="store_true",
                     help="cfg4: draw each token with sampleToken on the device (temperature "
                          "0.8, topK 50, topP 0.9) instead of the greedy argmax")
@@ -97,7 +116,8 @@ def profiled_stages(dev, torch, fn, steps):
     return {k: (n, ms / n) for k, (n, ms) in rep.items()}   # stage -> (launches, avg ms)
 
 
-def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None, traffic=None):
+def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None, traffic=None,
+             traffic_key=None):
     """Achieved rate of one kernel/stage against its binding peak."""
     t = avg_ms * 1e-3
     if bound is None:
@@ -112,27 +132,72 @@ def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None, traf
         ach = nbytes / t / 1e9
         peak = HBM_PEAK_GBS
         unit = "GB/s"
-    return {"kernel": name, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
-            "frac": round(ach / peak, 4), "traffic": traffic, "avg_ms": round(avg_ms, 5),
-            "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
+    out = {"kernel": name, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+           "frac": round(ach / peak, 4), "traffic": traffic, "avg_ms": round(avg_ms, 5),
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
+    if traffic is not None and traffic_key is not None:
+        out["traffic_measured_at"] = TRAFFIC_MEASURED_AT.get(traffic_key)
+    return out
 
 
-def cpu_time(fn, budget_s=20.0):
-    """Run fn at least once and until ~budget; return seconds per call."""
+def cpu_time(fn, budget_s=20.0, min_runs=3):
+    """Run fn at least once and until ~budget (at most min_runs if the budget allows more);
+    return seconds per call."""
     t0 = time.perf_counter()
     n = 0
     while True:
         fn()
         n += 1
         el = time.perf_counter() - t0
-        if el > budget_s or n >= 3:
+        if el > budget_s or n >= min_runs:
             return el / n
+
+
+def host_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def js_ssd_baseline(np, x, dt, A, Bm, Cm, D):
+    """The single-threaded JavaScript restatement (oracle/ssm_ref.js) on these fp32 inputs
+    under the host's Node: (seconds of the recurrence, y), or None without node."""
+    import shutil
+    import subprocess
+    import tempfile
+    node = shutil.which("node")
+    if node is None:
+        return None
+    B, L, H, P = x.shape
+    N = Bm.shape[-1]
+    here = os.path.dirname(os.path.abspath(__file__))
+    with tempfile.TemporaryDirectory() as td:
+        inp, outp = os.path.join(td, "in.bin"), os.path.join(td, "out.bin")
+        with open(inp, "wb") as f:
+            for a in (x, dt, A, Bm, Cm, D):
+                f.write(np.ascontiguousarray(a, np.float32).tobytes())
+        r = subprocess.run([node, os.path.join(here, "oracle", "ssm_ref.js"), inp, outp,
+                            str(B), str(L), str(H), str(P), str(N)],
+                           capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            log("[bench] JS baseline failed:", r.stderr[-400:])
+            return None
+        sec = json.loads(r.stdout)["seconds"]
+        y = np.fromfile(outp, np.float32).reshape(B, L, H, P)
+    return sec, y
 
 
 # ---------------------------------------------------------------- workloads
 
 def w_cfg2(torch, np, dev, args):
-    from ssmjs_amd import backend
+    from ssmjs_amd import _lib, backend
     B, L, d, N, R, K = 4, 2048, 768, 16, 48, 4
     D = 2 * d
     T = B * L
@@ -140,13 +205,16 @@ def w_cfg2(torch, np, dev, args):
            "nHeads": 12, "dtRank": R, "layers": [{"type": "mamba1"}]}
     m = backend.Model(dev, cfg, seed=1002)
     g = torch.Generator(device="cuda").manual_seed(1002)
-    x = torch.randn(B, L, d, device="cuda", generator=g)
-    y = torch.empty_like(x)
-
-    from ssmjs_amd import _lib
+    # inputs rotate over 12 batches (302 MB, more than the 256 MB last-level cache), so a
+    # step's input is not served from the cache of the previous ones
+    xs = [torch.randn(B, L, d, device="cuda", generator=g) for _ in range(12)]
+    y = torch.empty_like(xs[0])
+    k = [0]
 
     def step():
-        _lib.call("ssm_mixer_forward_device", m.handle, 0, x.data_ptr(), y.data_ptr(), B, L)
+        _lib.call("ssm_mixer_forward_device", m.handle, 0, xs[k[0] % 12].data_ptr(),
+                  y.data_ptr(), B, L)
+        k[0] += 1
 
     steps, warm = args.steps or 20, args.warmup if args.warmup is not None else 5
     ms = timed(torch, step, steps, warm)
@@ -161,10 +229,11 @@ def w_cfg2(torch, np, dev, args):
         "m1.out_proj": (2.0 * T * D * d, 4.0 * (T * D + d * D + T * d)),
     }
     stages = {}
-    for k, (n, avg) in st.items():
-        f, b = alg[k]
+    for kk, (n, avg) in st.items():
+        f, b = alg[kk]
         bound = "hbm" if f is None else None
-        stages[k] = roofline(k, avg, f, b, "f32", bound, TRAFFIC.get(("cfg2", k)))
+        stages[kk] = roofline(kk, avg, f, b, "f32", bound, TRAFFIC.get(("cfg2", kk)),
+                              ("cfg2", kk))
     dom = max(stages.values(), key=lambda r: r["avg_ms"])
     out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
            "dtype": "f32",
@@ -172,19 +241,20 @@ def w_cfg2(torch, np, dev, args):
                                   "x_proj/dt_proj, selective scan + D skip + SiLU(z) gate, "
                                   "out_proj)", "batch": B, "seq_len": L, "d_model": d,
                       "d_inner": D, "d_state": N, "dt_rank": R, "d_conv": K,
-                      "tokens_per_step": T},
+                      "tokens_per_step": T, "input_rotation": "12 batches, 302 MB"},
            "roofline": dom, "stages": stages}
     if not args.no_cpu_baseline:
         from oracle import oracle as O
         blob = m.export_weights()
         om = O.Model(blob)
         Ls = 512
-        xs = x[:1, :Ls].cpu().numpy()
-        sec = cpu_time(lambda: om.mixer(0, xs))
-        out["cpu_baseline"] = {"value": Ls / sec, "unit": "tokens/s", "cores": 1, "kind": "port",
-                               "sample": f"B=1, L={Ls} slice of the cfg2 input through the same "
-                                         "block weights; single-threaded C oracle (fp64 "
-                                         "accumulate), oracle/ssm_oracle.c"}
+        xn = xs[0][:1, :Ls].cpu().numpy()
+        sec = cpu_time(lambda: om.mixer(0, xn))
+        out["cpu_baseline"] = dict(
+            {"value": Ls / sec, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+             "sample": f"B=1, L={Ls} slice of the cfg2 input through the same block weights; "
+                       "C oracle (oracle/ssm_oracle.c, fp64 accumulate), OpenMP"},
+            **host_info())
     m.destroy()
     return out
 
@@ -224,9 +294,9 @@ def w_cfg1(torch, np, dev, args):
             un = O.causal_conv1d(xn, wn, None)
             O.selective_scan(un, dtn, An, Bn, Cn, np.ones(D, np.float32), zn, None, True)
         sec = cpu_time(cpu, 10.0)
-        out["cpu_baseline"] = {"value": B * L / sec, "unit": "tokens/s", "cores": 1,
-                               "kind": "port", "sample": "the full cfg1 workload, single-threaded "
-                                                         "C oracle"}
+        out["cpu_baseline"] = dict(
+            {"value": B * L / sec, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+             "sample": "the full cfg1 workload; C oracle, OpenMP"}, **host_info())
     return out
 
 
@@ -242,7 +312,20 @@ def ssd_inputs(torch, B, L, H, P, N, dtype, bc_std, seed):
     return x, dt, A, Bm, Cm, Dk
 
 
-def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype):
+def ssd_alg(B, L, H, P, N, esz, Q=256):
+    """SURVEY 8(d)'s algorithmic counts for the SSD core at chunk length Q (the config's
+    chunkLen): causal FLOPs (C B^T once per chunk for one group; (C B^T . L) X; chunk
+    states; state-to-output) and bytes (x, B, C in the input type; dt, y, final state fp32)."""
+    T = B * L
+    nchunk = T / Q
+    flops = (2.0 * Q * Q * N / 2 * nchunk          # C B^T (causal, shared across heads, G=1)
+             + 2.0 * Q * Q * P / 2 * nchunk * H    # intra-chunk (CB^T . L) X
+             + 2.0 * Q * P * N * nchunk * H * 2)   # chunk states + state-to-output
+    nbytes = esz * (T * H * P + 2.0 * T * N) + 4.0 * (T * H + T * H * P + B * H * P * N)
+    return flops, nbytes
+
+
+def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, with_cpu=True):
     from ssmjs_amd import kernels
     P, N = 64, 128
     dtype = args.dtype or default_dtype
@@ -259,39 +342,105 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype):
     ms = timed(torch, step, steps, warm)
     T = B * L
     esz = 2 if dtype == "bf16" else 4
-    Q = 256
-    nchunk = T / Q
-    flops = (2.0 * Q * Q * N / 2 * nchunk          # C B^T (causal, shared across heads, G=1)
-             + 2.0 * Q * Q * P / 2 * nchunk * H    # intra-chunk (CB^T . L) X
-             + 2.0 * Q * P * N * nchunk * H * 2)   # chunk states + state-to-output
-    nbytes = esz * (T * H * P + 2.0 * T * N) + 4.0 * (T * H + T * H * P + B * H * P * N)
+    flops, nbytes = ssd_alg(B, L, H, P, N, esz)
+    prec = "bf16" if dtype == "bf16" else "f32"
+    kern = ("ssd_kernel (bf16 inputs, v_mfma_f32_16x16x32_bf16)" if dtype == "bf16" else
+            "ssd_f32_kernel (fp32, v_mfma_f32_16x16x4_f32)")
+    key = (name[:4], dtype)
     out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
            "dtype": dtype,
            "config": {"workload": name, "batch": B, "seq_len": L, "heads": H, "head_dim": P,
-                      "d_state": N, "groups": 1, "chunk_len": Q, "input_dtype": dtype,
+                      "d_state": N, "groups": 1, "chunk_len": 256, "input_dtype": dtype,
                       "accumulate": "f32"},
-           "roofline": roofline("ssd_chunk_scan", ms, flops, nbytes,
-                                "bf16" if dtype == "bf16" else "f32",
-                                traffic=TRAFFIC.get((name[:4], dtype)))}
-    out["roofline"]["mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 /
-                                         PEAK_TFLOPS["bf16" if dtype == "bf16" else "f32"], 4)
-    out["roofline"]["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-    if not args.no_cpu_baseline:
+           "roofline": roofline(kern, ms, flops, nbytes, prec, traffic=TRAFFIC.get(key),
+                                traffic_key=key)}
+    rl = out["roofline"]
+    rl["mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[prec], 4)
+    rl["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if dtype == "f32":
+        # the kernel's own MFMA work per launch: 32-step chunks, 16x16 tiles (the diagonal
+        # C B^T tiles whole), C B^T once per head
+        QF = 32
+        per_chunk_head = 3 * 32 + 4 * (2 * 32 + 3 * 4 + 2 * 32)   # 16x16x4 MFMAs
+        rl["issued_mfma_flops"] = per_chunk_head * 2048.0 * (T / QF) * H
+    if with_cpu and not args.no_cpu_baseline:
         from oracle import oracle as O
-        Ls = 256
-        xs = x[:1, :Ls, :8].float().cpu().numpy()
-        a = (xs, dt[:1, :Ls, :8].cpu().numpy(), A[:8].cpu().numpy(),
-             Bm[:1, :Ls].float().cpu().numpy(), Cm[:1, :Ls].float().cpu().numpy(),
-             Dk[:8].cpu().numpy())
-        sec = cpu_time(lambda: O.ssd(*a), 10.0)
-        # tokens/s for all H heads: the sample ran 8 of H heads
-        out["cpu_baseline"] = {"value": Ls / (sec * H / 8), "unit": "tokens/s", "cores": 1,
-                               "kind": "port",
-                               "sample": f"B=1, L={Ls}, 8 of {H} heads of the same inputs, "
-                                         "scaled to all heads; single-threaded C oracle "
-                                         "(sequential SSD recurrence)"}
+        Ls = 2048
+        xs = x[:1, :Ls].float().cpu().numpy()
+        smp = (xs, dt[:1, :Ls].cpu().numpy(), A.cpu().numpy(), Bm[:1, :Ls].float().cpu().numpy(),
+               Cm[:1, :Ls].float().cpu().numpy(), Dk.cpu().numpy())
+        sec = cpu_time(lambda: O.ssd(*smp), 20.0)
+        cb = {"value": Ls / sec, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+              "sample": f"B=1, L={Ls}, all {H} heads of the same inputs (fp32); C oracle "
+                        "(oracle/ssm_oracle.c, sequential SSD recurrence, fp64 accumulate), "
+                        "OpenMP over heads"}
+        cb.update(host_info())
+        # the reference's execution model: one JS thread (8 of the heads, scaled to all)
+        Lj, Hj = 256, 8
+        sub = tuple(np.ascontiguousarray(a) for a in (smp[0][:, :Lj, :Hj], smp[1][:, :Lj, :Hj],
+                                                       smp[2][:Hj], smp[3][:, :Lj],
+                                                       smp[4][:, :Lj], smp[5][:Hj]))
+        js = js_ssd_baseline(np, *sub)
+        if js is not None:
+            sec_js, y_js = js
+            ref = O.ssd(*sub)
+            cb["js_single_thread"] = {
+                "value": Lj / (sec_js * H / Hj), "unit": "tokens/s", "cores": 1,
+                "kind": "port",
+                "sample": f"B=1, L={Lj}, {Hj} of {H} heads, scaled to all heads; "
+                          "oracle/ssm_ref.js under Node (double arithmetic, float32 storage)",
+                "agrees_with_c_oracle": bool(np.array_equal(y_js, ref))}
+        out["cpu_baseline"] = cb
     return out
 
+
+def w_cfg3layer(torch, np, dev, args):
+    """The whole cfg3 Mamba-2 layer in fp32 at cfg3's dimensions (d_model 2048, expand 2,
+    64 heads x 64, d_state 128, one group, conv 4; B=8, L=4096), one ssm_mixer_forward_device
+    per step, timed per stage."""
+    from ssmjs_amd import _lib, backend
+    B, L, d, H, N, K = 8, 4096, 2048, 64, 128, 4
+    D, P = 2 * d, 64
+    T = B * L
+    cfg = {"vocabSize": 16, "dModel": d, "numLayers": 1, "dState": N, "dConv": K, "expand": 2,
+           "nHeads": H, "nGroups": 1, "layers": [{"type": "mamba2"}]}
+    m = backend.Model(dev, cfg, seed=1003)
+    g = torch.Generator(device="cuda").manual_seed(1003)
+    x = torch.randn(B, L, d, device="cuda", generator=g)
+    y = torch.empty_like(x)
+
+    def step():
+        _lib.call("ssm_mixer_forward_device", m.handle, 0, x.data_ptr(), y.data_ptr(), B, L)
+
+    steps, warm = args.steps or 5, args.warmup if args.warmup is not None else 2
+    steps = min(steps, 10)
+    ms = timed(torch, step, steps, warm)
+    st = profiled_stages(dev, torch, step, steps)
+    cd, nin = D + 2 * N, 2 * D + 2 * N + H
+    sf, sb = ssd_alg(B, L, H, P, N, 4)
+    alg = {
+        "m2.in_proj": (2.0 * T * d * nin, 4.0 * (T * d + nin * d + T * nin)),
+        "m2.conv": (None, 4.0 * (T * cd * 2 + cd * (K + 1))),
+        "m2.ssd": (sf, sb),
+        "m2.gated_norm": (None, 4.0 * (T * D * 3 + D)),
+        "m2.out_proj": (2.0 * T * D * d, 4.0 * (T * D + d * D + T * d)),
+    }
+    stages = {}
+    for kk, (n, avg) in st.items():
+        f, b = alg[kk]
+        stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None)
+    dom = max(stages.values(), key=lambda r: r["avg_ms"])
+    layer_flops = sum(f for f, _ in alg.values() if f)
+    out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+           "dtype": "f32",
+           "config": {"workload": "cfg3 layer: Mamba-2 layer prefill (in_proj, conv1d+SiLU over "
+                                  "x/B/C, SSD, gated RMSNorm, out_proj)",
+                      "batch": B, "seq_len": L, "d_model": d, "heads": H, "head_dim": P,
+                      "d_state": N, "groups": 1, "tokens_per_step": T},
+           "roofline": dom, "stages": stages,
+           "layer_mfma_frac": round(layer_flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4)}
+    m.destroy()
+    return out
 
 def time_state_update(torch, st, nl, B, H, P, N, reps):
     """Average launch duration of the decode step's dominant kernel, the Mamba-2 state update
@@ -410,10 +559,10 @@ def w_cfg4(torch, np, dev, args):
         ost = om.new_state(1)
         tok = np.array([1], np.uint32)
         sec = cpu_time(lambda: ost.decode(tok), 10.0)
-        out["cpu_baseline"] = {"value": 1.0 / sec, "unit": "tokens/s", "cores": 1,
-                               "kind": "port",
-                               "sample": "one recurrent decode step of 1 sequence through the same "
-                                         "24-layer weights (single-threaded C oracle)"}
+        out["cpu_baseline"] = dict(
+            {"value": 1.0 / sec, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+             "sample": "one recurrent decode step of 1 sequence through the same 24-layer "
+                       "weights; C oracle, OpenMP over projection rows"}, **host_info())
         del blob, om
     st.destroy()
     m.destroy()
@@ -454,29 +603,59 @@ def main():
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     dev.set_stream(stream.cuda_stream)
-    log(f"[bench] device {dev.arch} with {dev.compute_units} CUs; workload {args.workload}")
+    log(f"[bench] device {dev.arch} with {dev.compute_units} CUs; "
+        f"workload {args.workload or 'cfg3 (+ extras)'}")
     if args.workload == "copy":
         print(json.dumps(w_copy(torch, args)), flush=True)
         dev.destroy()
         return
-    if args.workload == "cfg1":
-        r = w_cfg1(torch, np, dev, args)
-    elif args.workload == "cfg2":
-        r = w_cfg2(torch, np, dev, args)
-    elif args.workload == "cfg3":
-        r = ssd_workload(torch, np, dev, args, 8, 4096, 64, 1.0,
-                         "cfg3: Mamba-2 SSD prefill core (chunked SSD, fused)", "bf16")
-    elif args.workload == "cfg4":
-        r = w_cfg4(torch, np, dev, args)
-    else:
-        r = ssd_workload(torch, np, dev, args, 1, 65536, 32, 128 ** -0.25,
-                         "cfg5: Mamba-2 SSD long-context prefill core", "bf16")
+    cfg3_name = "cfg3: Mamba-2 SSD prefill core (chunked SSD, fused)"
+    cfg5_name = "cfg5: Mamba-2 SSD long-context prefill core"
+    runs = {
+        "cfg1": lambda a: w_cfg1(torch, np, dev, a),
+        "cfg2": lambda a: w_cfg2(torch, np, dev, a),
+        "cfg3": lambda a: ssd_workload(torch, np, dev, a, 8, 4096, 64, 1.0, cfg3_name, "f32"),
+        "cfg3layer": lambda a: w_cfg3layer(torch, np, dev, a),
+        "cfg4": lambda a: w_cfg4(torch, np, dev, a),
+        "cfg5": lambda a: ssd_workload(torch, np, dev, a, 1, 65536, 32, 128 ** -0.25, cfg5_name,
+                                       "bf16"),
+    }
+    r = runs[args.workload or "cfg3"](args)
+    extra = {}
+    if args.workload is None and not args.no_extras:
+        # the other configurations, each with its own default steps, no CPU baseline
+        for key, wl, dtype in (("cfg3_layer_f32", "cfg3layer", None), ("cfg3_bf16", "cfg3", "bf16"),
+                               ("cfg2", "cfg2", None), ("cfg4", "cfg4", None),
+                               ("cfg5", "cfg5", None)):
+            a2 = argparse.Namespace(**vars(args))
+            a2.steps, a2.warmup, a2.no_cpu_baseline, a2.dtype = None, None, True, dtype
+            log(f"[bench] extra {key}")
+            try:
+                e = runs[wl](a2)
+            except Exception as err:  # noqa: BLE001 (an extra never hides the headline line)
+                log(f"[bench] extra {key} failed: {err}")
+                continue
+            rl = e["roofline"]
+            extra[key] = {"workload": e["config"]["workload"], "value": round(e["value"], 3),
+                          "unit": "tokens/s", "ms_per_step": round(e["ms_per_step"], 5),
+                          "steps": e["steps"], "dtype": e["dtype"],
+                          "roofline": {k: rl[k] for k in ("kernel", "bound", "achieved", "peak",
+                                                          "unit", "frac", "avg_ms", "traffic")}}
+            if "stages" in e:
+                extra[key]["stages"] = {k: {kk: v[kk] for kk in ("bound", "achieved", "unit",
+                                                                 "frac", "avg_ms")}
+                                        for k, v in e["stages"].items()}
+            for k in ("layer_mfma_frac", "step_hbm_frac"):
+                if k in e:
+                    extra[key][k] = e[k]
     line = {"metric": METRIC, "value": round(r.pop("value"), 3), "unit": "tokens/s",
             "n_gpus": 1, "steps": r.pop("steps"), "warmup": r.pop("warmup"),
             "ms_per_step": round(r.pop("ms_per_step"), 5), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": r.pop("dtype"),
             "data": "synthetic (seeded; random-init weights of the named architecture)"}
     line.update(r)
+    if extra:
+        line["extra"] = extra
     dev.destroy()
     print(json.dumps(line), flush=True)
 
