@@ -19,7 +19,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libssm_oracle.so")
+# SSM_ORACLE_LIB selects another build of the same source (the sanitizer build of
+# tests/test_sanitizers.py)
+_LIB_PATH = os.environ.get("SSM_ORACLE_LIB") or os.path.join(_HERE, "libssm_oracle.so")
 _lib = None
 
 _fp = C.POINTER(C.c_float)

@@ -59,8 +59,28 @@ ssm_status from_hip(hipError_t e, const char* what) {
     return fail(code, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Fault injection for tests of the error contract (session.ts:262-270,393-401): the
+// environment variable SSM_HIP_FAULT names a failure the library reports as if HIP had
+// returned it. "nodevice": ssm_ctx_create finds no device; "alloc": every device allocation
+// of the library fails (out of memory); "launch": every launch check reports a failed launch
+// after the (normally running) kernel was queued. Read at each use, so a process can switch it.
+bool fault(const char* kind) {
+    const char* f = std::getenv("SSM_HIP_FAULT");
+    return f && std::strcmp(f, kind) == 0;
+}
+
+hipError_t dev_malloc(void** p, size_t bytes) {
+    if (fault("alloc")) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
 ssm_status check_launch(const char* what) {
     hipError_t e = hipGetLastError();
+    if (e == hipSuccess && fault("launch"))
+        return fail(SSM_ERR_HIP, "%s: launch failure (injected by SSM_HIP_FAULT=launch)", what);
     return e == hipSuccess ? SSM_OK : from_hip(e, what);
 }
 
@@ -228,9 +248,8 @@ ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, co
 extern "C" ssm_status ssm_ctx_create(int device_ordinal, ssm_ctx** out) {
     if (!out) return ssm::fail(SSM_ERR_INVALID_ARG, "ssm_ctx_create: null out");
     *out = nullptr;
-    if (const char* f = std::getenv("SSM_HIP_FAULT"))
-        if (std::strcmp(f, "nodevice") == 0)
-            return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "no HIP device (SSM_HIP_FAULT=nodevice)");
+    if (ssm::fault("nodevice"))
+        return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "no HIP device (SSM_HIP_FAULT=nodevice)");
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n == 0)
@@ -271,7 +290,7 @@ extern "C" ssm_status ssm_ctx_create(int device_ordinal, ssm_ctx** out) {
     }
     // without hipBLASLt (or its workspace) every GEMM goes to rocBLAS
     if (hipblasLtCreate(&c->lt) != HIPBLAS_STATUS_SUCCESS) c->lt = nullptr;
-    if (c->lt && hipMalloc(&c->lt_ws, kLtWorkspace) != hipSuccess) {
+    if (c->lt && ssm::dev_malloc(&c->lt_ws, kLtWorkspace) != hipSuccess) {
         hipblasLtDestroy(c->lt);
         c->lt = nullptr;
         c->lt_ws = nullptr;
@@ -369,7 +388,7 @@ extern "C" ssm_status ssm_malloc(ssm_ctx* c, size_t bytes, void** dptr) {
     CtxLock lk;
     SSM_TRY(ctx_enter(c, lk));
     SSM_REQUIRE(dptr, "ssm_malloc: null out");
-    SSM_HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
+    SSM_HIP_TRY(ssm::dev_malloc(dptr, bytes ? bytes : 1));
     return SSM_OK;
 }
 extern "C" ssm_status ssm_free(ssm_ctx* c, void* p) {
@@ -634,7 +653,7 @@ ssm_status ensure_ws(ssm_model* m, int B, int L, bool full_logits, Ws* w) {
         if (m->ws) SSM_HIP_TRY(hipFree(m->ws));
         m->ws = nullptr;
         m->ws_bytes = 0;
-        SSM_HIP_TRY(hipMalloc((void**)&m->ws, need));
+        SSM_HIP_TRY(ssm::dev_malloc((void**)&m->ws, need));
         m->ws_bytes = need;
     }
     plan_ws(m, B, L, full_logits, w);
@@ -646,7 +665,7 @@ ssm_status ensure_ids(ssm_model* m, size_t n) {
         SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
         if (m->d_ids) SSM_HIP_TRY(hipFree(m->d_ids));
         m->d_ids = nullptr;
-        SSM_HIP_TRY(hipMalloc((void**)&m->d_ids, n * sizeof(uint32_t)));
+        SSM_HIP_TRY(ssm::dev_malloc((void**)&m->d_ids, n * sizeof(uint32_t)));
         m->ids_cap = n;
     }
     return SSM_OK;
@@ -727,7 +746,7 @@ ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const flo
             if (m->rg) SSM_HIP_TRY(hipFree(m->rg));
             m->rg = nullptr;
             m->rg_bytes = 0;
-            SSM_HIP_TRY(hipMalloc((void**)&m->rg, need));
+            SSM_HIP_TRY(ssm::dev_malloc((void**)&m->rg, need));
             m->rg_bytes = need;
         }
         return ssm::launch_rowgemm(mode, x, ldx, z, ldz, g, W, y, ldy, M, N, K, beta, d.eps,
@@ -900,9 +919,9 @@ extern "C" ssm_status ssm_model_create(ssm_ctx* ctx, const ssm_config* cfg, uint
     if (s != SSM_OK) { delete m; return s; }
     build_layout(m);
     hipError_t e;
-    if ((e = hipMalloc((void**)&m->w, m->nfloats * sizeof(float))) != hipSuccess ||
-        (e = hipMalloc((void**)&m->Ab, (m->nA ? m->nA : 1) * sizeof(float))) != hipSuccess ||
-        (e = hipMalloc((void**)&m->d_flag, sizeof(int))) != hipSuccess ||
+    if ((e = ssm::dev_malloc((void**)&m->w, m->nfloats * sizeof(float))) != hipSuccess ||
+        (e = ssm::dev_malloc((void**)&m->Ab, (m->nA ? m->nA : 1) * sizeof(float))) != hipSuccess ||
+        (e = ssm::dev_malloc((void**)&m->d_flag, sizeof(int))) != hipSuccess ||
         (e = hipMemsetAsync(m->d_flag, 0, sizeof(int), ctx->stream)) != hipSuccess) {
         hipFree(m->w); hipFree(m->Ab); hipFree(m->d_flag);
         delete m;
@@ -1135,9 +1154,9 @@ extern "C" ssm_status ssm_state_create(ssm_model* m, int B, ssm_state** out) {
     s->floats = 0;
     for (size_t i = 0; i < s->ssm_n.size(); ++i) s->floats += s->ssm_n[i] + s->conv_n[i];
     hipError_t e;
-    if ((e = hipMalloc((void**)&s->buf, (total ? total : 1) * 4)) != hipSuccess ||
-        (e = hipMalloc((void**)&s->d_tok, (size_t)B * 4)) != hipSuccess ||
-        (e = hipMalloc((void**)&s->d_logits, (size_t)B * d.V * 4)) != hipSuccess) {
+    if ((e = ssm::dev_malloc((void**)&s->buf, (total ? total : 1) * 4)) != hipSuccess ||
+        (e = ssm::dev_malloc((void**)&s->d_tok, (size_t)B * 4)) != hipSuccess ||
+        (e = ssm::dev_malloc((void**)&s->d_logits, (size_t)B * d.V * 4)) != hipSuccess) {
         hipFree(s->buf); hipFree(s->d_tok); hipFree(s->d_logits);
         delete s;
         return ssm::from_hip(e, "ssm_state_create");
@@ -1262,7 +1281,7 @@ ssm_status ensure_gen(ssm_state* s, size_t n) {
         SSM_HIP_TRY(hipStreamSynchronize(s->m->ctx->stream));
         if (s->d_gen) SSM_HIP_TRY(hipFree(s->d_gen));
         s->d_gen = nullptr;
-        SSM_HIP_TRY(hipMalloc((void**)&s->d_gen, n * 4));
+        SSM_HIP_TRY(ssm::dev_malloc((void**)&s->d_gen, n * 4));
         s->gen_cap = n;
     }
     return SSM_OK;
@@ -1417,7 +1436,7 @@ extern "C" ssm_status ssm_generate_greedy(ssm_model* m, ssm_state* s, const uint
     SSM_TRY(prefill_device(m, s, m->d_ids, Lp, s->d_gen));
     // steps alternate between two id buffers (so they replay two captured graphs); each
     // step's argmax is then copied into the generation ring
-    if (n_new > 1 && !s->d_ping) SSM_HIP_TRY(hipMalloc((void**)&s->d_ping, (size_t)2 * B * 4));
+    if (n_new > 1 && !s->d_ping) SSM_HIP_TRY(ssm::dev_malloc((void**)&s->d_ping, (size_t)2 * B * 4));
     if (n_new > 1)
         SSM_HIP_TRY(hipMemcpyAsync(s->d_ping, s->d_gen, (size_t)B * 4, hipMemcpyDeviceToDevice, st));
     for (int k = 1; k < n_new; ++k) {
@@ -1456,10 +1475,10 @@ extern "C" ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint
         SSM_HIP_TRY(hipStreamSynchronize(st));
         if (s->d_u) SSM_HIP_TRY(hipFree(s->d_u));
         s->d_u = nullptr;
-        SSM_HIP_TRY(hipMalloc((void**)&s->d_u, nu * sizeof(double)));
+        SSM_HIP_TRY(ssm::dev_malloc((void**)&s->d_u, nu * sizeof(double)));
         s->u_cap = nu;
     }
-    if (!s->d_sws) SSM_HIP_TRY(hipMalloc(&s->d_sws, ssm::sample_workspace(B, V)));
+    if (!s->d_sws) SSM_HIP_TRY(ssm::dev_malloc(&s->d_sws, ssm::sample_workspace(B, V)));
     SSM_HIP_TRY(hipMemcpyAsync(s->d_u, u_host, nu * sizeof(double), hipMemcpyHostToDevice, st));
     SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, prompt, T * 4, hipMemcpyHostToDevice, st));
     SSM_TRY(prefill_device(m, s, m->d_ids, Lp, nullptr));
@@ -1468,7 +1487,7 @@ extern "C" ssm_status ssm_generate_sample(ssm_model* m, ssm_state* s, const uint
     // as in greedy generation, steps alternate between two id buffers so that they replay
     // two captured graphs; the sampler runs after each step, outside the graph (its draws
     // change every step)
-    if (n_new > 1 && !s->d_ping) SSM_HIP_TRY(hipMalloc((void**)&s->d_ping, (size_t)2 * B * 4));
+    if (n_new > 1 && !s->d_ping) SSM_HIP_TRY(ssm::dev_malloc((void**)&s->d_ping, (size_t)2 * B * 4));
     if (n_new > 1)
         SSM_HIP_TRY(hipMemcpyAsync(s->d_ping, s->d_gen, (size_t)B * 4, hipMemcpyDeviceToDevice, st));
     for (int k = 1; k < n_new; ++k) {
