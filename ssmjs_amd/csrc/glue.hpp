@@ -41,4 +41,51 @@ ssm_status launch_rowgemm(int mode, const float* X, long ldx, const float* Z, lo
                           float beta, float eps, void* workspace, size_t workspace_bytes,
                           hipStream_t st, const float* g2 = nullptr, float* nout = nullptr,
                           long ldn = 0, bool* normed = nullptr);
+
+// One-token step projections (stepproj.hip): v = s[m] * X W^T on 16 x 16 tiles with an
+// epilogue; s[m] = 1 / sqrt(sum_j ssq[m * nssq + j] * inv_div + eps) when ssq is given.
+// X (M rows, padded to whole 16-row tiles) and W (N rows, likewise) are in fragment order.
+constexpr int kStepProjMaxRows = 64;
+constexpr int kStepProjMaxSsq = 256;
+
+// Fragment order of a (rows, K) matrix, K % 16 == 0, KB = K / 16: the 16-row tile t and
+// k-block kb form 256 contiguous floats at (t * KB + kb) * 256, lane-major: lane 16 q + i
+// holds row 16 t + i, k = 16 kb + 4 q .. 4 q + 3 (one MFMA operand fragment per b128 load).
+__host__ __device__ inline long frag_off(int m, int k, int KB) {
+    return ((long)(m >> 4) * KB + (k >> 4)) * 256 + (((k >> 2) & 3) * 16 + (m & 15)) * 4 + (k & 3);
+}
+size_t frag_floats(int rows, int K);
+
+enum { EPI_STORE = 0, EPI_CONV = 1, EPI_RESID = 2 };
+struct StepProj {
+    const float* X = nullptr;              // (M, K) fragment order
+    const float* W = nullptr;              // (N, K) fragment order (launch_pack_frag)
+    int M = 0, N = 0, K = 0;
+    const float* ssq = nullptr; int nssq = 0; float inv_div = 0.f, eps = 0.f;
+    float* Y = nullptr; long ldy = 0; float beta = 0.f;
+    // EPI_CONV: columns [c0, c0 + C) -> conv update (weights (C, Kc), bias, state (M, C, Kc-1))
+    int c0 = 0, C = 0, Kc = 0;
+    const float* cw = nullptr; const float* cb = nullptr; float* cst = nullptr;
+    float* Yc = nullptr; long ldyc = 0;
+    // EPI_RESID with g2: xg = Y * g2 in fragment order (K = N), ssq_out (M, N / 16)
+    const float* g2 = nullptr; float* xg = nullptr; float* ssq_out = nullptr;
+    int mt = 0, nt = 0, rotate = 0;        // tiles and k-start rotation (set by the launcher)
+};
+bool stepproj_ok(int M, int N, int K);
+ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st);
+// W (N, K) row stride ldw -> fragment order in out (frag_floats(N, K) floats).
+ssm_status launch_pack_frag(const float* W, long ldw, int N, int K, float* out, hipStream_t st);
+// xg = x * g in fragment order (K = d) and ssq (M, d / 16) partial sums of x^2: the first
+// RMSNorm of a step.
+ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,
+                         int d, hipStream_t st);
+// The Mamba-2 one-token state update with the gated RMSNorm's element-wise part:
+// y = (C.h + D x) * silu(z) * gn in fragment order (K = H P), and per workgroup the partial sum
+// of ((C.h + D x) silu(z))^2 into ssq (B, m2_gated_nssq(H, P, N)). ssd.hip.
+int m2_gated_nssq(int H, int P, int N);
+ssm_status launch_m2_update_gated(const float* x, long ldx, const float* dt, long lddt,
+                                  const float* dt_bias, const float* A, const float* Bm, long ldb,
+                                  const float* Cm, long ldc, const float* Dsk, const float* z,
+                                  long ldz, const float* gn, float* y, float* ssq, float* h, int B,
+                                  int H, int Pd, int G, int N, hipStream_t st);
 }  // namespace ssm

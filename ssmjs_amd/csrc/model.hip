@@ -451,6 +451,11 @@ struct ssm_model {
     // few-row projection split-K workspace (partial products), grown on demand
     char* rg = nullptr;
     size_t rg_bytes = 0;
+    // in_proj / out_proj weights of the layers with a fused one-token step, in the step
+    // projection's fragment order (stepproj.hip); built at the first such step and rebuilt
+    // whenever the weights change
+    float* wp = nullptr;
+    std::vector<long> wp_in, wp_out;   // float offsets into wp per layer (-1: not packed)
     int* d_flag = nullptr;   // out-of-range token id flag
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
@@ -546,13 +551,16 @@ void build_layout(ssm_model* m) {
     m->nA = (size_t)aoff;
 }
 
+ssm_status pack_weights(ssm_model* m);
+
+// Everything derived from the weights: A = -exp(A_log) and, once built, the packed copies.
 ssm_status refresh_A(ssm_model* m) {
     hipStream_t st = m->ctx->stream;
     for (const LayerW& L : m->layers) {
         const long n = L.type == SSM_LAYER_MAMBA1 ? (long)m->dm.D * m->dm.N : m->dm.H;
         SSM_TRY(ssm::launch_neg_exp(m->w + L.A_log, m->Ab + L.A, n, st));
     }
-    return SSM_OK;
+    return m->wp ? pack_weights(m) : SSM_OK;
 }
 
 ssm_status random_init(ssm_model* m, uint64_t seed) {
@@ -595,6 +603,10 @@ ssm_status random_init(ssm_model* m, uint64_t seed) {
 // Workspace plan for T = B*L tokens (bytes, 256-aligned carve-outs).
 struct Ws {
     float *hid, *nrm, *a, *b, *c, *d, *e, *last, *logits;
+    // one-token steps (stepproj.hip): x * g of the next RMSNorm and the gated norm's output,
+    // both in fragment order, and the two norms' partial sums of squares; null for longer
+    // sequences
+    float *xg, *yf, *ssq_in, *ssq_y;
     void* scan;
     size_t scan_bytes;
 };
@@ -634,6 +646,12 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
     size_t o_last = off; off += al(4 * (size_t)B * d.d);
     size_t o_log = off; off += al(4 * nlog);
     size_t o_scan = off; off += al(scan);
+    const size_t nstep = L == 1 ? (size_t)B : 0;
+    const size_t nstep16 = (nstep + 15) / 16 * 16;   // fragment order pads to 16-row tiles
+    size_t o_xg = off; off += al(4 * nstep16 * d.d);
+    size_t o_yf = off; off += al(4 * nstep16 * (has2 ? d.D : 0));
+    size_t o_sqi = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
+    size_t o_sqy = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
     if (out) {
         char* base = m->ws;
         out->hid = (float*)(base + o_hid); out->nrm = (float*)(base + o_nrm);
@@ -642,6 +660,10 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
         out->e = (float*)(base + o_e); out->last = (float*)(base + o_last);
         out->logits = (float*)(base + o_log);
         out->scan = base + o_scan; out->scan_bytes = scan;
+        out->xg = nstep ? (float*)(base + o_xg) : nullptr;
+        out->yf = nstep && has2 ? (float*)(base + o_yf) : nullptr;
+        out->ssq_in = nstep ? (float*)(base + o_sqi) : nullptr;
+        out->ssq_y = nstep ? (float*)(base + o_sqy) : nullptr;
     }
     return off;
 }
@@ -827,6 +849,91 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* 
     return SSM_OK;
 }
 
+// Whether a layer can take the fused one-token step: a Mamba-2 layer with one group whose
+// projections fit the step kernel (stepproj.hip) and whose state update has a gated variant.
+bool fusable(const ssm_model* m, const LayerW& Ly) {
+    const Dims& d = m->dm;
+    if (Ly.type != SSM_LAYER_MAMBA2 || d.G != 1) return false;
+    if (!(d.N == 64 || d.N == 128 || d.N == 256) || d.K > 8) return false;
+    if (d.d % 16 != 0 || d.d / 16 > ssm::kStepProjMaxSsq) return false;
+    if (ssm::m2_gated_nssq(d.H, d.P, d.N) > ssm::kStepProjMaxSsq) return false;
+    if (d.D % 16 != 0 || d.cd % 4 != 0) return false;   // whole k-blocks; 16-byte B, C rows
+    return ssm::stepproj_ok(1, d.nin, d.d) && ssm::stepproj_ok(1, d.d, d.D);
+}
+
+bool fused_step_ok(const ssm_model* m, const LayerW& Ly, int B, const Ws& w) {
+    return B >= 1 && B <= ssm::kStepProjMaxRows && w.xg && w.yf && fusable(m, Ly);
+}
+
+// (Re)builds the fragment-order copies of the fusable layers' in_proj and out_proj.
+ssm_status pack_weights(ssm_model* m) {
+    const Dims& d = m->dm;
+    hipStream_t st = m->ctx->stream;
+    if (!m->wp) {
+        long off = 0;
+        m->wp_in.assign(d.nl, -1);
+        m->wp_out.assign(d.nl, -1);
+        for (int l = 0; l < d.nl; ++l) {
+            if (!fusable(m, m->layers[l])) continue;
+            m->wp_in[l] = off; off += (long)ssm::frag_floats(d.nin, d.d);
+            m->wp_out[l] = off; off += (long)ssm::frag_floats(d.d, d.D);
+        }
+        if (off == 0) return SSM_OK;
+        SSM_HIP_TRY(ssm::dev_malloc((void**)&m->wp, (size_t)off * sizeof(float)));
+    }
+    for (int l = 0; l < d.nl; ++l) {
+        if (m->wp_in[l] < 0) continue;
+        const LayerW& Ly = m->layers[l];
+        SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, d.nin, d.d, m->wp + m->wp_in[l], st));
+        SSM_TRY(ssm::launch_pack_frag(m->w + Ly.out_proj, d.D, d.d, d.D, m->wp + m->wp_out[l],
+                                      st));
+    }
+    return SSM_OK;
+}
+
+// The fused one-token Mamba-2 layer step, three launches:
+//   in_proj  (row scale 1/rms from w.ssq_in on w.xg = hid * norm) with the conv update of the
+//            xBC columns in its epilogue: zx (z, dt) and xbc;
+//   state update with the gated norm's element-wise part: w.yf = (C.h + D x) silu(z) gnorm
+//            and the partial sums of ((C.h + D x) silu(z))^2 in w.ssq_y;
+//   out_proj (row scale from w.ssq_y) with the residual add into hid, and, given g_next, the
+//            next RMSNorm's operand hid * g_next in w.xg and its partial sums in w.ssq_in.
+// Same arithmetic as mixer_step up to the order of the norms' sums and where each norm's
+// scale is applied (the row scale multiplies the projected row).
+ssm_status mixer_step_fused(ssm_model* m, int l, float* hid, int B, float* ssm_st,
+                            float* conv_st, const Ws& w, const float* g_next) {
+    const Dims& d = m->dm;
+    const LayerW& Ly = m->layers[l];
+    ssm_ctx* c = m->ctx;
+    hipStream_t st = c->stream;
+    const float* W = m->w;
+    const float* A = m->Ab + Ly.A;
+    float *zx = w.a, *xbc = w.b;
+    const int GN = d.G * d.N;
+    { Stage g(c, "m2.step.in_proj");
+      ssm::StepProj p;
+      p.X = w.xg; p.W = m->wp + m->wp_in[l]; p.M = B; p.N = d.nin; p.K = d.d;
+      p.ssq = w.ssq_in; p.nssq = d.d / 16; p.inv_div = 1.f / (float)d.d; p.eps = d.eps;
+      p.Y = zx; p.ldy = d.nin;
+      p.c0 = d.D; p.C = d.cd; p.Kc = d.K; p.cw = W + Ly.conv_w; p.cb = W + Ly.conv_b;
+      p.cst = conv_st; p.Yc = xbc; p.ldyc = d.cd;
+      SSM_TRY(ssm::launch_stepproj(ssm::EPI_CONV, p, st)); }
+    { Stage g(c, "m2.step.state_update");
+      SSM_TRY(ssm::launch_m2_update_gated(xbc, d.cd, zx + d.D + d.cd, d.nin, W + Ly.dt_b, A,
+                                          xbc + d.D, d.cd, xbc + d.D + GN, d.cd, W + Ly.Dsk, zx,
+                                          d.nin, W + Ly.gnorm, w.yf, w.ssq_y, ssm_st, B, d.H,
+                                          d.P, d.G, d.N, st)); }
+    { Stage g(c, "m2.step.out_proj");
+      ssm::StepProj p;
+      p.X = w.yf; p.W = m->wp + m->wp_out[l]; p.M = B; p.N = d.d; p.K = d.D;
+      p.ssq = w.ssq_y; p.nssq = ssm::m2_gated_nssq(d.H, d.P, d.N);
+      p.inv_div = 1.f / (float)d.D; p.eps = d.eps;
+      p.Y = hid; p.ldy = d.d;
+      if (g_next) { p.g2 = g_next; p.xg = w.xg; p.ssq_out = w.ssq_in; }
+      SSM_TRY(ssm::launch_stepproj(ssm::EPI_RESID, p, st)); }
+    return SSM_OK;
+}
+
 // embeddings -> layers; then the final norm into w.nrm unless `final_norm` is false (the
 // one-token path, whose LM head applies it in its prologue: the result stays in w.hid).
 ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s, const Ws& w,
@@ -836,13 +943,28 @@ ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s
     const long T = (long)B * L;
     SSM_TRY(ssm::launch_embed(d_ids, m->w + m->emb, w.hid, T, d.d, d.V, m->d_flag, st));
     bool normed = false;   // w.nrm holds the next layer's normalised input (one-token path)
+    bool pre = false;      // w.xg / w.ssq_in hold the next layer's x * g and partial sums
     for (int l = 0; l < d.nl; ++l) {
         const LayerW& Ly = m->layers[l];
         float* ss = s ? s->ssm[l] : nullptr;
         float* cs = s ? s->conv[l] : nullptr;
         if (L == 1 && s) {
-            const float* g_next = l + 1 < d.nl ? m->w + m->layers[l + 1].norm : nullptr;
-            SSM_TRY(mixer_step(m, Ly, w.hid, B, ss, cs, w, normed, g_next, &normed));
+            const LayerW* nx = l + 1 < d.nl ? &m->layers[l + 1] : nullptr;
+            const bool next_fused = nx && fused_step_ok(m, *nx, B, w);
+            if (fused_step_ok(m, Ly, B, w)) {
+                if (!m->wp) SSM_TRY(pack_weights(m));   // eager: the first step never replays
+                if (!pre)
+                    SSM_TRY(ssm::launch_xg_ssq(w.hid, d.d, m->w + Ly.norm, w.xg, w.ssq_in, B, d.d,
+                                               st));
+                SSM_TRY(mixer_step_fused(m, l, w.hid, B, ss, cs, w,
+                                         next_fused ? m->w + nx->norm : nullptr));
+                pre = next_fused;
+                normed = false;
+            } else {
+                const float* g_next = nx && !next_fused ? m->w + nx->norm : nullptr;
+                SSM_TRY(mixer_step(m, Ly, w.hid, B, ss, cs, w, normed, g_next, &normed));
+                pre = false;
+            }
         } else {
             SSM_TRY(ssm_rmsnorm(w.hid, d.d, m->w + Ly.norm, w.nrm, d.d, (int)T, d.d, d.eps, st));
             SSM_TRY(mixer(m, Ly, w.nrm, w.hid, 1.f, B, L, ss, cs, w));
@@ -949,7 +1071,7 @@ extern "C" ssm_status ssm_model_destroy(ssm_model* m) {
         hipSetDevice(m->ctx->device);
         hipStreamSynchronize(m->ctx->stream);
         hipFree(m->w); hipFree(m->Ab); hipFree(m->ws); hipFree(m->d_flag); hipFree(m->d_ids);
-        hipFree(m->rg);
+        hipFree(m->rg); hipFree(m->wp);
     }
     m->destroyed = true;
     return SSM_OK;

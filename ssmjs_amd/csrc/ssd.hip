@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "glue.hpp"
 #include "ssd.hpp"
 
 namespace {
@@ -613,15 +614,23 @@ void plan(int B, int L, int H, int& nchunks, int& nseg, int& per) {
 // The state goes through non-temporal loads and stores: it is touched once per step and not
 // again before the other layers' states have streamed through the caches, and keeping it out
 // of L2 and the MALL measured 13% faster (22.8 against 26.1 us at 64 x 32 x 64 x 128).
-template <int LPR, int R>
+//
+// GATED: y = (C.h + D x) * silu(z) * gn (the gated RMSNorm's element-wise part), stored in
+// fragment order for the out_proj (frag_off, K = H * P), and the workgroup's sum of
+// ((C.h + D x) silu(z))^2 over its rows into ssq[blockIdx.x] (a row's partial sums are
+// contiguous: blockIdx.x = (b H + h) * blocks_per_head + block). z and gn are fetched with
+// the state, so that no load waits behind the reduction.
+template <int LPR, int R, bool GATED>
 __global__ __launch_bounds__(256) void m2_update_kernel(
     const float* __restrict__ x, long ldx, const float* __restrict__ dt, long lddt,
     const float* __restrict__ dt_bias, int softplus, float dt_min, float dt_max,
     const float* __restrict__ A, const float* __restrict__ Bm, long ldb,
     const float* __restrict__ Cm, long ldc, const float* __restrict__ Dsk,
-    const float* __restrict__ z, long ldz, float* __restrict__ y, long ldy,
+    const float* __restrict__ z, long ldz, const float* __restrict__ gn,
+    float* __restrict__ ssq, float* __restrict__ y, long ldy,
     float* __restrict__ hs, int H, int Pd, int G, int N, int blocks_per_head) {
     constexpr int RPP = 256 / LPR;
+    __shared__ float sq[GATED ? RPP * R : 1];
     const int tid = threadIdx.x;
     const int c4 = tid % LPR;            // float4 column
     const int rsub = tid / LPR;
@@ -631,7 +640,7 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
     float* hb = hs + (long)bh * Pd * N;
 
     float4 v[R];
-    float xp[R];
+    float xp[R], zg[R], gg[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
         const int p = p0 + k * RPP;
@@ -640,6 +649,10 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
             v[k] = make_float4(__builtin_nontemporal_load(src), __builtin_nontemporal_load(src + 1),
                                __builtin_nontemporal_load(src + 2), __builtin_nontemporal_load(src + 3));
             xp[k] = x[(long)b * ldx + (long)h * Pd + p];
+            if (GATED) {
+                zg[k] = z[(long)b * ldz + (long)h * Pd + p];
+                gg[k] = gn[(long)h * Pd + p];
+            }
         }
     }
     const float4 bv = *reinterpret_cast<const float4*>(Bm + (long)b * ldb + (long)g * N + 4 * c4);
@@ -652,7 +665,10 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
 #pragma unroll
     for (int k = 0; k < R; ++k) {
         const int p = p0 + k * RPP;
-        if (p >= Pd) break;
+        if (p >= Pd) {
+            if (GATED && c4 == 0) sq[k * RPP + rsub] = 0.f;
+            continue;
+        }
         const float dx = dl * xp[k];
         float4 u = v[k];
         u.x = fmaf(dA, u.x, dx * bv.x);
@@ -669,8 +685,25 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
         for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
         if (c4 == 0) {
             acc = fmaf(Dh, xp[k], acc);
-            if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
-            y[(long)b * ldy + (long)h * Pd + p] = acc;
+            if (GATED) {
+                acc *= ssm::silu(zg[k]);
+                sq[k * RPP + rsub] = acc * acc;
+                y[ssm::frag_off(b, h * Pd + p, H * Pd / 16)] = acc * gg[k];
+            } else {
+                if (z) acc *= ssm::silu(z[(long)b * ldz + (long)h * Pd + p]);
+                y[(long)b * ldy + (long)h * Pd + p] = acc;
+            }
+        }
+    }
+    if constexpr (GATED) {
+        // the workgroup's row sums, added by the first wave's lanes in a fixed butterfly
+        static_assert(RPP * R <= 64, "one value per lane");
+        __syncthreads();
+        if (tid < 64) {
+            float t = tid < RPP * R ? sq[tid] : 0.f;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
+            if (tid == 0) ssq[blockIdx.x] = t;
         }
     }
 }
@@ -997,9 +1030,10 @@ extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float*
     const int bph = (int)ssm::cdiv(Pd, rpp * R);
     const unsigned grid = (unsigned)((long)B * H * bph);
 #define M2U(LPR)                                                                             \
-    m2_update_kernel<LPR, R><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus, dt_min, \
-                                                   dt_max, A, Bm, ldb, Cm, ldc, Dsk, z, ldz, y, \
-                                                   ldy, h, H, Pd, G, N, bph)
+    m2_update_kernel<LPR, R, false><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus,  \
+                                                          dt_min, dt_max, A, Bm, ldb, Cm, ldc,    \
+                                                          Dsk, z, ldz, nullptr, nullptr, y, ldy,  \
+                                                          h, H, Pd, G, N, bph)
     switch (lpr) {
         case 2: M2U(2); break;
         case 4: M2U(4); break;
@@ -1011,3 +1045,44 @@ extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float*
 #undef M2U
     return ssm::check_launch("m2_state_update");
 }
+
+namespace ssm {
+
+// Two state rows per thread, as in ssm_m2_state_update: P / (2 * 256 / (N / 4)) workgroups
+// per (b, h), each one partial sum.
+int m2_gated_nssq(int H, int P, int N) {
+    const int rpp = 256 / (N / 4);
+    return H * (int)cdiv(P, rpp * 2);
+}
+
+ssm_status launch_m2_update_gated(const float* x, long ldx, const float* dt, long lddt,
+                                  const float* dt_bias, const float* A, const float* Bm, long ldb,
+                                  const float* Cm, long ldc, const float* Dsk, const float* z,
+                                  long ldz, const float* gn, float* y, float* ssq, float* h,
+                                  int B, int H, int Pd, int G, int N, hipStream_t st) {
+    SSM_REQUIRE(x && dt && A && Bm && Cm && z && gn && y && ssq && h, "m2_update_gated: null");
+    SSM_REQUIRE((H * Pd) % 16 == 0, "m2_update_gated: d_inner %d not a multiple of 16", H * Pd);
+    SSM_REQUIRE(N == 64 || N == 128 || N == 256, "m2_update_gated: d_state %d", N);
+    SSM_REQUIRE(ldb % 4 == 0 && ldc % 4 == 0 && (uintptr_t)Bm % 16 == 0 &&
+                    (uintptr_t)Cm % 16 == 0 && (uintptr_t)h % 16 == 0,
+                "m2_update_gated: B/C/state must be 16-byte aligned");
+    if (B == 0) return SSM_OK;
+    constexpr int R = 2;
+    const int lpr = N / 4, rpp = 256 / lpr;
+    const int bph = (int)cdiv(Pd, rpp * R);
+    const unsigned grid = (unsigned)((long)B * H * bph);
+#define M2G(LPR)                                                                            \
+    m2_update_kernel<LPR, R, true><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, 1, 0.f,  \
+                                                         INFINITY, A, Bm, ldb, Cm, ldc, Dsk, \
+                                                         z, ldz, gn, ssq, y, 0, h, H, Pd,    \
+                                                         G, N, bph)
+    switch (lpr) {
+        case 16: M2G(16); break;
+        case 32: M2G(32); break;
+        default: M2G(64); break;
+    }
+#undef M2G
+    return check_launch("m2_update_gated");
+}
+
+}  // namespace ssm

@@ -10,8 +10,10 @@ through the C ABI, against the CPU oracle on the same seeded inputs and weights.
   cfg4  the recurrent decode step of a Mamba-2 model with cfg4's layer and vocabulary
         dimensions (d_model 1024, 32 heads x 64, d_state 128, vocab 32000) for 64 cached
         sequences (state ~ N(0, 0.1)), two layers so the oracle stays fast: the
-        model.generate path (src/session/session.ts:421-425), hipBLASLt in_proj at 64 rows,
-        the few-row gated out_proj, the LM head and the device argmax. Eager launches and
+        model.generate path (src/session/session.ts:421-425) through the fused layer step
+        (in_proj with the RMSNorm scale and the conv update in its epilogue, the state update
+        with the gated norm's element-wise part, out_proj with the residual add and the next
+        layer's norm operand), the LM head and the device argmax. Eager launches and
         graph-replayed steps are both checked.
 
 Tolerance, per element (north_star: max rel err <= 1e-4 fp32):
