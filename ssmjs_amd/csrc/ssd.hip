@@ -620,7 +620,11 @@ void plan(int B, int L, int H, int& nchunks, int& nseg, int& per) {
 // ((C.h + D x) silu(z))^2 over its rows into ssq[blockIdx.x] (a row's partial sums are
 // contiguous: blockIdx.x = (b H + h) * blocks_per_head + block). z and gn are fetched with
 // the state, so that no load waits behind the reduction.
-template <int LPR, int R, bool GATED>
+//
+// FULL: Pd is a whole number of workgroup row blocks (RPP * R), so no row needs a bound check;
+// with the checks, each guarded load sat behind its own branch and the compiler waited for
+// it before issuing the next, serialising the state loads.
+template <int LPR, int R, bool GATED, bool FULL>
 __global__ __launch_bounds__(256) void m2_update_kernel(
     const float* __restrict__ x, long ldx, const float* __restrict__ dt, long lddt,
     const float* __restrict__ dt_bias, int softplus, float dt_min, float dt_max,
@@ -644,7 +648,7 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
 #pragma unroll
     for (int k = 0; k < R; ++k) {
         const int p = p0 + k * RPP;
-        if (p < Pd) {
+        if (FULL || p < Pd) {
             const float* src = hb + (long)p * N + 4 * c4;
             v[k] = make_float4(__builtin_nontemporal_load(src), __builtin_nontemporal_load(src + 1),
                                __builtin_nontemporal_load(src + 2), __builtin_nontemporal_load(src + 3));
@@ -665,7 +669,7 @@ __global__ __launch_bounds__(256) void m2_update_kernel(
 #pragma unroll
     for (int k = 0; k < R; ++k) {
         const int p = p0 + k * RPP;
-        if (p >= Pd) {
+        if (!FULL && p >= Pd) {
             if (GATED && c4 == 0) sq[k * RPP + rsub] = 0.f;
             continue;
         }
@@ -1029,11 +1033,14 @@ extern "C" ssm_status ssm_m2_state_update(const float* x, long ldx, const float*
     constexpr int R = 2;
     const int bph = (int)ssm::cdiv(Pd, rpp * R);
     const unsigned grid = (unsigned)((long)B * H * bph);
+    const bool full = Pd % (rpp * R) == 0;
 #define M2U(LPR)                                                                             \
-    m2_update_kernel<LPR, R, false><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus,  \
-                                                          dt_min, dt_max, A, Bm, ldb, Cm, ldc,    \
-                                                          Dsk, z, ldz, nullptr, nullptr, y, ldy,  \
-                                                          h, H, Pd, G, N, bph)
+    (full ? m2_update_kernel<LPR, R, false, true><<<grid, 256, 0, st>>>(                    \
+                x, ldx, dt, lddt, dt_bias, softplus, dt_min, dt_max, A, Bm, ldb, Cm, ldc, Dsk, \
+                z, ldz, nullptr, nullptr, y, ldy, h, H, Pd, G, N, bph)                       \
+          : m2_update_kernel<LPR, R, false, false><<<grid, 256, 0, st>>>(                   \
+                x, ldx, dt, lddt, dt_bias, softplus, dt_min, dt_max, A, Bm, ldb, Cm, ldc, Dsk, \
+                z, ldz, nullptr, nullptr, y, ldy, h, H, Pd, G, N, bph))
     switch (lpr) {
         case 2: M2U(2); break;
         case 4: M2U(4); break;
@@ -1071,11 +1078,14 @@ ssm_status launch_m2_update_gated(const float* x, long ldx, const float* dt, lon
     const int lpr = N / 4, rpp = 256 / lpr;
     const int bph = (int)cdiv(Pd, rpp * R);
     const unsigned grid = (unsigned)((long)B * H * bph);
+    const bool full = Pd % (rpp * R) == 0;
 #define M2G(LPR)                                                                            \
-    m2_update_kernel<LPR, R, true><<<grid, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, 1, 0.f,  \
-                                                         INFINITY, A, Bm, ldb, Cm, ldc, Dsk, \
-                                                         z, ldz, gn, ssq, y, 0, h, H, Pd,    \
-                                                         G, N, bph)
+    (full ? m2_update_kernel<LPR, R, true, true><<<grid, 256, 0, st>>>(                    \
+                x, ldx, dt, lddt, dt_bias, 1, 0.f, INFINITY, A, Bm, ldb, Cm, ldc, Dsk, z,    \
+                ldz, gn, ssq, y, 0, h, H, Pd, G, N, bph)                                    \
+          : m2_update_kernel<LPR, R, true, false><<<grid, 256, 0, st>>>(                   \
+                x, ldx, dt, lddt, dt_bias, 1, 0.f, INFINITY, A, Bm, ldb, Cm, ldc, Dsk, z,    \
+                ldz, gn, ssq, y, 0, h, H, Pd, G, N, bph))
     switch (lpr) {
         case 16: M2G(16); break;
         case 32: M2G(32); break;

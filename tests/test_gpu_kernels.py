@@ -387,10 +387,13 @@ def test_ssd_chunk_equals_decode_steps():
     assert err(host(hs), host(hd)) <= F32_TOL
 
 
-def test_m2_state_update():
-    case("m2_state_update")
+@pytest.mark.parametrize("P", [64, 40])
+def test_m2_state_update(P):
+    """P = 64 fills whole workgroups of state rows (the unguarded kernel); P = 40 leaves a
+    partial block (the guarded one)."""
+    case(f"m2_state_update P={P}")
     r = rng(13)
-    B, H, P, G, N = 3, 8, 64, 2, 128
+    B, H, G, N = 3, 8, 2, 128
     h0 = r.standard_normal((B, H, P, N)).astype(np.float32)
     x, z = r.standard_normal((B, H, P)).astype(np.float32), r.standard_normal((B, H, P)).astype(np.float32)
     dt = r.standard_normal((B, H)).astype(np.float32)

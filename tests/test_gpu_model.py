@@ -87,10 +87,14 @@ def test_forward_matches_oracle(device, layers, N, H):
     m.destroy()
 
 
-@pytest.mark.parametrize("layers,N", [(["mamba1", "mamba1"], 16), (["mamba2", "mamba2"], 128)])
-def test_prefill_decode_state_matches_oracle(device, layers, N):
-    case(f"prefill/decode state {layers}")
-    m, blob = _model(device, layers, N=N)
+@pytest.mark.parametrize("layers,N,H", [(["mamba1", "mamba1"], 16, 4),
+                                        (["mamba2", "mamba2"], 128, 4),
+                                        (["mamba2", "mamba2"], 128, 32)])
+def test_prefill_decode_state_matches_oracle(device, layers, N, H):
+    """H = 32 gives head dim 8, less than one workgroup's block of state rows in the one-token
+    update (the guarded variant of the fused step's state update)."""
+    case(f"prefill/decode state {layers} N={N} H={H}")
+    m, blob = _model(device, layers, N=N, H=H)
     om = O.Model(blob)
     ids = np.random.default_rng(2).integers(0, 512, (3, 40)).astype(np.uint32)
     st = m.new_state(3)
