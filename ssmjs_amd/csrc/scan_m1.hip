@@ -1,12 +1,18 @@
 // K2: Mamba-1 selective scan (Gu & Dao 2023, Algorithm 2) for gfx950, and its one-token
-// decode update.
+// decode update. Two designs, chosen by how many waves the channels alone give:
 //
-// Work split: one lane per channel d (64 adjacent channels per wave, so u/dt/z/y rows are
-// read and written as 256-byte runs) holding all N state entries in registers (N is a
-// template constant, so the state loop is straight-line code). B_t and C_t are the same for
-// every channel: their addresses are wave-uniform and the pointers are read-only restrict
-// parameters, so they are fetched with scalar loads into SGPRs. Time is cut into NC chunks
-// so that B*D/64*NC waves fill the chip:
+// Single pass (scan_single_kernel, when B * D * N / 64 waves give every SIMD one): lane
+// (c, n) holds state h[d, n] in a register and walks the whole sequence once; the inputs of
+// a 64- or 128-step block are staged in LDS by the workgroup, and the per-step outputs
+// y = C_t . h_t are reduced over the N lanes of a channel through LDS. One v_exp_f32 per
+// (t, d, n); no intermediate state leaves the CU. Its own description is below.
+//
+// Chunked (when the channels are too few, e.g. one sequence of 512 channels): one lane per
+// channel d (64 adjacent channels per wave, so u/dt/z/y rows are read and written as 256-byte
+// runs) holding all N state entries in registers (N is a template constant, so the state loop
+// is straight-line code). B_t and C_t are the same for every channel: their addresses are
+// wave-uniform and the pointers are read-only restrict parameters, so they are fetched with
+// scalar loads into SGPRs. Time is cut into NC chunks so that B*D/64*NC waves fill the chip:
 //   pass A  scan_chunk_state : each chunk from a zero state -> chunk-end state + sum(dt')
 //   pass B  scan_chunk_prefix: per (b,n,d) sequential combine over chunks -> state entering
 //                               each chunk (h_in[c] = exp(A*sum_dt[c-1]) h_in[c-1] + hend[c-1]),
@@ -14,6 +20,8 @@
 //   pass C  scan_chunk_output: re-run each chunk from its entering state, emit y with the D
 //                               skip and SiLU(z) gate.
 // exp(dt A) is exp2(dt * (A log2 e)) with A pre-scaled once per lane (one v_exp_f32 each).
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace {
@@ -243,6 +251,232 @@ void launch_all(const ScanArgs& a, hipStream_t st) {
                                                  a.T, a.NC, a.hc);
 }
 
+// ---------------------------------------------------------------- single-pass scan
+// When the channels alone give every SIMD a wave, the whole sequence is walked once and each
+// exp(dt A) is evaluated once (the chunked passes above evaluate it twice: a v_exp_f32 costs
+// about three FMAs on this chip and does not overlap them, so that second evaluation is the
+// larger part of their cost).
+//
+// Lane (c, n) of a wave holds the state h[d, n] of channel d = c0 + c in a register, with
+// 64 / N channels per wave and N lanes per channel; a workgroup of W waves covers CW adjacent
+// channels of one sequence b. The sequence goes by in blocks of TK = 64 or 128 steps:
+//   staging  the block's u, dt, z (TK x CW) and B_t, C_t rows (TK x N), loaded one block
+//            ahead into registers, go to LDS as dt' = softplus(dt + bias), dt' u, silu(z),
+//            D u, B and C;
+//   then, per sub-block of SB = N steps:
+//   scan     lane (c, n), each step: h = exp2(dt' A log2 e) h + dt' u B_t[n]; h goes to LDS;
+//   output   lane (c, t) of the same wave: y = (sum_n h_t[c, n] C_t[n] + D u) silu(z);
+//   and the block's outputs are stored by the workgroup as whole rows of CW channels.
+// The scan's inner step is one multiply, one v_exp_f32, one multiply and one FMA per (t, d, n)
+// and the output's one FMA; only the final state goes to memory. State entries n >= Nr have
+// A = 0 and B = C = 0 and stay exactly zero.
+template <int N>
+struct Scan1 {
+    static constexpr int W = (N == 4 || N == 64) ? 4 : 8;   // waves (LDS <= 110 KB)
+    static constexpr int CPW = 64 / N;     // channels per wave
+    static constexpr int CW = W * CPW;     // channels per workgroup
+    // steps per block: the block's loads are issued one block ahead, so a block's work must
+    // outlast a memory latency under load (a 64-step block at N = 16, about 1.2 us of
+    // arithmetic, measured latency-bound); 128 where the LDS (160 KB) holds it
+    static constexpr int TK = N >= 16 ? 128 : 64;
+    static constexpr int SB = N;           // steps per output sub-block (64 lanes = CPW x SB)
+    static constexpr int NT = 64 * W;      // threads
+    static constexpr int UE = TK * CW / NT;        // u/dt/z values per thread and block
+    static constexpr int BE = (TK * N + NT - 1) / NT;   // B (and C) values per thread and block
+    // Row paddings keep the LDS accesses free of bank conflicts (32 banks): [channel][step]
+    // rows are read as one float per lane for N = 16 (odd pitch) and as float4 otherwise.
+    static constexpr int PD = N == 16 ? TK + 1 : TK + 4;
+    static constexpr int PT = TK + 4;      // [n][step] rows (float4 reads)
+    static constexpr int PC = CW + 1;      // [step][channel] rows
+    static constexpr int RR = CW * N + 4;  // padded row of one step's states
+    struct Smem {
+        float dl[CW][PD], du[CW][PD];      // dt', dt' u
+        float bt[N][PT];                   // B_t[n]
+        float ct[TK][N + 4];               // C_t[n]
+        float gz[TK][PC], dx[TK][PC];      // silu(z), D u
+        float red[SB][RR];                 // h_t[c, n] of one sub-block
+        float ys[TK][PC];                  // outputs
+    };
+};
+
+// Value of lane j of this lane's 16-lane row (DPP row_newbcast); as an operand of a VALU
+// instruction the compiler folds it into that instruction.
+template <int J>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, true));
+}
+
+template <int N, bool EXACT>
+__global__ __launch_bounds__(64 * Scan1<N>::W) void scan_single_kernel(ScanArgs a) {
+    using S = Scan1<N>;
+    constexpr int CPW = S::CPW, CW = S::CW, TK = S::TK, SB = S::SB, NT = S::NT, UE = S::UE,
+                  BE = S::BE;
+    __shared__ __attribute__((aligned(16))) typename S::Smem sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int b = blockIdx.y, c0 = blockIdx.x * CW;
+    const int D = a.D, L = a.L, Nr = EXACT ? N : a.N;
+
+    // scan lane: channel cl of the workgroup, state n
+    const int cl = w * CPW + lane / N, n = lane % N;
+    const int d = c0 + cl;
+    const bool live = d < D && n < Nr;
+    const float A2 = live ? a.A[(long)d * Nr + n] * ssm::kLog2e : 0.f;
+    float h = (live && a.h0) ? a.h0[((long)b * D + d) * Nr + n] : 0.f;
+    // output lane: channel cl2 of the workgroup (of this wave), step ot of the sub-block
+    const int cl2 = w * CPW + lane / SB, ot = lane % SB;
+    // staging elements: channel sc (fixed per thread: NT is a multiple of CW), steps
+    // st0 + e * (NT / CW)
+    constexpr int SR = NT / CW;            // steps covered by one pass of the threads
+    const int sc = tid % CW, st0 = tid / CW, sd = c0 + sc;
+    const bool sdok = sd < D;
+    const float bias = (sdok && a.dt_bias) ? a.dt_bias[sd] : 0.f;
+    const float Dd = (sdok && a.Dsk) ? a.Dsk[sd] : 0.f;
+    const float spf = a.softplus ? 1.f : 0.f, gzf = a.z ? 1.f : 0.f;
+
+    // per-sequence descriptors: rows past L read zeros and take no stores
+    const long r0 = (long)b * L;
+    const auto ru = ssm::rsrc(a.u + r0 * a.ldu, (unsigned)(((long)(L - 1) * a.ldu + D) * 4));
+    const auto rd = ssm::rsrc(a.dt + r0 * a.lddt, (unsigned)(((long)(L - 1) * a.lddt + D) * 4));
+    const auto rz = ssm::rsrc(a.z ? a.z + r0 * a.ldz : a.u, a.z ? (unsigned)(((long)(L - 1) * a.ldz + D) * 4) : 0u);
+    const auto rb = ssm::rsrc(a.Bm + r0 * a.ldb, (unsigned)(((long)(L - 1) * a.ldb + Nr) * 4));
+    const auto rc = ssm::rsrc(a.Cm + r0 * a.ldc, (unsigned)(((long)(L - 1) * a.ldc + Nr) * 4));
+    const auto ry = ssm::rsrc(a.y + r0 * a.ldy, (unsigned)(((long)(L - 1) * a.ldy + D) * 4));
+
+    // Block k's values of this thread, loaded one block ahead. The offsets carry no select
+    // (a lane-dependent `cond ? offset : out-of-range` was split by the compiler into two
+    // branches, each with its own load, whose join waited for every load in flight): rows
+    // are clamped to L, which the descriptors read as zeros, and a channel past D or a state
+    // past Nr reads some in-range value that the staging never uses.
+    float uv[UE], dv[UE], zv[UE], bv[BE], cv[BE];
+    auto load = [&](int k) {
+#pragma unroll
+        for (int e = 0; e < UE; ++e) {
+            const unsigned t = (unsigned)min(k * TK + st0 + e * SR, L);
+            uv[e] = ssm::bload4(ru, (t * (unsigned)a.ldu + (unsigned)sd) * 4u);
+            dv[e] = ssm::bload4(rd, (t * (unsigned)a.lddt + (unsigned)sd) * 4u);
+            zv[e] = ssm::bload4(rz, (t * (unsigned)a.ldz + (unsigned)sd) * 4u);
+        }
+#pragma unroll
+        for (int j = 0; j < BE; ++j) {
+            const int i = (tid + NT * j) % (TK * N), nn = i % N;
+            const unsigned t = (unsigned)min(k * TK + i / N, L);
+            bv[j] = ssm::bload4(rb, (t * (unsigned)a.ldb + (unsigned)nn) * 4u);
+            cv[j] = ssm::bload4(rc, (t * (unsigned)a.ldc + (unsigned)nn) * 4u);
+        }
+    };
+
+    const int nblk = (L + TK - 1) / TK;
+    load(0);
+    for (int k = 0; k < nblk; ++k) {
+        // staging (no data-dependent branch: the flags blend arithmetically)
+#pragma unroll
+        for (int e = 0; e < UE; ++e) {
+            const int st = st0 + e * SR;
+            const float ok = (sdok && k * TK + st < L) ? 1.f : 0.f;   // past L: dt' = 0
+            const float raw = dv[e] + bias;
+            const float dl = ok * (spf * ssm::softplus_sel(raw) + (1.f - spf) * raw);
+            sm.dl[sc][st] = dl;
+            sm.du[sc][st] = dl * uv[e];
+            sm.gz[st][sc] = fmaf(gzf, ssm::silu_fast(zv[e]) - 1.f, 1.f);
+            sm.dx[st][sc] = Dd * uv[e];
+        }
+#pragma unroll
+        for (int j = 0; j < BE; ++j) {
+            // threads past the block's TK x N values repeat the first ones (the same value to
+            // the same place), so no thread branches around its write
+            const int i = (tid + NT * j) % (TK * N);
+            const float nm = (EXACT || i % N < Nr) ? 1.f : 0.f;
+            sm.bt[i % N][i / N] = nm * bv[j];
+            sm.ct[i / N][i % N] = nm * cv[j];
+        }
+        load(k + 1);   // the next block's loads have this whole block to arrive
+        __syncthreads();
+#pragma unroll 1
+        for (int s0 = 0; s0 < TK; s0 += SB) {
+            if constexpr (N == 16) {
+                // A channel's 16 lanes are one DPP row: lane (c, j) fetches dt' and dt' u of
+                // step s0 + j and step j broadcasts them across the row, inside the multiplies;
+                // B_t[n] of the 16 steps comes in four float4 reads.
+                const float dlr = sm.dl[cl][s0 + n], dur = sm.du[cl][s0 + n];
+                float bq[16];
+#pragma unroll
+                for (int q = 0; q < 16; q += 4) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(&sm.bt[n][s0 + q]);
+                    bq[q] = b4.x; bq[q + 1] = b4.y; bq[q + 2] = b4.z; bq[q + 3] = b4.w;
+                }
+#define SCAN_STEP(J)                                                                         \
+                h = fmaf(ssm::ex2(row_bcast<J>(dlr) * A2), h, row_bcast<J>(dur) * bq[J]);   \
+                sm.red[J][cl * N + n] = h;
+                SCAN_STEP(0) SCAN_STEP(1) SCAN_STEP(2) SCAN_STEP(3)
+                SCAN_STEP(4) SCAN_STEP(5) SCAN_STEP(6) SCAN_STEP(7)
+                SCAN_STEP(8) SCAN_STEP(9) SCAN_STEP(10) SCAN_STEP(11)
+                SCAN_STEP(12) SCAN_STEP(13) SCAN_STEP(14) SCAN_STEP(15)
+#undef SCAN_STEP
+            } else {
+                // four steps per LDS read
+#pragma unroll
+                for (int t4 = 0; t4 < SB; t4 += 4) {
+                    const float4 dl4 = *reinterpret_cast<const float4*>(&sm.dl[cl][s0 + t4]);
+                    const float4 du4 = *reinterpret_cast<const float4*>(&sm.du[cl][s0 + t4]);
+                    const float4 b4 = *reinterpret_cast<const float4*>(&sm.bt[n][s0 + t4]);
+                    h = fmaf(ssm::ex2(dl4.x * A2), h, du4.x * b4.x);
+                    sm.red[t4][cl * N + n] = h;
+                    h = fmaf(ssm::ex2(dl4.y * A2), h, du4.y * b4.y);
+                    sm.red[t4 + 1][cl * N + n] = h;
+                    h = fmaf(ssm::ex2(dl4.z * A2), h, du4.z * b4.z);
+                    sm.red[t4 + 2][cl * N + n] = h;
+                    h = fmaf(ssm::ex2(dl4.w * A2), h, du4.w * b4.w);
+                    sm.red[t4 + 3][cl * N + n] = h;
+                }
+            }
+            // output: the same wave's states, one (channel, step) per lane
+            float acc = sm.dx[s0 + ot][cl2];
+#pragma unroll
+            for (int q = 0; q < N; q += 4) {
+                const float4 r4 = *reinterpret_cast<const float4*>(&sm.red[ot][cl2 * N + q]);
+                const float4 c4 = *reinterpret_cast<const float4*>(&sm.ct[s0 + ot][q]);
+                acc = fmaf(r4.x, c4.x, acc);
+                acc = fmaf(r4.y, c4.y, acc);
+                acc = fmaf(r4.z, c4.z, acc);
+                acc = fmaf(r4.w, c4.w, acc);
+            }
+            sm.ys[s0 + ot][cl2] = acc * sm.gz[s0 + ot][cl2];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < UE; ++e) {
+            // rows past L fall outside the descriptor (dropped); so does a channel past D
+            const int st = st0 + e * SR;
+            const unsigned off = ((unsigned)(k * TK + st) * (unsigned)a.ldy + (unsigned)sd) * 4u;
+            ssm::bstore4(sm.ys[st][sc], ry, off | (sdok ? 0u : 0x80000000u));
+        }
+    }
+    if (live && a.hT) a.hT[((long)b * D + d) * Nr + n] = h;
+}
+
+template <int N, bool EXACT>
+void launch_single(const ScanArgs& a, hipStream_t st) {
+    using S = Scan1<N>;
+    dim3 grid((unsigned)ssm::cdiv(a.D, S::CW), (unsigned)a.B);
+    scan_single_kernel<N, EXACT><<<grid, S::NT, 0, st>>>(a);
+}
+
+// Whether the single pass has at least one wave per SIMD (256 CUs x 4).
+template <int N>
+bool single_ok_n(int B, int D) {
+    using S = Scan1<N>;
+    return (long)B * ssm::cdiv(D, S::CW) * S::W >= 1024;
+}
+bool single_ok(int B, int D, int Np) {
+    switch (Np) {
+        case 4: return single_ok_n<4>(B, D);
+        case 8: return single_ok_n<8>(B, D);
+        case 16: return single_ok_n<16>(B, D);
+        case 32: return single_ok_n<32>(B, D);
+        default: return single_ok_n<64>(B, D);
+    }
+}
+
 // One-token update: one thread per (b, d) with the N state entries in registers.
 template <int N>
 __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
@@ -325,8 +559,15 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
 
 }  // namespace
 
+namespace {
+int pad_n(int N) { return N <= 4 ? 4 : N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64; }
+// The single pass addresses a sequence's rows of every input through 32-bit offsets.
+bool single_fits(int L, int D, long ld) { return ((long)(L - 1) * ld + D) * 4 < (1L << 31); }
+}  // namespace
+
 extern "C" size_t ssm_selective_scan_workspace(int B, int L, int D, int N) {
     if (B <= 0 || L <= 0 || D <= 0 || N <= 0) return 0;
+    if (N <= 64 && single_ok(B, D, pad_n(N))) return 0;   // the single pass needs none
     const int T = pick_chunk(B, L, D);
     const long NC = ssm::cdiv(L, T);
     return sizeof(float) * (size_t)B * NC * D * ((size_t)N + 1);
@@ -355,8 +596,11 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
         }
         return SSM_OK;
     }
-    const size_t need = ssm_selective_scan_workspace(B, L, D, N);
-    SSM_REQUIRE(workspace && workspace_bytes >= need,
+    const int Np = pad_n(N);
+    const long ldmax = std::max({ldu, lddt, ldy, z ? ldz : 0L, ldb, ldc});
+    const bool single = single_ok(B, D, Np) && single_fits(L, D, ldmax);
+    const size_t need = single ? 0 : ssm_selective_scan_workspace(B, L, D, N);
+    SSM_REQUIRE(need == 0 || (workspace && workspace_bytes >= need),
                 "ssm_selective_scan: workspace of %zu bytes needed", need);
     ScanArgs a;
     a.u = u; a.ldu = ldu; a.dt = dt; a.lddt = lddt; a.dt_bias = dt_bias; a.softplus = softplus;
@@ -368,6 +612,17 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
     a.sdt = a.hc + (size_t)B * a.NC * N * D;
     a.h0 = h0; a.hT = hT;
     hipStream_t st = (hipStream_t)stream;
+    if (single) {
+        const bool exact = N == Np;
+        switch (Np) {
+            case 4: exact ? launch_single<4, true>(a, st) : launch_single<4, false>(a, st); break;
+            case 8: exact ? launch_single<8, true>(a, st) : launch_single<8, false>(a, st); break;
+            case 16: exact ? launch_single<16, true>(a, st) : launch_single<16, false>(a, st); break;
+            case 32: exact ? launch_single<32, true>(a, st) : launch_single<32, false>(a, st); break;
+            default: exact ? launch_single<64, true>(a, st) : launch_single<64, false>(a, st); break;
+        }
+        return ssm::check_launch("selective_scan");
+    }
     switch (N) {
         case 4: launch_all<4, true>(a, st); break;
         case 8: launch_all<8, true>(a, st); break;

@@ -84,12 +84,14 @@ def _mixer_vs_oracle(device, cfg, B, L, seed):
     return got, ref
 
 
-def test_cfg2_mamba1_block(device):
-    """cfg2's block dimensions, B = 2, L = 700 (the scan cuts time into many chunks)."""
-    case("cfg2 Mamba-1 block d768 D1536 N16 R48 K4, B=2 L=700")
+@pytest.mark.parametrize("B,L", [(2, 700), (4, 300)])
+def test_cfg2_mamba1_block(device, B, L):
+    """cfg2's block dimensions. B = 2, L = 700: the scan cuts time into many chunks (too few
+    channels for one wave per SIMD); B = 4 (cfg2's batch): the single-pass scan."""
+    case(f"cfg2 Mamba-1 block d768 D1536 N16 R48 K4, B={B} L={L}")
     cfg = {"vocabSize": 16, "dModel": 768, "numLayers": 1, "dState": 16, "dConv": 4,
            "expand": 2, "nHeads": 12, "dtRank": 48, "layers": [{"type": "mamba1"}]}
-    got, ref = _mixer_vs_oracle(device, cfg, 2, 700, 1002)
+    got, ref = _mixer_vs_oracle(device, cfg, B, L, 1002)
     check_close(got, ref, "block output")
 
 

@@ -154,6 +154,42 @@ def test_scan_shapes(B, L, D, N, h0):
     assert err(host(hd), hT) <= F32_TOL
 
 
+@pytest.mark.parametrize("B,L,D,N,h0,full", [
+    (4, 77, 1040, 16, True, True),     # partial channel tile, tail block of 13 steps
+    (4, 100, 1536, 16, False, True),   # cfg2's channels and state size
+    (8, 40, 1024, 8, True, True),
+    (2, 70, 1024, 32, True, False),    # no z, D, dt bias; raw dt
+    (1, 130, 1024, 64, True, True),
+    (16, 20, 1024, 4, False, True),
+    (4, 50, 1024, 12, True, True),     # state size between template sizes (masked lanes)
+])
+def test_scan_single_pass(B, L, D, N, h0, full):
+    """Shapes whose channels give every SIMD a wave take the single-pass scan (one walk over
+    the sequence, state in registers); these cover every template state size."""
+    case(f"selective_scan single pass B={B} L={L} D={D} N={N} h0={h0} full={full}")
+    r = rng(4000 + N + D)
+    u, z, Bm, Cm, dt, A = _scan_inputs(r, B, L, D, N)
+    Dk = r.standard_normal(D).astype(np.float32) if full else None
+    db = (0.1 * r.standard_normal(D)).astype(np.float32) if full else None
+    zz = z if full else None
+    if not full:
+        dt = np.abs(dt) * 0.3   # raw (already positive) dt when softplus is off
+    h0a = (0.3 * r.standard_normal((B, D, N))).astype(np.float32) if h0 else None
+    ref, hT = O.selective_scan(u, dt, A, Bm, Cm, Dk, zz, db, full, h0=h0a, return_state=True)
+    hd = torch.zeros(B, D, N, device="cuda")
+    assert _lib_scan_ws(B, L, D, N) == 0, "expected the single-pass path (no workspace)"
+    y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk) if full else None,
+                           dev(zz) if full else None, dev(db) if full else None, full,
+                           dev(h0a) if h0 else None, hd)
+    assert err(host(y), ref) <= F32_TOL
+    assert err(host(hd), hT) <= F32_TOL
+
+
+def _lib_scan_ws(B, L, D, N):
+    from ssmjs_amd import _lib
+    return _lib.lib().ssm_selective_scan_workspace(B, L, D, N)
+
+
 def test_scan_strided_views():
     """B, C and dt as column slices of one (B,L,R+2N) buffer, z as a slice of xz."""
     case("selective_scan strided")
