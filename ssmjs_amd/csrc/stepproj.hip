@@ -203,7 +203,8 @@ __global__ __launch_bounds__(256) void xg_ssq_kernel(const float* __restrict__ x
 }
 
 // W (N, K) row stride ldw -> fragment order, N padded with zero rows to whole 16-row tiles.
-// One thread per 16 bytes of the output.
+// One thread per 16 bytes of the output; W is read as scalars (a layer's weights start at any
+// float offset of the checkpoint buffer, and this runs once per weight change).
 __global__ __launch_bounds__(256) void pack_frag_kernel(const float* __restrict__ W, long ldw,
                                                         int N, int K, float* __restrict__ out) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;   // float4 index
@@ -215,7 +216,10 @@ __global__ __launch_bounds__(256) void pack_frag_kernel(const float* __restrict_
     const int kb = (int)(blk % KB), tn = (int)(blk / KB);
     const int n = tn * 16 + (lane & 15), k = kb * 16 + 4 * (lane >> 4);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (n < N) v = *reinterpret_cast<const float4*>(W + (long)n * ldw + k);
+    if (n < N) {
+        const float* r = W + (long)n * ldw + k;
+        v = make_float4(r[0], r[1], r[2], r[3]);
+    }
     reinterpret_cast<float4*>(out)[i] = v;
 }
 
@@ -239,8 +243,7 @@ bool stepproj_ok(int M, int N, int K) {
 size_t frag_floats(int rows, int K) { return (size_t)((rows + 15) / 16) * 16 * K; }
 
 ssm_status launch_pack_frag(const float* W, long ldw, int N, int K, float* out, hipStream_t st) {
-    SSM_REQUIRE(K % 16 == 0 && ldw % 4 == 0 && ((uintptr_t)W & 15) == 0 &&
-                    ((uintptr_t)out & 15) == 0,
+    SSM_REQUIRE(K % 16 == 0 && ldw >= K && ((uintptr_t)out & 15) == 0,
                 "pack_frag: K %d / ldw %ld / alignment", K, ldw);
     const long n4 = (long)frag_floats(N, K) / 4;
     if (n4 == 0) return SSM_OK;
