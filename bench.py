@@ -65,7 +65,8 @@ TRAFFIC = {
 # an entry goes stale when its kernel changes after that commit.
 TRAFFIC_MEASURED_AT = {k: "e7034fa" for k in TRAFFIC}
 TRAFFIC_MEASURED_AT.update({("cfg3", "f32"): "805df87", ("cfg3", "bf16"): "805df87",
-                            ("cfg5", "bf16"): "805df87"})
+                            ("cfg5", "bf16"): "805df87", ("cfg2", "m1.in_proj"): "7c96b77",
+                            ("cfg4", "m2.step.state_update"): "7c96b77"})
 
 
 def parse():
