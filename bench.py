@@ -226,6 +226,9 @@ def w_cfg2(torch, np, dev, args):
         "m1.conv": (None, 4.0 * (T * D * 2 + D * (K + 1))),
         "m1.x_proj": (2.0 * T * D * RN, 4.0 * (T * D + RN * D + T * RN)),
         "m1.dt_proj": (2.0 * T * R * D, 4.0 * (T * R + D * R + T * D)),
+        # x_proj and dt_proj in one kernel: xc in, dbl and dt out (dt_low stays on chip)
+        "m1.x_dt_proj": (2.0 * T * D * RN + 2.0 * T * R * D,
+                         4.0 * (T * D + RN * D + D * R + T * RN + T * D)),
         "m1.scan": (None, 4.0 * (T * D * 4 + T * 2 * N + D * (N + 2))),
         "m1.out_proj": (2.0 * T * D * d, 4.0 * (T * D + d * D + T * d)),
     }
@@ -424,6 +427,9 @@ def w_cfg3layer(torch, np, dev, args):
         "m2.conv": (None, 4.0 * (T * cd * 2 + cd * (K + 1))),
         "m2.ssd": (sf, sb),
         "m2.gated_norm": (None, 4.0 * (T * D * 3 + D)),
+        # the SSD with the gate applied in its epilogue: reads z too, writes u g and the
+        # per-head sums of u^2 (y's own bytes are in ssd_alg)
+        "m2.ssd_gate": (sf, sb + 4.0 * (T * D + D + T * H)),
         "m2.out_proj": (2.0 * T * D * d, 4.0 * (T * D + d * D + T * d)),
     }
     stages = {}
@@ -431,7 +437,7 @@ def w_cfg3layer(torch, np, dev, args):
         f, b = alg[kk]
         stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None)
     dom = max(stages.values(), key=lambda r: r["avg_ms"])
-    layer_flops = sum(f for f, _ in alg.values() if f)
+    layer_flops = sum(alg[kk][0] for kk in st if alg[kk][0])
     out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
            "dtype": "f32",
            "config": {"workload": "cfg3 layer: Mamba-2 layer prefill (in_proj, conv1d+SiLU over "

@@ -181,6 +181,28 @@ ssm_status ssm_linear_rows(int mode, const float* x, long ldx, const float* z, l
                            float beta, float eps, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Projection of any number of rows (the Linear layers of the MambaCode.js model behind
+ * model.forward at prefill, streaming.ts:31-35: the Mamba blocks' in_proj, x_proj, dt_proj
+ * and out_proj):
+ *   y[m,n] = beta*y[m,n] + sum_k x[m,k] W[n,k] (+ bias[n] when bias is not NULL)
+ * W (N,K) row-major with row stride ldw. fp32 arithmetic on the fp32 matrix cores; the sum
+ * over k is in a fixed order (results do not depend on scheduling). K % 4 == 0; x and W
+ * 16-byte aligned with ldx, ldw multiples of 4; 128 rows of any operand span < 2 GiB. */
+ssm_status ssm_linear(const float* x, long ldx, const float* W, long ldw, const float* bias,
+                      float* y, long ldy, int M, int N, int K, float beta, void* stream);
+
+/* The Mamba-1 block's x_proj and dt_proj in one pass over x (the conv output), for the
+ * Linear layers between the conv and the scan in MambaCode.js's Mamba-1 block behind
+ * model.forward (streaming.ts:31-35):
+ *   dbl[t, :] = x[t, :] Wx^T            (T, R + 2N): dt_low | B | C, row stride lddbl
+ *   dt[t, :]  = dbl[t, 0:R] Wdt^T        (T, D), row stride lddt (before bias and softplus)
+ * Wx (R + 2N, D) and Wdt (D, R) row-major. fp32 matrix cores, sums in a fixed order.
+ * Needs D % 4 == 0, R % 4 == 0, R <= 64, R + 2N <= 128; x, Wx, Wdt 16-byte aligned with
+ * ldx % 4 == 0 (SSM_ERR_INVALID_ARG otherwise). */
+ssm_status ssm_m1_xproj_dt(const float* x, long ldx, const float* Wx, const float* Wdt,
+                           float* dbl, long lddbl, float* dt, long lddt, int T, int D, int R,
+                           int N, void* stream);
+
 /* Greedy pick per row (sampleToken with topK = 1, src/session/streaming.ts:74-75): index
  * of the largest value, lowest index among equal maxima; NaN never wins (0 for an all-NaN
  * row). x (rows, n) with row stride ldx; out (rows) uint32. */

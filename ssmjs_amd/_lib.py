@@ -105,6 +105,8 @@ PROTOTYPES = {
     "ssm_linear_rows_workspace": (_sz, [_i, _i, _i]),
     "ssm_linear_rows": (_i, [_i, _fp, _l, _fp, _l, _fp, _fp, _fp, _l, _i, _i, _i, _f, _f, _vp, _sz,
                              _vp]),
+    "ssm_linear": (_i, [_fp, _l, _fp, _l, _fp, _fp, _l, _i, _i, _i, _f, _vp]),
+    "ssm_m1_xproj_dt": (_i, [_fp, _l, _fp, _fp, _fp, _l, _fp, _l, _i, _i, _i, _i, _vp]),
     "ssm_argmax": (_i, [_fp, _l, _i, _i, _vp, _vp]),
     "ssm_sample_workspace": (_sz, [_i, _i]),
     "ssm_sample": (_i, [_fp, _l, _i, _i, _d, _i, _d, _vp, _vp, _vp, _sz, _vp]),

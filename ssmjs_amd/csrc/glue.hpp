@@ -79,6 +79,20 @@ ssm_status launch_pack_frag(const float* W, long ldw, int N, int K, float* out, 
 // RMSNorm of a step.
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,
                          int d, hipStream_t st);
+// Prefill projection (gemm.hip): Y = beta * Y + s[m] X W^T (+ bias) on the fp32 matrix
+// cores; with ssq, s[m] = 1 / sqrt(inv_div * sum_j ssq[m nssq + j] + eps) (a row RMSNorm of
+// X applied after the product), else 1.
+bool gemm_ok(int M, int N, int K, long ldx, long ldw, long ldy);
+ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const float* bias,
+                       float* Y, long ldy, int M, int N, int K, float beta, hipStream_t st,
+                       const float* ssq = nullptr, int nssq = 0, float inv_div = 0.f,
+                       float eps = 0.f);
+// The Mamba-1 block's x_proj and dt_proj in one pass (gemm.hip): dbl = x Wx^T (T, R + 2N),
+// dt = dbl[:, :R] Wdt^T (T, D).
+bool xproj_dt_ok(int T, int D, int R, int N, long ldx, long lddbl, long lddt);
+ssm_status launch_xproj_dt(const float* x, long ldx, const float* Wx, const float* Wdt,
+                           float* dbl, long lddbl, float* dt, long lddt, int T, int D, int R,
+                           int N, hipStream_t st);
 // The Mamba-2 one-token state update with the gated RMSNorm's element-wise part:
 // y = (C.h + D x) * silu(z) * gn in fragment order (K = H P), and per workgroup the partial sum
 // of ((C.h + D x) silu(z))^2 into ssq (B, m2_gated_nssq(H, P, N)). ssd.hip.

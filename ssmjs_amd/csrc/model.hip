@@ -27,6 +27,7 @@
 
 #include "common.hpp"
 #include "glue.hpp"
+#include "ssd.hpp"
 
 // ------------------------------------------------------------------ errors
 namespace ssm {
@@ -216,8 +217,18 @@ ssm_ctx::LtPlan& lt_plan(ssm_ctx* c, int M, int Nout, int K, long ldx, long ldy)
 }
 
 // Y (M, Nout) [ld ldy] = X (M, K) [ld ldx] * W^T, W (Nout, K) row-major; Y = beta*Y + ...
-// hipBLASLt takes K >= 128 (below that rocBLAS measured faster), rocBLAS the rest and any
-// shape hipBLASLt has no algorithm for; SSM_GEMM=rocblas sends everything to rocBLAS.
+// Prefill-sized products (M >= kOwnGemmRows) run the fp32 matrix-core kernel of gemm.hip;
+// the few-row products of decode go to hipBLASLt for K >= 128 (below that rocBLAS measured
+// faster) and rocBLAS for the rest and any shape hipBLASLt has no algorithm for.
+// SSM_GEMM=lib sends every product to the libraries, SSM_GEMM=rocblas everything to rocBLAS.
+constexpr int kOwnGemmRows = 256;
+bool own_kernels(int M) {
+    static const bool lib_only = [] {
+        const char* e = std::getenv("SSM_GEMM");
+        return e && (std::strcmp(e, "lib") == 0 || std::strcmp(e, "rocblas") == 0);
+    }();
+    return !lib_only && M >= kOwnGemmRows;
+}
 ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, const float* W,
                 float* Y, long ldy, float beta) {
     if (M == 0 || Nout == 0) return SSM_OK;
@@ -226,6 +237,9 @@ ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, co
         const char* e = std::getenv("SSM_GEMM");
         return e && std::strcmp(e, "rocblas") == 0;
     }();
+    if (own_kernels(M) && ssm::gemm_ok(M, Nout, K, ldx, K, ldy) &&
+        (((uintptr_t)X | (uintptr_t)W) & 15) == 0)
+        return ssm::launch_gemm(X, ldx, W, K, nullptr, Y, ldy, M, Nout, K, beta, c->stream);
     if (c->lt && K >= 128 && !rb_only) {
         auto& p = lt_plan(c, M, Nout, K, ldx, ldy);
         if (p.ok) {
@@ -693,6 +707,8 @@ ssm_status ensure_ids(ssm_model* m, size_t n) {
     return SSM_OK;
 }
 
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 // One mixer over (B, L) tokens: reads x (T, d) [normalised], adds its output into out (T, d)
 // with beta (0: overwrite, 1: residual add). ssm/conv state may be null (zero initial state).
 ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, float beta, int B,
@@ -710,8 +726,16 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
         { Stage g(c, "m1.conv");
           SSM_TRY(ssm_causal_conv1d(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, B, L, d.D,
                                     d.K, 1, conv_st, conv_st, st)); }
-        { Stage g(c, "m1.x_proj"); SSM_TRY(gemm(c, T, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
-        { Stage g(c, "m1.dt_proj"); SSM_TRY(gemm(c, T, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
+        if (own_kernels(T) && ssm::xproj_dt_ok(T, d.D, d.R, d.N, d.D, RN, d.D) &&
+            al16(W + Ly.x_proj) && al16(W + Ly.dt_w)) {
+            // x_proj and dt_proj in one pass (dt_low stays on chip)
+            Stage g(c, "m1.x_dt_proj");
+            SSM_TRY(ssm::launch_xproj_dt(xc, d.D, W + Ly.x_proj, W + Ly.dt_w, dbl, RN, dtv, d.D,
+                                         T, d.D, d.R, d.N, st));
+        } else {
+            { Stage g(c, "m1.x_proj"); SSM_TRY(gemm(c, T, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
+            { Stage g(c, "m1.dt_proj"); SSM_TRY(gemm(c, T, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
+        }
         { Stage g(c, "m1.scan");
           SSM_TRY(ssm_selective_scan(xc, d.D, dtv, d.D, W + Ly.dt_b, 1, A, dbl + d.R, RN,
                                      dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D, y, d.D, B,
@@ -724,20 +748,39 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
         { Stage g(c, "m2.conv");
           SSM_TRY(ssm_causal_conv1d(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc, d.cd, B, L,
                                     d.cd, d.K, 1, conv_st, conv_st, st)); }
-        { Stage g(c, "m2.ssd");
-          SSM_TRY(ssm_ssd_chunk_scan(SSM_F32, xbc, d.cd, zx + d.D + d.cd, d.nin, W + Ly.dt_b, 1,
-                                     0.f, INFINITY, A, xbc + d.D, d.cd, xbc + d.D + GN, d.cd,
-                                     W + Ly.Dsk, y, d.D, B, L, d.H, d.P, d.G, d.N, ssm_st, ssm_st,
-                                     w.scan, w.scan_bytes, st)); }
-        { Stage g(c, "m2.gated_norm");
-          SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, T, d.D, d.G, d.eps,
-                                    st)); }
-        { Stage g(c, "m2.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, beta)); }
+        const float* dtp = zx + d.D + d.cd;
+        const bool fuse_gate =
+            own_kernels(T) && ssm::gemm_ok(T, d.d, d.D, d.D, d.D, d.d) &&
+            al16(W + Ly.out_proj) &&
+            ssm::ssd_gated_ok(d.P, d.G, d.N, d.cd, d.nin, d.cd, d.cd, d.D, d.nin, xbc, xbc + d.D,
+                              xbc + d.D + GN, y, zx, W + Ly.gnorm);
+        if (fuse_gate) {
+            // The gated RMSNorm split over its neighbours: the SSD stores u * g (u = y silu(z))
+            // and per-head sums of u^2 (in yn's space), and out_proj scales each row by
+            // 1 / rms(u) after the product.
+            { Stage g(c, "m2.ssd_gate");
+              SSM_TRY(ssm::ssd_f32(xbc, d.cd, dtp, d.nin, W + Ly.dt_b, 1, 0.f, INFINITY, A,
+                                   xbc + d.D, d.cd, xbc + d.D + GN, d.cd, W + Ly.Dsk, y, d.D, B, L,
+                                   d.H, d.G, d.N, ssm_st, ssm_st, w.scan, w.scan_bytes, st, zx,
+                                   d.nin, W + Ly.gnorm, yn)); }
+            { Stage g(c, "m2.out_proj");
+              SSM_TRY(ssm::launch_gemm(y, d.D, W + Ly.out_proj, d.D, nullptr, out, d.d, T, d.d,
+                                       d.D, beta, st, yn, d.H, 1.f / (float)d.D, d.eps)); }
+        } else {
+            { Stage g(c, "m2.ssd");
+              SSM_TRY(ssm_ssd_chunk_scan(SSM_F32, xbc, d.cd, dtp, d.nin, W + Ly.dt_b, 1,
+                                         0.f, INFINITY, A, xbc + d.D, d.cd, xbc + d.D + GN, d.cd,
+                                         W + Ly.Dsk, y, d.D, B, L, d.H, d.P, d.G, d.N, ssm_st,
+                                         ssm_st, w.scan, w.scan_bytes, st)); }
+            { Stage g(c, "m2.gated_norm");
+              SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, T, d.D, d.G,
+                                        d.eps, st)); }
+            { Stage g(c, "m2.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, beta)); }
+        }
     }
     return SSM_OK;
 }
 
-bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // y (M, N) [ld ldy] = beta*y + s * p(x) W^T (mode 1: RMSNorm with weight g; mode 2: gated
 // RMSNorm with z, one group): the few-row kernel (M <= 64) with the norm in its prologue

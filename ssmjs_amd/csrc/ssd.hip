@@ -925,6 +925,24 @@ extern "C" size_t ssm_ssd_workspace(int B, int L, int H, int Pd, int G, int N) {
     return std::max(bf, ssm::ssd_f32_workspace(B, L, H, Pd, N));
 }
 
+namespace ssm {
+
+// Whether the fp32 matrix-core SSD can also apply the gated RMSNorm's element-wise part (one
+// norm group; the offsets and alignments of its fp32 path).
+bool ssd_gated_ok(int Pd, int G, int N, long ldx, long lddt, long ldb, long ldc, long ldy,
+                  long ldz, const void* x, const void* Bm, const void* Cm, const float* y,
+                  const float* z, const float* gn) {
+    const long lim = (1L << 31) / Q;
+    const bool fit = ldx * 4 < lim && ldb * 4 < lim && ldc * 4 < lim && ldy * 4 < lim &&
+                     lddt * 4 < lim && ldz * 4 < lim;
+    const bool al = (((uintptr_t)x | (uintptr_t)Bm | (uintptr_t)Cm | (uintptr_t)y |
+                      (uintptr_t)z | (uintptr_t)gn) & 15) == 0 &&
+                    (ldx | ldb | ldc | ldy | ldz) % 4 == 0;
+    return G == 1 && ssd_f32_shape(Pd, N) && fit && al;
+}
+
+}  // namespace ssm
+
 extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, const float* dt,
                                          long lddt, const float* dt_bias, int softplus,
                                          float dt_min, float dt_max, const float* A,

@@ -67,9 +67,14 @@ struct F32Args {
     float* seg_state;   // (B,H,nseg,P,N)
     float* seg_decay;   // (B,H,nseg)
     int remap;
+    // gated output (GATED): y <- u * gn with u = y * silu(z), and ssq (B*L, H) = sum over the
+    // head's P channels of u^2 (the gated RMSNorm's element-wise part and its partial sums)
+    const float* z; long ldz;
+    const float* gn;
+    float* ssq;
 };
 
-template <int NN, bool FULL>
+template <int NN, bool FULL, bool GATED>
 struct SmemF32 {
     static constexpr int BP = NN + 4;    // B / C row pitch (floats): b128 rows conflict-free
     static constexpr int MP = QF + 4;    // M^T row pitch
@@ -79,6 +84,7 @@ struct SmemF32 {
     float ac[2][QF];    // acum_t in log2 units
     float dv[2][QF];    // dt'_t
     float wj[2][QF];    // w_t = 2^(acum_end - acum_t) dt'_t
+    float sq[GATED ? 2 : 1][GATED ? 4 : 1][GATED ? QF : 1];   // per-wave sums of u^2 per row
 };
 
 using ssm::bload16;
@@ -106,10 +112,10 @@ __device__ __forceinline__ float wave_prefix_sum(float v) {
 
 __device__ __forceinline__ float4 as_f4(floatx4 v) { return make_float4(v[0], v[1], v[2], v[3]); }
 
-template <int NN, bool FULL>
+template <int NN, bool FULL, bool GATED = false>
 __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
-    __shared__ __attribute__((aligned(16))) SmemF32<NN, FULL> sm;
-    using SM = SmemF32<NN, FULL>;
+    __shared__ __attribute__((aligned(16))) SmemF32<NN, FULL, GATED> sm;
+    using SM = SmemF32<NN, FULL, GATED>;
     constexpr int NB = NN / 16;          // n blocks (state tiles per wave, k groups of C B^T)
     constexpr int QB = QF / 16;          // time blocks per chunk
     constexpr int NCB = QB * (QB + 1) / 2;   // causal C B^T tiles per chunk
@@ -137,6 +143,9 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     const float Ah = a.A[h] * ssm::kLog2e;
     const float dtb = a.dt_bias ? a.dt_bias[h] : 0.f;
     const float Dh = a.Dsk ? a.Dsk[h] : 0.f;
+    // gated output: this lane's four norm weights (columns p0 + 4 q4 .. + 3 of the head)
+    float4 gw = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (GATED) gw = *reinterpret_cast<const float4*>(a.gn + (long)h * PF + p0 + 4 * q4);
 
     const int c_begin = seg * a.chunks_per_seg;
     const int c_end = min(c_begin + a.chunks_per_seg, a.nchunks);
@@ -147,6 +156,15 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     const float* cm0 = a.Cm + brow * a.ldc + (long)g * NN;
     const float* d0 = a.dt + brow * a.lddt + h;
     auto rows_of = [&](int c) { return c < c_end ? min(QF, a.L - c * QF) : 0; };
+    // ssq[(b L + t) H + h] for row tid of chunk c from the four waves' partial sums
+    auto flush_ssq = [&](int c, int bf) {
+        const int t = c * QF + tid;
+        if (t < a.L) {
+            const float v = (sm.sq[bf][0][tid] + sm.sq[bf][1][tid]) +
+                            (sm.sq[bf][2][tid] + sm.sq[bf][3][tid]);
+            a.ssq[(brow + t) * a.H + h] = v;
+        }
+    };
     auto span = [](int qv, long ld, int width) {
         return qv > 0 ? (unsigned)(((long)(qv - 1) * ld + width) * 4) : 0u;
     };
@@ -243,6 +261,10 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
             for (int s = 0; s < 4; ++s) xv[jb][s] = raw.x[jb][s];
         __syncthreads();
         load_raw(c + 1);   // past the segment: an empty range, the loads return zeros
+        if constexpr (GATED) {
+            // the previous chunk's row sums of u^2, added over the four waves in order
+            if (c > c_begin && tid < QF) flush_ssq(c - 1, buf ^ 1);
+        }
 
         if constexpr (FULL) {
             // ---- M^T tiles of C B^T (this wave's share of the causal tiles)
@@ -340,9 +362,28 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
                 }
             // ---- y rows 16 ib + l16, columns p0 + 4 q4 .. +3 (rows past L are dropped)
             const auto ry = rsrc(a.y + row0 * a.ldy + (long)h * PF, span(qv, a.ldy, PF));
+            if constexpr (GATED) {
+                // u = y silu(z) and u * gn; the row's sum of u^2 over this wave's 16 columns
+                // (lane groups q4 added pairwise with xor shuffles: the same bits in each)
+                const auto rz = rsrc(a.z + row0 * a.ldz + (long)h * PF, span(qv, a.ldz, PF));
 #pragma unroll
-            for (int ib = 0; ib < QB; ++ib)
-                bstore16(as_f4(Y[ib]), ry, (unsigned)((16 * ib + l16) * a.ldy + p0 + 4 * q4) * 4u);
+                for (int ib = 0; ib < QB; ++ib) {
+                    const float4 zv =
+                        bload16<float4>(rz, (unsigned)((16 * ib + l16) * a.ldz + p0 + 4 * q4) * 4u);
+                    const float u0 = Y[ib][0] * ssm::silu(zv.x), u1 = Y[ib][1] * ssm::silu(zv.y);
+                    const float u2 = Y[ib][2] * ssm::silu(zv.z), u3 = Y[ib][3] * ssm::silu(zv.w);
+                    float ss = (u0 * u0 + u1 * u1) + (u2 * u2 + u3 * u3);
+                    ss += __shfl_xor(ss, 16);
+                    ss += __shfl_xor(ss, 32);
+                    if (q4 == 0) sm.sq[buf][w][16 * ib + l16] = ss;
+                    bstore16(make_float4(u0 * gw.x, u1 * gw.y, u2 * gw.z, u3 * gw.w), ry,
+                             (unsigned)((16 * ib + l16) * a.ldy + p0 + 4 * q4) * 4u);
+                }
+            } else {
+#pragma unroll
+                for (int ib = 0; ib < QB; ++ib)
+                    bstore16(as_f4(Y[ib]), ry, (unsigned)((16 * ib + l16) * a.ldy + p0 + 4 * q4) * 4u);
+            }
         }
 
         // ---- state: S^T = 2^acum_end S^T + sum_j B[j][n] (X[j][p] w_j)
@@ -378,6 +419,11 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
             }
         }
         state_live = true;
+    }
+
+    if constexpr (GATED) {
+        __syncthreads();
+        if (c_end > c_begin && tid < QF) flush_ssq(c_end - 1, (c_end - 1) & 1);
     }
 
     // ---- outputs of the state
@@ -437,7 +483,8 @@ ssm_status launch(F32Args& a, hipStream_t st) {
     }
     const int nwg = a.B * a.H * a.nseg;
     a.remap = (nwg % 8 == 0) ? 1 : 0;
-    ssd_f32_kernel<NN, true><<<nwg, 256, 0, st>>>(a);
+    if (a.ssq) ssd_f32_kernel<NN, true, true><<<nwg, 256, 0, st>>>(a);
+    else ssd_f32_kernel<NN, true><<<nwg, 256, 0, st>>>(a);
     return ssm::check_launch("ssd_f32_chunk_scan");
 }
 
@@ -459,8 +506,16 @@ ssm_status ssd_f32(const float* x, long ldx, const float* dt, long lddt, const f
                    int softplus, float dt_min, float dt_max, const float* A, const float* Bm,
                    long ldb, const float* Cm, long ldc, const float* Dsk, float* y, long ldy,
                    int B, int L, int H, int G, int N, const float* h0, float* hT,
-                   void* workspace, size_t workspace_bytes, hipStream_t st) {
+                   void* workspace, size_t workspace_bytes, hipStream_t st, const float* z,
+                   long ldz, const float* gn, float* ssq) {
     F32Args a{};
+    a.z = z; a.ldz = ldz; a.gn = gn; a.ssq = ssq;
+    if (ssq) {
+        SSM_REQUIRE(z && gn && ldz >= (long)H * PF, "ssd_f32: the gated output needs z and gn");
+        SSM_REQUIRE(((uintptr_t)z | (uintptr_t)gn | (uintptr_t)y) % 16 == 0 && ldz % 4 == 0 &&
+                        ldy % 4 == 0,
+                    "ssd_f32: gated output needs 16-byte aligned z, gn, y rows");
+    }
     a.x = x; a.ldx = ldx; a.dt = dt; a.lddt = lddt; a.dt_bias = dt_bias; a.softplus = softplus;
     a.dt_min = dt_min; a.dt_max = dt_max; a.A = A; a.Bm = Bm; a.ldb = ldb; a.Cm = Cm;
     a.ldc = ldc; a.Dsk = Dsk; a.y = y; a.ldy = ldy; a.B = B; a.L = L; a.H = H; a.G = G;

@@ -193,6 +193,29 @@ def linear_rows(x, W, mode=0, g=None, z=None, eps=1e-5, out=None, beta=0.0, work
     return y
 
 
+def linear(x, W, bias=None, out=None, beta=0.0):
+    """y = beta*y + x W^T (+ bias) for any number of rows (ssm_linear, fp32 matrix cores)."""
+    M, K = x.shape
+    N = W.shape[0]
+    y = out if out is not None else torch.zeros(M, N, device=x.device, dtype=torch.float32)
+    _lib.call("ssm_linear", _p(x), x.stride(0), _p(W), W.stride(0),
+              _p(bias) if bias is not None else None, _p(y), y.stride(0), M, N, K, float(beta),
+              _stream())
+    return y
+
+
+def m1_xproj_dt(x, Wx, Wdt, d_state):
+    """Mamba-1 x_proj then dt_proj in one pass (ssm_m1_xproj_dt): returns (dbl, dt) with
+    dbl = x Wx^T (T, R + 2N) and dt = dbl[:, :R] Wdt^T (T, D)."""
+    T, D = x.shape
+    R = Wdt.shape[1]
+    dbl = torch.empty(T, R + 2 * d_state, device=x.device, dtype=torch.float32)
+    dt = torch.empty(T, D, device=x.device, dtype=torch.float32)
+    _lib.call("ssm_m1_xproj_dt", _p(x), x.stride(0), _p(Wx), _p(Wdt), _p(dbl), dbl.stride(0),
+              _p(dt), dt.stride(0), T, D, R, d_state, _stream())
+    return dbl, dt
+
+
 def gated_rmsnorm(x, z, w, groups=1, eps=1e-5, out=None):
     M, n = x.shape
     y = out if out is not None else torch.empty_like(x)

@@ -493,6 +493,76 @@ def test_linear_rows(mode, M, N, Kd, strided):
         assert np.array_equal(outs[1], outs[2])
 
 
+def _elementwise_ok(a, b, rel=1e-4, floor=1e-6):
+    """|a - b| <= rel |b| + floor max|b| for every element."""
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return bool(np.all(np.abs(a - b) <= rel * np.abs(b) + floor * np.abs(b).max()))
+
+
+@pytest.mark.parametrize("M,N,Kd,pad,bias,beta", [
+    (5, 16, 48, 0, False, 0.0),          # one partial tile, K = 48: a partial 32-wide step
+    (1000, 80, 1536, 8, False, 0.0),     # x_proj shape: 80 of 128 columns, strided x
+    (777, 130, 52, 4, True, 1.0),        # ragged in every dimension, bias and residual add
+    (513, 1536, 48, 0, True, 0.0),       # dt_proj shape: K = 48 only
+    (256, 768, 1536, 0, False, 1.0),     # out_proj shape with the residual add
+])
+def test_linear_prefill_vs_oracle(M, N, Kd, pad, bias, beta):
+    """Prefill projection (ssm_linear, the Linear layers behind model.forward,
+    streaming.ts:31-35) against the oracle's linear, element by element:
+    |gpu - ref| <= 1e-4 |ref| + 1e-6 max|ref|."""
+    case(f"linear M={M} N={N} K={Kd} pad={pad} bias={bias} beta={beta}")
+    r = rng(60 + M)
+    xb = r.standard_normal((M, Kd + pad)).astype(np.float32)
+    x = xb[:, :Kd]
+    W = (r.standard_normal((N, Kd)) / np.sqrt(Kd)).astype(np.float32)
+    b = r.standard_normal(N).astype(np.float32) if bias else None
+    y0 = r.standard_normal((M, N)).astype(np.float32)
+    ref = O.linear(np.ascontiguousarray(x), W, b) + beta * y0
+    out = dev(y0)
+    K().linear(dev(xb)[:, :Kd], dev(W), bias=dev(b) if bias else None, out=out, beta=beta)
+    got = host(out)
+    assert _elementwise_ok(got, ref), err(got, ref)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(8192, 3072, 768), (8192, 768, 1536), (4096, 8512, 2048)])
+def test_linear_prefill_full_shapes(M, N, Kd):
+    """The cfg2 in_proj / out_proj and a cfg3-layer in_proj slice (4096 of its 32768 rows)
+    at full width, element by element against a float64 product of the same fp32 inputs
+    (|gpu - ref| <= 1e-4 |ref| + 1e-6 max|ref|); a second call gives the same bits."""
+    case(f"linear full M={M} N={N} K={Kd}")
+    g = torch.Generator().manual_seed(M + N + Kd)
+    x = torch.randn(M, Kd, generator=g)
+    W = torch.randn(N, Kd, generator=g) / Kd ** 0.5
+    ref = (x.double() @ W.double().T).numpy()
+    xd, Wd = x.cuda(), W.cuda()
+    a = host(K().linear(xd, Wd))
+    b = host(K().linear(xd, Wd))
+    assert np.array_equal(a, b)
+    assert _elementwise_ok(a, ref), err(a, ref)
+
+
+@pytest.mark.parametrize("T,D,R,N,pad", [(8192, 1536, 48, 16, 0), (1000, 1536, 48, 16, 8),
+                                         (77, 256, 16, 16, 0), (300, 128, 8, 16, 4),
+                                         (64, 2048, 64, 32, 0)])
+def test_m1_xproj_dt_vs_oracle(T, D, R, N, pad):
+    """x_proj then dt_proj of the Mamba-1 block in one kernel (ssm_m1_xproj_dt) against the
+    oracle's two linears, element by element (|gpu - ref| <= 1e-4 |ref| + 1e-6 max|ref|): dbl
+    = x Wx^T (dt_low | B | C) and dt = dt_low Wdt^T. cfg2's shape (T = B L = 8192, D 1536,
+    R 48, N 16), ragged row counts, strided x, and R = 8 / 16 / 64."""
+    case(f"m1_xproj_dt T={T} D={D} R={R} N={N} pad={pad}")
+    r = rng(70 + T)
+    xb = r.standard_normal((T, D + pad)).astype(np.float32)
+    x = xb[:, :D]
+    Wx = (0.5 * r.standard_normal((R + 2 * N, D)) / np.sqrt(D)).astype(np.float32)
+    Wdt = (r.standard_normal((D, R)) / np.sqrt(R)).astype(np.float32)
+    dbl_ref = O.linear(np.ascontiguousarray(x), Wx)
+    dt_ref = O.linear(np.ascontiguousarray(dbl_ref[:, :R]), Wdt)
+    dbl, dt = K().m1_xproj_dt(dev(xb)[:, :D], dev(Wx), dev(Wdt), N)
+    dbl, dt = host(dbl), host(dt)
+    assert _elementwise_ok(dbl, dbl_ref), err(dbl, dbl_ref)
+    assert _elementwise_ok(dt, dt_ref), err(dt, dt_ref)
+
+
 @pytest.mark.parametrize("n,pad", [(32000, 0), (1001, 3), (7, 0)])
 def test_argmax_ties_nan_and_tails(n, pad):
     """Greedy pick = sampleToken with topK 1 (streaming.ts:74-75): the lowest index among
