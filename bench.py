@@ -55,7 +55,9 @@ METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 # profiles/. Re-measured when the
 # kernels change; None where not measured.
 TRAFFIC = {
-    ("cfg2", "m1.in_proj"): 339_224_576,               # hipBLASLt sgemm (tile re-reads)
+    ("cfg2", "m1.in_proj"): 268_210_726,               # gemm_f32_kernel<4>
+    ("cfg2", "m1.x_dt_proj"): 111_058_521,             # xproj_dt_kernel
+    ("cfg2", "m1.out_proj"): 113_500_326,              # gemm_f32_kernel<3>
     ("cfg3", "bf16"): 848_125_952,                     # ssd_kernel (two heads per workgroup)
     ("cfg3", "f32"): 1_165_402_958,                    # ssd_f32_kernel
     ("cfg4", "m2.step.state_update"): 136_517_632,     # m2_update_kernel
@@ -65,7 +67,8 @@ TRAFFIC = {
 # an entry goes stale when its kernel changes after that commit.
 TRAFFIC_MEASURED_AT = {k: "e7034fa" for k in TRAFFIC}
 TRAFFIC_MEASURED_AT.update({("cfg3", "f32"): "805df87", ("cfg3", "bf16"): "805df87",
-                            ("cfg5", "bf16"): "805df87", ("cfg2", "m1.in_proj"): "7c96b77",
+                            ("cfg5", "bf16"): "805df87", ("cfg2", "m1.in_proj"): "6da5abd",
+                            ("cfg2", "m1.x_dt_proj"): "6da5abd", ("cfg2", "m1.out_proj"): "6da5abd",
                             ("cfg4", "m2.step.state_update"): "7c96b77"})
 
 
