@@ -120,10 +120,19 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
         ox[u] = (unsigned)(((long)r * a.ldx + 4 * q) * 4);
         ow[u] = (2 * w + u < 2 * NJ) ? (unsigned)(((long)r * a.ldw + 4 * q) * 4) : 0x80000000u;
     }
+    // The step's k offset rides in the scalar offset. In the main loop every load is in
+    // range and the per-lane offsets are fixed (no vector ALU work between the MFMAs); in the
+    // tail, lanes whose k is past K (the last partial step, and the steps after it) get bit
+    // 31 in their own offset, which alone puts them out of range.
     auto load = [&](float* s, int k0) {
-        // The step's k offset rides in the scalar offset; lanes whose k is past K (the tail of
-        // the last step, and the steps after it) get bit 31 in their own offset, which alone
-        // puts them out of range.
+        const unsigned kk = (unsigned)k0 * 4u;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            to_lds(rx, s + (2 * w + u) * kFrag, ox[u], kk);
+            to_lds(rw, s + (8 + 2 * w + u) * kFrag, ow[u], kk);
+        }
+    };
+    auto load_tail = [&](float* s, int k0) {
         const unsigned kk = (unsigned)min(k0, a.K) * 4u;
         const unsigned oor = k0 + 4 * q < a.K ? 0u : 0x80000000u;
 #pragma unroll
@@ -156,26 +165,38 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
                 for (int j = 0; j < NJ; ++j) acc[i][j] = mfma4(xa[i][t], wb[j][t], acc[i][j]);
     };
 
-    // Steps in blocks of four (one per stage); a block that runs past K computes on zeros.
+    // Steps in blocks of four (one per stage): the main loop while every load of a block is
+    // a whole step inside K, then the tail blocks with range-checked loads (a block that
+    // runs past K computes on zeros).
     const int nk = (a.K + BK - 1) / BK;
-    load(s0, 0);
-    load(s1, BK);
-    load(s2, 2 * BK);
-    end_step();
-    for (int s = 0; s < nk; s += 4) {
-        load(s3, (s + 3) * BK);
+    const int nfull = a.K / BK;   // steps that lie wholly inside K
+    auto block = [&](int s, auto ld) {
+        ld(s3, (s + 3) * BK);
         compute(s0);
         end_step();
-        load(s0, (s + 4) * BK);
+        ld(s0, (s + 4) * BK);
         compute(s1);
         end_step();
-        load(s1, (s + 5) * BK);
+        ld(s1, (s + 5) * BK);
         compute(s2);
         end_step();
-        load(s2, (s + 6) * BK);
+        ld(s2, (s + 6) * BK);
         compute(s3);
         end_step();
+    };
+    if (nfull >= 3) {
+        load(s0, 0);
+        load(s1, BK);
+        load(s2, 2 * BK);
+    } else {
+        load_tail(s0, 0);
+        load_tail(s1, BK);
+        load_tail(s2, 2 * BK);
     }
+    end_step();
+    int s = 0;
+    for (; s + 7 <= nfull; s += 4) block(s, load);
+    for (; s < nk; s += 4) block(s, load_tail);
 
     // ---- row scales of the tile's rows (partial sums added in order)
     if constexpr (RS) {
