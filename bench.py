@@ -9,7 +9,8 @@ BASELINE.json's configurations that runs on one GPU. Its `value` is the SSD core
 its `roofline` is the SSD kernel against the fp32 matrix-core peak with the SURVEY 8(d)
 algorithmic FLOP count. The default run also reports, under "extra": the whole cfg3 layer
 (in_proj -> conv -> SSD -> gated RMSNorm -> out_proj) timed per stage, the SSD with bf16
-inputs, the cfg2 Mamba-1 block, the cfg4 decode step and the cfg5 long-context SSD.
+inputs, the cfg2 Mamba-1 block, the cfg4 decode step, the cfg5 long-context SSD and the
+decode step through Mamba-1 layers.
 
 Workloads (--workload picks one line; the default is cfg3 with the extras):
   cfg1  Mamba-1 causal conv1d + selective scan, fp32, B=1 L=256 D=512 N=16 (parity case)
@@ -21,6 +22,8 @@ Workloads (--workload picks one line; the default is cfg3 with the extras):
         one greedy step (24 layers + LM head + argmax) per bench step, fp32; --sampling
         draws the token with sampleToken on the device instead (T 0.8, topK 50, topP 0.9)
   cfg5  Mamba-2 SSD long-context prefill core, B=1 L=65536 H=32 P=64 N=128, bf16
+  decode_m1  the cfg4 decode step through 24 Mamba-1 layers (the reference's default layer
+        type) with cfg2's block dimensions (d=768 D=1536 N=16 R=48), V=32000, 64 sequences
 A step is one pass of the path over one batch of synthetic input that is already resident in
 HBM. Timing: W untimed warmup steps, then K steps between HIP events on the stream the
 library launches on (torch's current stream, handed to the library context).
@@ -78,7 +81,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default=None,
-                    choices=["cfg1", "cfg2", "cfg3", "cfg3layer", "cfg4", "cfg5", "copy"],
+                    choices=["cfg1", "cfg2", "cfg3", "cfg3layer", "cfg4", "cfg5", "decode_m1",
+                             "copy"],
                     help="one line for this workload only (default: cfg3 fp32 plus extras)")
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -579,6 +583,60 @@ def w_cfg4(torch, np, dev, args):
     return out
 
 
+def w_decode_m1(torch, np, dev, args):
+    """The same greedy decode step through 24 Mamba-1 layers (the reference's default layer
+    type) with cfg2's block dimensions, 64 cached sequences, vocabulary 32000."""
+    from ssmjs_amd import _lib, backend
+    Bsz, d, nl, N, R, V = 64, 768, 24, 16, 48, 32000
+    D = 2 * d
+    cfg = {"vocabSize": V, "dModel": d, "numLayers": nl, "dState": N, "dConv": 4, "expand": 2,
+           "nHeads": 12, "dtRank": R, "layers": [{"type": "mamba1"}] * nl}
+    m = backend.Model(dev, cfg, seed=1006)
+    st = m.new_state(Bsz)
+    n = _lib.lib().ssm_state_floats(st._h)
+    r = np.random.default_rng(1006)
+    st.write((0.1 * r.standard_normal(n, dtype=np.float32)).astype(np.float32))
+    bufs = [torch.from_numpy(r.integers(0, V, Bsz).astype(np.int32)).cuda(),
+            torch.empty(Bsz, dtype=torch.int32, device="cuda")]
+    k = [0]
+    steps, warm = args.steps or 256, args.warmup if args.warmup is not None else 8
+
+    def step():
+        a, b = bufs[k[0] % 2], bufs[(k[0] + 1) % 2]
+        _lib.call("ssm_decode_step_device", m.handle, st._h, a.data_ptr(), None, b.data_ptr())
+        k[0] += 1
+
+    ms = timed(torch, step, steps, warm)
+    stg = profiled_stages(dev, torch, step, min(steps, 32))
+    RN = R + 2 * N
+    alg = {
+        "m1.step.in_proj": (2.0 * Bsz * d * 2 * D,
+                            4.0 * (2 * D * d + Bsz * (d + 3 * D) + Bsz * D * 3 * 2)),
+        "m1.step.x_proj": (2.0 * Bsz * D * RN, 4.0 * (RN * D + Bsz * (D + RN + R))),
+        "m1.step.dt_proj": (2.0 * Bsz * R * D, 4.0 * (D * R + Bsz * (R + D))),
+        "m1.step.state_update": (None, 4.0 * Bsz * D * N * 2 + 4.0 * D * N
+                                 + 4.0 * Bsz * (4 * D + 2 * N)),
+        "m1.step.out_proj": (2.0 * Bsz * D * d, 4.0 * (d * D + Bsz * (D + 3 * d))),
+    }
+    stages = {}
+    for kk, (nl_, avg) in stg.items():
+        if kk in alg:
+            f, b = alg[kk]
+            stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None)
+    step_bytes = nl * sum(v[1] for v in alg.values()) + 4.0 * V * d
+    dom = max(stages.values(), key=lambda r_: r_["avg_ms"])
+    st.destroy()
+    m.destroy()
+    return {"value": Bsz / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+            "dtype": "f32",
+            "config": {"workload": "Mamba-1 24-layer recurrent decode (cfg2's block dimensions), "
+                                   "one greedy token for each of 64 cached sequences per step",
+                       "batch": Bsz, "d_model": d, "layers": nl, "d_inner": D, "d_state": N,
+                       "dt_rank": R, "vocab": V, "tokens_per_step": Bsz},
+            "roofline": dom, "stages": stages,
+            "step_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def w_copy(torch, args):
     """Counter calibration, not a bench line: one elementwise kernel (y = x * 1) that reads
     and writes exactly 1 GiB each, so FETCH_SIZE / WRITE_SIZE of a rocprofv3 --pmc run can be
@@ -627,6 +685,7 @@ def main():
         "cfg3": lambda a: ssd_workload(torch, np, dev, a, 8, 4096, 64, 1.0, cfg3_name, "f32"),
         "cfg3layer": lambda a: w_cfg3layer(torch, np, dev, a),
         "cfg4": lambda a: w_cfg4(torch, np, dev, a),
+        "decode_m1": lambda a: w_decode_m1(torch, np, dev, a),
         "cfg5": lambda a: ssd_workload(torch, np, dev, a, 1, 65536, 32, 128 ** -0.25, cfg5_name,
                                        "bf16"),
     }
@@ -636,7 +695,7 @@ def main():
         # the other configurations, each with its own default steps, no CPU baseline
         for key, wl, dtype in (("cfg3_layer_f32", "cfg3layer", None), ("cfg3_bf16", "cfg3", "bf16"),
                                ("cfg2", "cfg2", None), ("cfg4", "cfg4", None),
-                               ("cfg5", "cfg5", None)):
+                               ("cfg5", "cfg5", None), ("decode_m1", "decode_m1", None)):
             a2 = argparse.Namespace(**vars(args))
             a2.steps, a2.warmup, a2.no_cpu_baseline, a2.dtype = None, None, True, dtype
             log(f"[bench] extra {key}")

@@ -69,12 +69,32 @@ struct StepProj {
     float* Yc = nullptr; long ldyc = 0;
     // EPI_RESID with g2: xg = Y * g2 in fragment order (K = N), ssq_out (M, N / 16)
     const float* g2 = nullptr; float* xg = nullptr; float* ssq_out = nullptr;
+    // EPI_CONV: the conv outputs also in fragment order (K = C, C % 16 == 0; rows M .. 16 mt - 1
+    // written as zeros), the operand of the step's next projection
+    float* Yf = nullptr;
     int mt = 0, nt = 0, rotate = 0;        // tiles and k-start rotation (set by the launcher)
 };
 bool stepproj_ok(int M, int N, int K);
 ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st);
 // W (N, K) row stride ldw -> fragment order in out (frag_floats(N, K) floats).
 ssm_status launch_pack_frag(const float* W, long ldw, int N, int K, float* out, hipStream_t st);
+// Mamba-1 one-token state update (scan_m1.hip): ykb = 0 writes y (B, D) with row stride ldy,
+// ykb > 0 in fragment order with K = 16 ykb. dtr given: the raw dt (before bias and softplus)
+// is formed in the kernel as dtr (B, R) [ld lddtr] times Wdt^T (Wdt (D, R) row-major, 16-byte
+// aligned, R % 4 == 0; D % 64 == 0) instead of read from dt.
+ssm_status launch_m1_update(const float* x, long ldx, const float* dt, long lddt,
+                            const float* dt_bias, int softplus, const float* A, const float* Bm,
+                            long ldb, const float* Cm, long ldc, const float* Dsk, const float* z,
+                            long ldz, float* y, long ldy, int ykb, float* h, int B, int D, int N,
+                            hipStream_t st, const float* dtr, long lddtr, const float* Wdt,
+                            int R);
+// The fused step's update: dt_proj formed in the kernel, softplus on, y in fragment order
+// (K = D, D % 64 == 0), the input of the step's out_proj.
+ssm_status launch_m1_update_frag(const float* x, long ldx, const float* dtr, long lddtr,
+                                 const float* Wdt, int R, const float* dt_bias, const float* A,
+                                 const float* Bm, long ldb, const float* Cm, long ldc,
+                                 const float* Dsk, const float* z, long ldz, float* yf, float* h,
+                                 int B, int D, int N, hipStream_t st);
 // xg = x * g in fragment order (K = d) and ssq (M, d / 16) partial sums of x^2: the first
 // RMSNorm of a step.
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,

@@ -470,6 +470,7 @@ struct ssm_model {
     // whenever the weights change
     float* wp = nullptr;
     std::vector<long> wp_in, wp_out;   // float offsets into wp per layer (-1: not packed)
+    std::vector<long> wp_x, wp_dt;     // Mamba-1 layers: x_proj and dt_proj
     int* d_flag = nullptr;   // out-of-range token id flag
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
@@ -663,7 +664,7 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
     const size_t nstep = L == 1 ? (size_t)B : 0;
     const size_t nstep16 = (nstep + 15) / 16 * 16;   // fragment order pads to 16-row tiles
     size_t o_xg = off; off += al(4 * nstep16 * d.d);
-    size_t o_yf = off; off += al(4 * nstep16 * (has2 ? d.D : 0));
+    size_t o_yf = off; off += al(4 * nstep16 * d.D);
     size_t o_sqi = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
     size_t o_sqy = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
     if (out) {
@@ -675,7 +676,7 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
         out->logits = (float*)(base + o_log);
         out->scan = base + o_scan; out->scan_bytes = scan;
         out->xg = nstep ? (float*)(base + o_xg) : nullptr;
-        out->yf = nstep && has2 ? (float*)(base + o_yf) : nullptr;
+        out->yf = nstep ? (float*)(base + o_yf) : nullptr;
         out->ssq_in = nstep ? (float*)(base + o_sqi) : nullptr;
         out->ssq_y = nstep ? (float*)(base + o_sqy) : nullptr;
     }
@@ -893,9 +894,20 @@ ssm_status mixer_step(ssm_model* m, const LayerW& Ly, float* hid, int B, float* 
 }
 
 // Whether a layer can take the fused one-token step: a Mamba-2 layer with one group whose
-// projections fit the step kernel (stepproj.hip) and whose state update has a gated variant.
+// projections fit the step kernel (stepproj.hip) and whose state update has a gated variant,
+// or a Mamba-1 layer whose in_proj, x_proj and out_proj fit it (dt_proj is formed inside the
+// state update).
 bool fusable(const ssm_model* m, const LayerW& Ly) {
     const Dims& d = m->dm;
+    if (Ly.type == SSM_LAYER_MAMBA1) {
+        if (d.N > 64 || d.K > 8) return false;
+        if (d.d % 16 != 0 || d.d / 16 > ssm::kStepProjMaxSsq) return false;
+        // dt_proj rows as float4; the update's workgroups span 64 channels
+        if (d.D % 64 != 0 || d.R % 4 != 0) return false;
+        const int RN = d.R + 2 * d.N;
+        return ssm::stepproj_ok(1, 2 * d.D, d.d) && ssm::stepproj_ok(1, RN, d.D) &&
+               ssm::stepproj_ok(1, d.d, d.D);
+    }
     if (Ly.type != SSM_LAYER_MAMBA2 || d.G != 1) return false;
     if (!(d.N == 64 || d.N == 128 || d.N == 256) || d.K > 8) return false;
     if (d.d % 16 != 0 || d.d / 16 > ssm::kStepProjMaxSsq) return false;
@@ -916,9 +928,17 @@ ssm_status pack_weights(ssm_model* m) {
         long off = 0;
         m->wp_in.assign(d.nl, -1);
         m->wp_out.assign(d.nl, -1);
+        m->wp_x.assign(d.nl, -1);
+        m->wp_dt.assign(d.nl, -1);
         for (int l = 0; l < d.nl; ++l) {
             if (!fusable(m, m->layers[l])) continue;
-            m->wp_in[l] = off; off += (long)ssm::frag_floats(d.nin, d.d);
+            if (m->layers[l].type == SSM_LAYER_MAMBA1) {
+                m->wp_in[l] = off; off += (long)ssm::frag_floats(2 * d.D, d.d);
+                m->wp_x[l] = off; off += (long)ssm::frag_floats(d.R + 2 * d.N, d.D);
+                m->wp_dt[l] = off; off += ((long)d.D * d.R + 63) / 64 * 64;
+            } else {
+                m->wp_in[l] = off; off += (long)ssm::frag_floats(d.nin, d.d);
+            }
             m->wp_out[l] = off; off += (long)ssm::frag_floats(d.d, d.D);
         }
         if (off == 0) return SSM_OK;
@@ -927,10 +947,69 @@ ssm_status pack_weights(ssm_model* m) {
     for (int l = 0; l < d.nl; ++l) {
         if (m->wp_in[l] < 0) continue;
         const LayerW& Ly = m->layers[l];
-        SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, d.nin, d.d, m->wp + m->wp_in[l], st));
+        if (Ly.type == SSM_LAYER_MAMBA1) {
+            const int RN = d.R + 2 * d.N;
+            SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, 2 * d.D, d.d,
+                                          m->wp + m->wp_in[l], st));
+            SSM_TRY(ssm::launch_pack_frag(m->w + Ly.x_proj, d.D, RN, d.D, m->wp + m->wp_x[l], st));
+            // dt_proj is formed inside the state update from row-major rows: an aligned copy
+            SSM_HIP_TRY(hipMemcpyAsync(m->wp + m->wp_dt[l], m->w + Ly.dt_w,
+                                       sizeof(float) * (size_t)d.D * d.R,
+                                       hipMemcpyDeviceToDevice, st));
+        } else {
+            SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, d.nin, d.d, m->wp + m->wp_in[l],
+                                          st));
+        }
         SSM_TRY(ssm::launch_pack_frag(m->w + Ly.out_proj, d.D, d.d, d.D, m->wp + m->wp_out[l],
                                       st));
     }
+    return SSM_OK;
+}
+
+// The fused one-token Mamba-1 layer step, four launches:
+//   in_proj  (row scale 1/rms from w.ssq_in on w.xg = hid * norm) with the conv update of the
+//            x columns in its epilogue: z into w.a (columns D .. 2D), SiLU(conv(x)) into w.b
+//            and, in fragment order, into w.yf;
+//   x_proj   w.yf -> (dt_r, B, C) into w.c;
+//   state update with dt_proj formed per thread (dt_r . W_dt[d], then bias and softplus),
+//            the D skip and the SiLU(z) gate; y in fragment order into w.yf;
+//   out_proj with the residual add into hid, and, given g_next, the next RMSNorm's operand
+//            hid * g_next in w.xg and its partial sums in w.ssq_in.
+// Same arithmetic as mixer_step up to the order of the norm's and dt_proj's sums and where
+// the norm's scale is applied (the row scale multiplies the projected row).
+ssm_status mixer_step_fused_m1(ssm_model* m, int l, float* hid, int B, float* ssm_st,
+                               float* conv_st, const Ws& w, const float* g_next) {
+    const Dims& d = m->dm;
+    const LayerW& Ly = m->layers[l];
+    ssm_ctx* c = m->ctx;
+    hipStream_t st = c->stream;
+    const float* W = m->w;
+    const int RN = d.R + 2 * d.N;
+    float *xz = w.a, *xc = w.b, *dbl = w.c;
+    { Stage g(c, "m1.step.in_proj");
+      ssm::StepProj p;
+      p.X = w.xg; p.W = m->wp + m->wp_in[l]; p.M = B; p.N = 2 * d.D; p.K = d.d;
+      p.ssq = w.ssq_in; p.nssq = d.d / 16; p.inv_div = 1.f / (float)d.d; p.eps = d.eps;
+      p.Y = xz; p.ldy = 2 * d.D;
+      p.c0 = 0; p.C = d.D; p.Kc = d.K; p.cw = W + Ly.conv_w; p.cb = W + Ly.conv_b;
+      p.cst = conv_st; p.Yc = xc; p.ldyc = d.D; p.Yf = w.yf;
+      SSM_TRY(ssm::launch_stepproj(ssm::EPI_CONV, p, st)); }
+    { Stage g(c, "m1.step.x_proj");
+      ssm::StepProj p;
+      p.X = w.yf; p.W = m->wp + m->wp_x[l]; p.M = B; p.N = RN; p.K = d.D;
+      p.Y = dbl; p.ldy = RN;
+      SSM_TRY(ssm::launch_stepproj(ssm::EPI_STORE, p, st)); }
+    { Stage g(c, "m1.step.state_update");
+      SSM_TRY(ssm::launch_m1_update_frag(xc, d.D, dbl, RN, m->wp + m->wp_dt[l], d.R,
+                                         W + Ly.dt_b, m->Ab + Ly.A, dbl + d.R, RN,
+                                         dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D,
+                                         w.yf, ssm_st, B, d.D, d.N, st)); }
+    { Stage g(c, "m1.step.out_proj");
+      ssm::StepProj p;
+      p.X = w.yf; p.W = m->wp + m->wp_out[l]; p.M = B; p.N = d.d; p.K = d.D;
+      p.Y = hid; p.ldy = d.d;
+      if (g_next) { p.g2 = g_next; p.xg = w.xg; p.ssq_out = w.ssq_in; }
+      SSM_TRY(ssm::launch_stepproj(ssm::EPI_RESID, p, st)); }
     return SSM_OK;
 }
 
@@ -951,6 +1030,8 @@ ssm_status mixer_step_fused(ssm_model* m, int l, float* hid, int B, float* ssm_s
     hipStream_t st = c->stream;
     const float* W = m->w;
     const float* A = m->Ab + Ly.A;
+    if (Ly.type == SSM_LAYER_MAMBA1)
+        return mixer_step_fused_m1(m, l, hid, B, ssm_st, conv_st, w, g_next);
     float *zx = w.a, *xbc = w.b;
     const int GN = d.G * d.N;
     { Stage g(c, "m2.step.in_proj");

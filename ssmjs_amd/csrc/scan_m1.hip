@@ -23,6 +23,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "glue.hpp"
 
 namespace {
 
@@ -477,7 +478,13 @@ bool single_ok(int B, int D, int Np) {
     }
 }
 
-// One-token update: one thread per (b, d) with the N state entries in registers.
+// One-token update: one thread per (b, d) with the N state entries in registers. ykb > 0:
+// y goes to fragment order with K = D = 16 ykb (the input of the fused step's out_proj).
+// dtr given: the raw dt is dt_proj formed here, sum over r < R of dtr[b, r] Wdt[d, r] (Wdt
+// (D, R) rows 16-byte aligned, R % 4 == 0), and the grid is (D / 64) x ceil(B / 4) workgroups:
+// wave w of workgroup (g, j) takes d = 64 g + lane of sequence b = 4 j + w, so the four waves
+// read the same 64 rows of Wdt (from L2 once, then L1) and each wave's row of dtr is uniform
+// (scalar loads). Otherwise one thread per i = b D + d.
 template <int N>
 __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
                                  const float* __restrict__ dt, long lddt,
@@ -486,48 +493,89 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
                                  long ldb, const float* __restrict__ Cm, long ldc,
                                  const float* __restrict__ Dsk, const float* __restrict__ z,
                                  long ldz, float* __restrict__ y, long ldy,
-                                 float* __restrict__ h, int B, int D, int Nr, int vec) {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)B * D) return;
-    const int b = (int)(i / D), d = (int)(i % D);
-    const float dl = delta_of(dt[(long)b * lddt + d], dt_bias ? dt_bias[d] : 0.f, softplus);
-    const float xx = x[(long)b * ldx + d];
-    const float du = dl * xx;
+                                 float* __restrict__ h, int B, int D, int Nr, int vec, int ykb,
+                                 const float* __restrict__ dtr, long lddtr,
+                                 const float* __restrict__ Wdt, int R) {
+    int b, d;
+    long i;
+    if (dtr) {
+        const int nd = D >> 6;
+        b = 4 * (int)(blockIdx.x / nd) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        d = 64 * (int)(blockIdx.x % nd) + (threadIdx.x & 63);
+        if (b >= B) return;
+        i = (long)b * D + d;
+    } else {
+        i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= (long)B * D) return;
+        b = (int)(i / D);
+        d = (int)(i % D);
+    }
     float* hp = h + i * Nr;
     // per group of up to 16 states: all loads first, then the arithmetic. When the state
     // count is the template's and the rows are 16-byte aligned (vec), h and A come in float4
     // loads; otherwise from clamped (in-bounds) scalar indices. (Loads behind a per-n branch
-    // were each waited for before the next.)
+    // were each waited for before the next.) The first group's loads, x and z are issued
+    // before dt is formed, so that their latency overlaps dt_proj's.
     constexpr int G = N < 16 ? N : 16;
+    struct Grp {
+        float h[G], a[G], b[G], c[G];
+    };
+    auto load_grp = [&](int n0) {
+        Grp g;
+#pragma unroll
+        for (int q = 0; q < G; q += 4) {
+            const float4 h4 = *reinterpret_cast<const float4*>(hp + n0 + q);
+            const float4 a4 = *reinterpret_cast<const float4*>(A + (long)d * N + n0 + q);
+            g.h[q] = h4.x; g.h[q + 1] = h4.y; g.h[q + 2] = h4.z; g.h[q + 3] = h4.w;
+            g.a[q] = a4.x; g.a[q + 1] = a4.y; g.a[q + 2] = a4.z; g.a[q + 3] = a4.w;
+        }
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            g.b[q] = Bm[(long)b * ldb + n0 + q];
+            g.c[q] = Cm[(long)b * ldc + n0 + q];
+        }
+        return g;
+    };
+    const bool vpath = Nr == N && vec;
+    Grp g0;
+    if (vpath) g0 = load_grp(0);
+    const float xx = x[(long)b * ldx + d];
+    const float zz = z ? z[(long)b * ldz + d] : 0.f;
+    float raw;
+    if (dtr) {
+        const float* dr = dtr + (long)b * lddtr;
+        const float* wr = Wdt + (long)d * R;
+        float s = 0.f;
+        for (int r = 0; r < R; r += 4) {
+            const float4 w4 = *reinterpret_cast<const float4*>(wr + r);
+            s = fmaf(dr[r], w4.x, s);
+            s = fmaf(dr[r + 1], w4.y, s);
+            s = fmaf(dr[r + 2], w4.z, s);
+            s = fmaf(dr[r + 3], w4.w, s);
+        }
+        raw = s;
+    } else {
+        raw = dt[(long)b * lddt + d];
+    }
+    const float dl = delta_of(raw, dt_bias ? dt_bias[d] : 0.f, softplus);
+    const float du = dl * xx;
     float acc = 0.f;
-    if (Nr == N && vec) {
+    if (vpath) {
 #pragma unroll
         for (int n0 = 0; n0 < N; n0 += G) {
-            float hv[G], av[G], bv[G], cv[G];
-#pragma unroll
-            for (int q = 0; q < G; q += 4) {
-                const float4 h4 = *reinterpret_cast<const float4*>(hp + n0 + q);
-                const float4 a4 = *reinterpret_cast<const float4*>(A + (long)d * N + n0 + q);
-                hv[q] = h4.x; hv[q + 1] = h4.y; hv[q + 2] = h4.z; hv[q + 3] = h4.w;
-                av[q] = a4.x; av[q + 1] = a4.y; av[q + 2] = a4.z; av[q + 3] = a4.w;
-            }
-#pragma unroll
-            for (int q = 0; q < G; ++q) {
-                bv[q] = Bm[(long)b * ldb + n0 + q];
-                cv[q] = Cm[(long)b * ldc + n0 + q];
-            }
+            const Grp gg = n0 == 0 ? g0 : load_grp(n0);
 #pragma unroll
             for (int q = 0; q < G; q += 4) {
                 float4 v;
-                v.x = fmaf(ssm::ex2(dl * av[q] * ssm::kLog2e), hv[q], du * bv[q]);
-                v.y = fmaf(ssm::ex2(dl * av[q + 1] * ssm::kLog2e), hv[q + 1], du * bv[q + 1]);
-                v.z = fmaf(ssm::ex2(dl * av[q + 2] * ssm::kLog2e), hv[q + 2], du * bv[q + 2]);
-                v.w = fmaf(ssm::ex2(dl * av[q + 3] * ssm::kLog2e), hv[q + 3], du * bv[q + 3]);
+                v.x = fmaf(ssm::ex2(dl * gg.a[q] * ssm::kLog2e), gg.h[q], du * gg.b[q]);
+                v.y = fmaf(ssm::ex2(dl * gg.a[q + 1] * ssm::kLog2e), gg.h[q + 1], du * gg.b[q + 1]);
+                v.z = fmaf(ssm::ex2(dl * gg.a[q + 2] * ssm::kLog2e), gg.h[q + 2], du * gg.b[q + 2]);
+                v.w = fmaf(ssm::ex2(dl * gg.a[q + 3] * ssm::kLog2e), gg.h[q + 3], du * gg.b[q + 3]);
                 *reinterpret_cast<float4*>(hp + n0 + q) = v;
-                acc = fmaf(v.x, cv[q], acc);
-                acc = fmaf(v.y, cv[q + 1], acc);
-                acc = fmaf(v.z, cv[q + 2], acc);
-                acc = fmaf(v.w, cv[q + 3], acc);
+                acc = fmaf(v.x, gg.c[q], acc);
+                acc = fmaf(v.y, gg.c[q + 1], acc);
+                acc = fmaf(v.z, gg.c[q + 2], acc);
+                acc = fmaf(v.w, gg.c[q + 3], acc);
             }
         }
     } else
@@ -553,8 +601,9 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
         }
     }
     if (Dsk) acc = fmaf(Dsk[d], xx, acc);
-    if (z) acc *= ssm::silu_fast(z[(long)b * ldz + d]);
-    y[(long)b * ldy + d] = acc;
+    if (z) acc *= ssm::silu_fast(zz);
+    if (ykb) y[ssm::frag_off(b, d, ykb)] = acc;
+    else y[(long)b * ldy + d] = acc;
 }
 
 }  // namespace
@@ -647,15 +696,28 @@ extern "C" ssm_status ssm_m1_state_update(const float* x, long ldx, const float*
     SSM_REQUIRE(x && dt && A && Bm && Cm && y && h, "ssm_m1_state_update: null input");
     SSM_REQUIRE(B >= 0 && D >= 0 && N >= 1 && N <= 64, "ssm_m1_state_update: need N <= 64");
     if (B == 0 || D == 0) return SSM_OK;
-    const long n = (long)B * D;
-    const unsigned g = (unsigned)ssm::cdiv(n, 256);
     hipStream_t st = (hipStream_t)stream;
+    return ssm::launch_m1_update(x, ldx, dt, lddt, dt_bias, softplus, A, Bm, ldb, Cm, ldc, Dsk,
+                                 z, ldz, y, ldy, 0, h, B, D, N, st, nullptr, 0, nullptr, 0);
+}
+
+namespace ssm {
+
+ssm_status launch_m1_update(const float* x, long ldx, const float* dt, long lddt,
+                            const float* dt_bias, int softplus, const float* A, const float* Bm,
+                            long ldb, const float* Cm, long ldc, const float* Dsk, const float* z,
+                            long ldz, float* y, long ldy, int ykb, float* h, int B, int D, int N,
+                            hipStream_t st, const float* dtr, long lddtr, const float* Wdt,
+                            int R) {
+    const long n = (long)B * D;
+    const unsigned g = dtr ? (unsigned)((D / 64) * ssm::cdiv(B, 4)) : (unsigned)ssm::cdiv(n, 256);
     // float4 access to h and A rows when N is a template size and the rows are aligned
     const int vec = (N == 8 || N == 16 || N == 32 || N == 64) && (uintptr_t)h % 16 == 0 &&
                     (uintptr_t)A % 16 == 0;
 #define M1U(NS)                                                                              \
     m1_update_kernel<NS><<<g, 256, 0, st>>>(x, ldx, dt, lddt, dt_bias, softplus, A, Bm, ldb, \
-                                            Cm, ldc, Dsk, z, ldz, y, ldy, h, B, D, N, vec)
+                                            Cm, ldc, Dsk, z, ldz, y, ldy, h, B, D, N, vec, ykb, \
+                                            dtr, lddtr, Wdt, R)
     if (N <= 8) M1U(8);
     else if (N <= 16) M1U(16);
     else if (N <= 32) M1U(32);
@@ -663,3 +725,17 @@ extern "C" ssm_status ssm_m1_state_update(const float* x, long ldx, const float*
 #undef M1U
     return ssm::check_launch("m1_state_update");
 }
+
+ssm_status launch_m1_update_frag(const float* x, long ldx, const float* dtr, long lddtr,
+                                 const float* Wdt, int R, const float* dt_bias, const float* A,
+                                 const float* Bm, long ldb, const float* Cm, long ldc,
+                                 const float* Dsk, const float* z, long ldz, float* yf, float* h,
+                                 int B, int D, int N, hipStream_t st) {
+    SSM_REQUIRE(x && dtr && Wdt && A && Bm && Cm && yf && h && B >= 1 && D % 64 == 0 &&
+                    N >= 1 && N <= 64 && R >= 4 && R % 4 == 0 && ((uintptr_t)Wdt & 15) == 0,
+                "m1_update_frag: arguments");
+    return launch_m1_update(x, ldx, nullptr, 0, dt_bias, 1, A, Bm, ldb, Cm, ldc, Dsk, z, ldz, yf,
+                            0, D / 16, h, B, D, N, st, dtr, lddtr, Wdt, R);
+}
+
+}  // namespace ssm

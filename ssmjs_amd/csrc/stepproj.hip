@@ -11,6 +11,8 @@
 //   EPI_RESID  Y[m, n] += v (the residual add); then, when g2 is given, the next RMSNorm's
 //              operand xg[m, n] = Y[m, n] * g2[n] (in fragment order, below) and the row's
 //              partial sum of squares over the tile's 16 columns, ssq_out[m, n / 16]
+//   Yf         EPI_CONV: the conv outputs also written in fragment order, the operand of the
+//              step's next projection (the Mamba-1 step's x_proj)
 //
 // The RMSNorms of the step are carried this way: the producer of a row writes x * g and
 // partial sums of x^2 per 16 columns, and the consumer's epilogue applies 1 / rms(x) as the
@@ -151,9 +153,14 @@ __global__ __launch_bounds__(64 * kNW, PD <= 4 ? 8 : 5) void stepproj_kernel(Ste
             *y = a.beta != 0.f ? v + a.beta * *y : v;
         }
     } else if constexpr (EPI == EPI_CONV) {
-        if (!ok) return;
         const int c = en - a.c0;
-        if (c < 0 || c >= a.C) {
+        const bool in_conv = c >= 0 && c < a.C;
+        if (!ok) {
+            // padding rows of the fragment-order copy: zeros for the next projection
+            if (a.Yf && in_conv && en < a.N) a.Yf[frag_off(em, c, a.C >> 4)] = 0.f;
+            return;
+        }
+        if (!in_conv) {
             a.Y[(long)em * a.ldy + en] = v;
             return;
         }
@@ -169,7 +176,9 @@ __global__ __launch_bounds__(64 * kNW, PD <= 4 ? 8 : 5) void stepproj_kernel(Ste
         }
         acc = fmaf(wc[Kc - 1], v, acc);
         if (Kc > 1) s[Kc - 2] = v;
-        a.Yc[(long)em * a.ldyc + c] = silu_fast(acc);
+        const float u = silu_fast(acc);
+        a.Yc[(long)em * a.ldyc + c] = u;
+        if (a.Yf) a.Yf[frag_off(em, c, a.C >> 4)] = u;
     } else {   // EPI_RESID
         float o = 0.f;
         if (ok) {
@@ -260,6 +269,8 @@ ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st) {
                 "stepproj: conv epilogue arguments");
     SSM_REQUIRE(epi != EPI_RESID || !a.g2 || (a.xg && a.ssq_out && a.N % 16 == 0),
                 "stepproj: residual epilogue arguments");
+    SSM_REQUIRE(!a.Yf || (epi == EPI_CONV && a.C % 16 == 0),
+                "stepproj: fragment-order copy arguments");
     a.mt = (a.M + 15) / 16;
     a.nt = (a.N + 15) / 16;
     const unsigned grid = (unsigned)(8L * a.mt * ((a.nt + 7) / 8));

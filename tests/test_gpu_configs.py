@@ -15,6 +15,8 @@ through the C ABI, against the CPU oracle on the same seeded inputs and weights.
         with the gated norm's element-wise part, out_proj with the residual add and the next
         layer's norm operand), the LM head and the device argmax. Eager launches and
         graph-replayed steps are both checked.
+  Mamba-1 decode  the same check through two Mamba-1 layers at cfg2's block dimensions (the
+        reference's default layer type), which take the fused Mamba-1 layer step.
 
 Tolerance, per element (north_star: max rel err <= 1e-4 fp32):
     |gpu - oracle| <= 1e-4 * |oracle| + 1e-5 * max|oracle|
@@ -114,19 +116,15 @@ def _greedy_rows(am, ref_logits):
     return ok, np.argmax(ref_logits, axis=1)
 
 
-def test_cfg4_decode_step(device, monkeypatch):
-    """Decode steps of 64 sequences through cfg4's layer and vocabulary dimensions, from a
-    cached state ~ N(0, 0.1): logits and state per step against the oracle, eager and with
-    the captured step graph replayed (steps 3.. replay it)."""
-    case("cfg4 decode d1024 H32 P64 N128 V32000, 64 sequences, 2 layers")
+def _decode_vs_oracle(device, monkeypatch, cfg, Bsz, steps, seed):
+    """Decode steps of Bsz sequences from a cached state ~ N(0, 0.1): logits and state per step
+    against the oracle, eager and with the captured step graph replayed (steps 3.. replay it)."""
     from ssmjs_amd import backend
-    Bsz, V, steps = 64, 32000, 5
-    cfg = {"vocabSize": V, "dModel": 1024, "numLayers": 2, "dState": 128, "dConv": 4,
-           "expand": 2, "nHeads": 32, "nGroups": 1, "layers": [{"type": "mamba2"}] * 2}
-    m = backend.Model(device, cfg, seed=1004)
+    V = cfg["vocabSize"]
+    m = backend.Model(device, cfg, seed=seed)
     blob = m.export_weights()
     om = O.Model(blob)
-    r = np.random.default_rng(1004)
+    r = np.random.default_rng(seed)
     st0 = m.new_state(Bsz)
     img = (0.1 * r.standard_normal(st0.read().size)).astype(np.float32)
     st0.destroy()
@@ -155,3 +153,25 @@ def test_cfg4_decode_step(device, monkeypatch):
         assert n_exact >= 0.95 * steps * Bsz
         st.destroy()
     m.destroy()
+
+
+def test_cfg4_decode_step(device, monkeypatch):
+    """Decode steps of 64 sequences through cfg4's layer and vocabulary dimensions (the fused
+    Mamba-2 layer step)."""
+    case("cfg4 decode d1024 H32 P64 N128 V32000, 64 sequences, 2 layers")
+    cfg = {"vocabSize": 32000, "dModel": 1024, "numLayers": 2, "dState": 128, "dConv": 4,
+           "expand": 2, "nHeads": 32, "nGroups": 1, "layers": [{"type": "mamba2"}] * 2}
+    _decode_vs_oracle(device, monkeypatch, cfg, 64, 5, 1004)
+
+
+@pytest.mark.parametrize("Bsz", [64, 5])
+def test_mamba1_decode_step(device, monkeypatch, Bsz):
+    """Decode steps through Mamba-1 layers at cfg2's block dimensions (d_model 768, d_inner
+    1536, d_state 16, dt_rank 48, conv 4): the fused Mamba-1 layer step (in_proj with the
+    RMSNorm scale and the conv update in its epilogue, x_proj, dt_proj, the state update,
+    out_proj with the residual add and the next layer's norm operand). Bsz = 5 leaves most of
+    the last 16-row tile as padding."""
+    case(f"Mamba-1 decode d768 D1536 N16 R48 V8192, {Bsz} sequences, 2 layers")
+    cfg = {"vocabSize": 8192, "dModel": 768, "numLayers": 2, "dState": 16, "dConv": 4,
+           "expand": 2, "nHeads": 12, "dtRank": 48, "layers": [{"type": "mamba1"}] * 2}
+    _decode_vs_oracle(device, monkeypatch, cfg, Bsz, 5, 1005)

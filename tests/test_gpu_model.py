@@ -59,11 +59,13 @@ def test_hf_fixture_logits(device, golden, kind):
     m.destroy()
 
 
-def _model(device, layers, d=128, N=16, H=4, V=512, seed=7, emb_scale=40.0):
+def _model(device, layers, d=128, N=16, H=4, V=512, seed=7, emb_scale=40.0, dt_rank=None):
     """Random-init GPU model; embedding scaled up for wide greedy margins. Returns (model, blob)."""
     from ssmjs_amd import backend, checkpoint
     cfg = {"vocabSize": V, "dModel": d, "numLayers": len(layers), "dState": N, "dConv": 4,
            "expand": 2, "nHeads": H, "nGroups": 1, "layers": [{"type": t} for t in layers]}
+    if dt_rank is not None:
+        cfg["dtRank"] = dt_rank
     m = backend.Model(device, cfg, seed=seed)
     dims, T = checkpoint.unpack(m.export_weights())
     T["embedding"] = T["embedding"] * emb_scale
@@ -87,14 +89,18 @@ def test_forward_matches_oracle(device, layers, N, H):
     m.destroy()
 
 
-@pytest.mark.parametrize("layers,N,H", [(["mamba1", "mamba1"], 16, 4),
-                                        (["mamba2", "mamba2"], 128, 4),
-                                        (["mamba2", "mamba2"], 128, 32)])
-def test_prefill_decode_state_matches_oracle(device, layers, N, H):
+@pytest.mark.parametrize("layers,N,H,R", [(["mamba1", "mamba1"], 16, 4, None),
+                                          (["mamba1", "mamba1"], 16, 4, 6),
+                                          (["mamba2", "mamba2"], 128, 4, None),
+                                          (["mamba2", "mamba2"], 128, 32, None),
+                                          (["mamba1", "mamba2", "mamba1"], 64, 4, None)])
+def test_prefill_decode_state_matches_oracle(device, layers, N, H, R):
     """H = 32 gives head dim 8, less than one workgroup's block of state rows in the one-token
-    update (the guarded variant of the fused step's state update)."""
-    case(f"prefill/decode state {layers} N={N} H={H}")
-    m, blob = _model(device, layers, N=N, H=H)
+    update (the guarded variant of the fused step's state update). The Mamba-1 layers take
+    the fused one-token step except with dt_rank 6 (not a multiple of 4: the separate
+    launches); the mixed stack hands the next layer's norm operand across layer types."""
+    case(f"prefill/decode state {layers} N={N} H={H} dt_rank={R}")
+    m, blob = _model(device, layers, N=N, H=H, dt_rank=R)
     om = O.Model(blob)
     ids = np.random.default_rng(2).integers(0, 512, (3, 40)).astype(np.uint32)
     st = m.new_state(3)
