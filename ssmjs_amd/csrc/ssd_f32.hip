@@ -84,6 +84,7 @@ struct SmemF32 {
     float ac[2][QF];    // acum_t in log2 units
     float dv[2][QF];    // dt'_t
     float wj[2][QF];    // w_t = 2^(acum_end - acum_t) dt'_t
+    float ae[2];        // acum_end
     float sq[GATED ? 2 : 1][GATED ? 4 : 1][GATED ? QF : 1];   // per-wave sums of u^2 per row
 };
 
@@ -119,6 +120,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     constexpr int NB = NN / 16;          // n blocks (state tiles per wave, k groups of C B^T)
     constexpr int QB = QF / 16;          // time blocks per chunk
     constexpr int NCB = QB * (QB + 1) / 2;   // causal C B^T tiles per chunk
+    static_assert(NCB == 3, "three tiles over four waves: one wave per chunk has no tile");
     constexpr int RL = NN / 4;           // lanes per staged B / C row (one float4 each)
     constexpr int RPP = 256 / RL;        // rows per staging pass
     constexpr int SP = QF / RPP;         // staging passes
@@ -176,10 +178,12 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         float4 c[FULL ? SP : 1];
         float dt;
     } raw;
-    auto load_raw = [&](int c) {
+    // x, B, C of chunk c and dt of chunk cd (the full pass reads dt one chunk further ahead:
+    // its scan runs a chunk early, below)
+    auto load_raw = [&](int c, int cd) {
         const int qv = rows_of(c);
         const long r0 = (long)c * QF;
-        const auto rd = rsrc(d0 + r0 * a.lddt, span(qv, a.lddt, 1));
+        const auto rd = rsrc(d0 + (long)cd * QF * a.lddt, span(rows_of(cd), a.lddt, 1));
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, 16));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN));
         raw.dt = bload4(rd, (unsigned)(lane * a.lddt) * 4u);
@@ -220,8 +224,34 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     // C B^T tiles rotate over the waves from one workgroup to the next, so that no SIMD always
     // gets the wave with the most (or no) tiles
     const int rot = blockIdx.x & 3;
+    // dt' of chunk cc (0 past the segment), its running sum times A_h and the weights w_t into
+    // LDS buffer bf (lane = time step)
+    auto scan_put = [&](int cc, float raw_dt, int bf) {
+        const int qv = rows_of(cc);
+        float dv = raw_dt + dtb;
+        if (a.softplus) dv = ssm::softplus_fast(dv);
+        dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
+        const float sc = wave_prefix_sum(dv * Ah);
+        const float ae = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), QF - 1));
+        if (lane < QF) {
+            sm.ac[bf][lane] = sc;
+            sm.dv[bf][lane] = dv;
+            sm.wj[bf][lane] = ssm::ex2(ae - sc) * dv;
+        }
+        if (lane == 0) sm.ae[bf] = ae;
+    };
 
-    load_raw(c_begin);
+    if constexpr (FULL) {
+        // the first chunk's scan (the loop's wave without a C B^T tile scans the next chunk
+        // while the others form their tiles); dt of the second chunk comes with the inputs
+        const int qv0 = rows_of(c_begin);
+        const auto rd0 = rsrc(d0 + (long)c_begin * QF * a.lddt, span(qv0, a.lddt, 1));
+        if (w == 0) scan_put(c_begin, bload4(rd0, (unsigned)(lane * a.lddt) * 4u), c_begin & 1);
+        load_raw(c_begin, c_begin + 1);
+    } else {
+        load_raw(c_begin, c_begin);
+    }
     if constexpr (FULL) {
         // Stores into an empty range (dropped by the range check) make the memory operations
         // in flight at loop entry match the back edge (the prefetch, then the chunk's y
@@ -235,18 +265,22 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         const int qv = min(QF, a.L - c * QF);
         const long row0 = brow + (long)c * QF;
 
-        // ---- dt' and its running sum times A_h (every wave; lane = time step)
-        float dv = raw.dt + dtb;
-        if (a.softplus) dv = ssm::softplus_fast(dv);
-        dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
-        const float sc = wave_prefix_sum(dv * Ah);
-        const float acend = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), QF - 1));
-        decay_sum += acend;
-        if (w == 0 && lane < QF) {
-            sm.ac[buf][lane] = sc;
-            sm.dv[buf][lane] = dv;
-            sm.wj[buf][lane] = ssm::ex2(acend - sc) * dv;
+        // ---- dt' and its running sum times A_h (state-only pass: every wave, lane = time
+        // step; the full pass formed them a chunk earlier)
+        float acend = 0.f;
+        if constexpr (!FULL) {
+            float dv = raw.dt + dtb;
+            if (a.softplus) dv = ssm::softplus_fast(dv);
+            dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
+            const float sc = wave_prefix_sum(dv * Ah);
+            acend = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), QF - 1));
+            decay_sum += acend;
+            if (w == 0 && lane < QF) {
+                sm.ac[buf][lane] = sc;
+                sm.dv[buf][lane] = dv;
+                sm.wj[buf][lane] = ssm::ex2(acend - sc) * dv;
+            }
         }
         // ---- stage B (and C) rows
 #pragma unroll
@@ -260,7 +294,10 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) xv[jb][s] = raw.x[jb][s];
         __syncthreads();
-        load_raw(c + 1);   // past the segment: an empty range, the loads return zeros
+        // past the segment: an empty range, the loads return zeros
+        const float dnext = raw.dt;   // full pass: dt of chunk c + 1
+        if constexpr (FULL) load_raw(c + 1, c + 2);
+        else load_raw(c + 1, c + 1);
         if constexpr (GATED) {
             // the previous chunk's row sums of u^2, added over the four waves in order
             if (c > c_begin && tid < QF) flush_ssq(c - 1, buf ^ 1);
@@ -268,6 +305,9 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 
         if constexpr (FULL) {
             // ---- M^T tiles of C B^T (this wave's share of the causal tiles)
+            // the wave without a tile scans chunk c + 1 into the other buffers (the last reads
+            // of those, chunk c - 1's, came before barrier 1)
+            if (((NCB + rot) & 3) == w) scan_put(c + 1, dnext, buf ^ 1);
 #pragma unroll
             for (int t = 0; t < NCB; ++t) {
                 if (((t + rot) & 3) != w) continue;
@@ -388,6 +428,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 
         // ---- state: S^T = 2^acum_end S^T + sum_j B[j][n] (X[j][p] w_j)
         {
+            if constexpr (FULL) acend = sm.ae[buf];
             const float e = ssm::ex2(acend);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) S[nb] *= e;
