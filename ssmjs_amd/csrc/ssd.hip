@@ -94,8 +94,11 @@ struct Smem {
     alignas(16) __bf16 c[CST ? Q : 1][BP];             // C   (i, n)
     alignas(16) __bf16 x[HPW][FULL ? Q : 1][XP];       // X   (j, p)
     alignas(16) __bf16 s[HPW][FULL ? NN : 1][XP];      // state^T (n, p)
-    alignas(16) float dv[HPW][Q];   // dt'_j
-    alignas(16) float ac[HPW][Q];   // acum_j log2(e)
+    // two chunks' worth (the full pass scans a chunk ahead)
+    alignas(16) float dv[2][HPW][Q];   // dt'_j
+    alignas(16) float ac[2][HPW][Q];   // acum_j log2(e)
+    alignas(16) float wj[2][HPW][Q];   // w_j = exp(acum_end - acum_j) dt'_j
+    float ae[2][HPW];                  // acum_end
 };
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -261,10 +264,12 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
 
     RW raw;
     using v8 = typename RW::v8;
-    auto load_raw = [&](int c) {
+    // x, B (, C) of chunk c and dt of chunk cd (the full pass reads dt one chunk further
+    // ahead: its scan runs a chunk early, below)
+    auto load_raw = [&](int c, int cd) {
         const int qv = rows_of(c);
         const long r0 = (long)c * Q;
-        const auto rd = rsrc(d0 + r0 * a.lddt, span(qv, a.lddt, 1, 4));
+        const auto rd = rsrc(d0 + (long)cd * Q * a.lddt, span(rows_of(cd), a.lddt, 1, 4));
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         raw.dt = bload4(rd, od);
@@ -326,7 +331,35 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         }
     };
     if (FULL && state_live) write_state_lds();
-    load_raw(c_begin);
+    // dt' of chunk cc (0 past the segment), acum in log2 units, the weights w_j and acum_end of
+    // the wave's head into LDS buffer bf (lane = time step)
+    auto scan_put = [&](int cc, float raw_dt, int bf) {
+        const int qv = rows_of(cc);
+        float dv = raw_dt + dtb;
+        if (a.softplus) dv = ssm::softplus_fast(dv);
+        dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
+        const float sc = wave_prefix_sum(dv * Ah);
+        const float ae = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
+        // decay weight exp(acum_i - acum_j) dt'_j = exp2(ac_i - ac_j) dt'_j: dt' keeps its
+        // sign (softplus off with no lower clamp allows dt' < 0)
+        sm.dv[bf][hw][lane] = dv;
+        sm.ac[bf][hw][lane] = sc * ssm::kLog2e;
+        sm.wj[bf][hw][lane] = ssm::ex2((ae - sc) * ssm::kLog2e) * dv;
+        if (lane == 0) sm.ae[bf][hw] = ae;
+    };
+    if constexpr (FULL) {
+        // the first chunk's scan (in the loop, each head's wave with the lightest Y_diag scans
+        // the next chunk while the others work); dt of the second chunk comes with the inputs
+        if (wl == 0) {
+            const auto rd0 = rsrc(d0 + (long)c_begin * Q * a.lddt, span(rows_of(c_begin), a.lddt, 1, 4));
+            scan_put(c_begin, bload4(rd0, od), c_begin & 1);
+        }
+        __syncthreads();
+        load_raw(c_begin, c_begin + 1);
+    } else {
+        load_raw(c_begin, c_begin);
+    }
     load_c(c_begin);
     if constexpr (FULL) {
         // Four stores into an empty range (dropped by the range check) make the memory
@@ -342,31 +375,31 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         const int qv = min(Q, a.L - t0);
         const long row0 = (long)b * a.L + t0;
 
-        // ---- dt' and the inclusive prefix of dt' * A (every wave; lane = time step)
-        float dv = raw.dt + dtb;
-        if (a.softplus) dv = ssm::softplus_fast(dv);
-        dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
-        const float av = dv * Ah;
-        const float sc = wave_prefix_sum(av);
-        const float acend = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
-        decay_sum += acend;
-        if (wl == 0) {
-            // decay weight exp(acum_i - acum_j) dt'_j = exp2(ac_i - ac_j) dt'_j: dt' keeps its
-            // sign (softplus off with no lower clamp allows dt' < 0)
-            const float sl = sc * ssm::kLog2e;
-            sm.dv[hw][lane] = dv;
-            sm.ac[hw][lane] = sl;
+        const int buf = c & 1;
+        // ---- dt' and the inclusive prefix of dt' * A (state-only pass: every wave, lane =
+        // time step; the full pass formed them a chunk earlier)
+        float acend, wl_ = 0.f;
+        if constexpr (FULL) {
+            acend = sm.ae[buf][hw];
+        } else {
+            float dv = raw.dt + dtb;
+            if (a.softplus) dv = ssm::softplus_fast(dv);
+            dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
+            const float sc = wave_prefix_sum(dv * Ah);
+            acend = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
+            decay_sum += acend;
+            wl_ = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
         }
-        const float wl_ = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
 
         // ---- stage X and X w (rows of the X prefetch; w_j comes from lane j of this wave)
 #pragma unroll
         for (int k = 0; k < RW::XK; ++k) {
             constexpr int E = RW::XE;
             const int j = 16 * wl + RW::XR * k + xr;
-            const float wj = __builtin_bit_cast(
-                float, __builtin_amdgcn_ds_bpermute(4 * j, __builtin_bit_cast(int, wl_)));
+            const float wj = FULL ? sm.wj[buf][hw][j]
+                                  : __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                  4 * j, __builtin_bit_cast(int, wl_)));
             bf16x8 wh;
 #pragma unroll
             for (int e = 0; e < E; ++e) wh[e] = hi_of((float)raw.x[k][e] * wj);
@@ -397,7 +430,9 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
 
         // ---- the next chunk's raw inputs are in flight while this one computes (a chunk past
         // the segment has an empty range: the loads return zeros without touching memory)
-        load_raw(c + 1);
+        const float dnext = raw.dt;   // full pass: dt of chunk c + 1
+        if constexpr (FULL) load_raw(c + 1, c + 2);
+        else load_raw(c + 1, c + 1);
 
         if constexpr (FULL) {
             if constexpr (CST) {
@@ -405,7 +440,7 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
                 for (int ks = 0; ks < KS; ++ks)
                     cfh[ks] = *reinterpret_cast<const bf16x8*>(&sm.c[ic][32 * ks + 8 * q4]);
             }
-            const float aci = sm.ac[hw][ic];
+            const float aci = sm.ac[buf][hw][ic];
             floatx4 Y[P / 16];
 #pragma unroll
             for (int pb = 0; pb < P / 16; ++pb) Y[pb] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -456,8 +491,8 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
                         for (int r = 0; r < 4; ++r) sv[jb][r] = 0.f;
                         continue;
                     }
-                    const float4 aj = *reinterpret_cast<const float4*>(&sm.ac[hw][16 * jb + 4 * q4]);
-                    const float4 dj = *reinterpret_cast<const float4*>(&sm.dv[hw][16 * jb + 4 * q4]);
+                    const float4 aj = *reinterpret_cast<const float4*>(&sm.ac[buf][hw][16 * jb + 4 * q4]);
+                    const float4 dj = *reinterpret_cast<const float4*>(&sm.dv[buf][hw][16 * jb + 4 * q4]);
                     const float ajr[4] = {aj.x, aj.y, aj.z, aj.w};
                     const float djr[4] = {dj.x, dj.y, dj.z, dj.w};
 #pragma unroll
@@ -494,6 +529,9 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
                 case 2: y_diag(std::integral_constant<int, 2>{}); break;
                 default: y_diag(std::integral_constant<int, 3>{}); break;
             }
+            // the lightest wave scans chunk c + 1 into the other buffers (the last reads of
+            // those, chunk c - 1's, came before this chunk's first barrier)
+            if (wl == 0) scan_put(c + 1, dnext, buf ^ 1);
 
             // ---- the next chunk's C fragments (the last use of this chunk's was Y_diag)
             load_c(c + 1);
