@@ -294,10 +294,10 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) xv[jb][s] = raw.x[jb][s];
         __syncthreads();
-        // past the segment: an empty range, the loads return zeros
+        // past the segment: an empty range, the loads return zeros. The full pass issues the
+        // next chunk's loads after its second barrier, so that the C B^T tiles start at once.
         const float dnext = raw.dt;   // full pass: dt of chunk c + 1
-        if constexpr (FULL) load_raw(c + 1, c + 2);
-        else load_raw(c + 1, c + 1);
+        if constexpr (!FULL) load_raw(c + 1, c + 1);
         if constexpr (GATED) {
             // the previous chunk's row sums of u^2, added over the four waves in order
             if (c > c_begin && tid < QF) flush_ssq(c - 1, buf ^ 1);
@@ -359,6 +359,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
                 *reinterpret_cast<float4*>(&sm.m[i][16 * jb + 4 * q4]) = make_float4(mv[0], mv[1], mv[2], mv[3]);
             }
             __syncthreads();   // M^T visible
+            load_raw(c + 1, c + 2);
 
             // ---- Y^T[p][i] for the wave's 16 p and the chunk's QF rows i
             floatx4 Y[QB];
