@@ -1,9 +1,13 @@
 """GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
 
-Tolerances (max |gpu - oracle| / max(1, max |oracle|)):
-  fp32 kernels            1e-4   (north_star: max rel err <= 1e-4 fp32)
-  SSD with bf16 inputs    2e-2   (north_star: <= 2e-2 for the bf16 SSD variant); the oracle
-                                  gets the same bf16-rounded inputs as float32.
+Tolerances:
+  fp32 kernels            per element, |gpu - oracle| <= 1e-4 |oracle| + 1e-5 max|oracle|
+                          (north_star: max rel err <= 1e-4 fp32; the floor holds elements near
+                          zero to the fp32 rounding of a K-term sum, about 2^-24 sqrt(K) of the
+                          tensor's scale); the fp32 SSD at config 3's dims with a 1e-6 floor
+  SSD with bf16 inputs    max |gpu - oracle| / max(1, max |oracle|) <= 2e-2 (north_star:
+                          <= 2e-2 for the bf16 SSD variant); the oracle gets the same
+                          bf16-rounded inputs as float32.
 """
 import sys
 
@@ -16,6 +20,7 @@ from oracle import oracle as O  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 F32_TOL = 1e-4
+F32_FLOOR = 1e-5   # per-element floor, as a fraction of the tensor's largest magnitude
 BF16_TOL = 2e-2
 
 
@@ -75,8 +80,8 @@ def test_conv1d_matches_oracle(B, L, C, Kw, strided, with_state):
     sd = dev(st) if with_state else None
     sout = dev(np.zeros((B, C, Kw - 1), np.float32))
     y = K().causal_conv1d(xd[:, :, :C], dev(w), dev(b), True, sd, sout)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(sout), ref_st) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(sout), ref_st, "conv state", atol_frac=F32_FLOOR)
 
 
 def test_conv1d_state_in_place():
@@ -89,8 +94,8 @@ def test_conv1d_state_in_place():
     ref, ref_st = O.causal_conv1d(x, w, None, state_in=st, return_state=True)
     sd = dev(st)
     y = K().causal_conv1d(dev(x), dev(w), None, True, sd, sd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(sd), ref_st) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(sd), ref_st, "conv state", atol_frac=F32_FLOOR)
 
 
 def test_conv1d_update_matches_oracle():
@@ -104,8 +109,8 @@ def test_conv1d_update_matches_oracle():
     ref, ref_st = O.conv_update(x, w, b, st)
     sd = dev(st)
     y = K().conv1d_update(dev(x), dev(w), dev(b), sd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(sd), ref_st) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(sd), ref_st, "conv state", atol_frac=F32_FLOOR)
 
 
 # ------------------------------------------------------------------------- Mamba-1 scan
@@ -133,8 +138,8 @@ def test_scan_config1():
     hd = torch.zeros(1, 512, 16, device="cuda")
     y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), None, True,
                            None, hd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), hT) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), hT, "final state", atol_frac=F32_FLOOR)
 
 
 @pytest.mark.parametrize("B,L,D,N,h0", [(2, 300, 100, 8, True), (3, 1, 64, 16, True),
@@ -150,8 +155,8 @@ def test_scan_shapes(B, L, D, N, h0):
     hd = torch.zeros(B, D, N, device="cuda")
     y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), dev(db),
                            True, dev(h0a) if h0 else None, hd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), hT) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), hT, "final state", atol_frac=F32_FLOOR)
 
 
 @pytest.mark.parametrize("B,L,D,N,h0,full", [
@@ -181,8 +186,8 @@ def test_scan_single_pass(B, L, D, N, h0, full):
     y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk) if full else None,
                            dev(zz) if full else None, dev(db) if full else None, full,
                            dev(h0a) if h0 else None, hd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), hT) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), hT, "final state", atol_frac=F32_FLOOR)
 
 
 def _lib_scan_ws(B, L, D, N):
@@ -202,7 +207,7 @@ def test_scan_strided_views():
     dd, xzd = dev(dbl), dev(xz)
     y = K().selective_scan(xzd[:, :, :D], dev(dt), dev(A), dd[:, :, R:R + N], dd[:, :, R + N:],
                            None, xzd[:, :, D:])
-    assert err(host(y), ref) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
 
 
 def test_m1_state_update():
@@ -217,8 +222,8 @@ def test_m1_state_update():
     ref, href = O.m1_state_update(x, dt, A, Bm, Cm, Dk, z, db, h0)
     hd = dev(h0)
     y = K().m1_state_update(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), dev(db), hd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), href) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), href, "final state", atol_frac=F32_FLOOR)
 
 
 # ------------------------------------------------------------------------- Mamba-2 SSD
@@ -261,11 +266,8 @@ def test_ssd_matches_oracle(B, L, H, G, N, h0, dtype):
     hd = torch.zeros(B, H, P, N, device="cuda")
     y = K().ssd_chunk_scan(dev(x, tdt), dev(dt), dev(A), dev(Bm, tdt), dev(Cm, tdt), dev(Dk),
                            dev(db), True, h0=dev(h0a) if h0 else None, hT=hd)
-    tol = F32_TOL if dtype == "f32" else BF16_TOL
-    e1, e2 = err(host(y), ref), err(host(hd), hT)
-    print(f"  y err {e1:.2e}  state err {e2:.2e}")
-    assert e1 <= tol
-    assert e2 <= tol
+    check_dtype(host(y), ref, "y", dtype)
+    check_dtype(host(hd), hT, "final state", dtype)
 
 
 def check_elementwise(got, ref, what, rtol=1e-4, atol_frac=1e-6):
@@ -277,6 +279,16 @@ def check_elementwise(got, ref, what, rtol=1e-4, atol_frac=1e-6):
     print(f"  {what}: worst |err|/bound {ratio:.3f}, "
           f"max|err|/max|ref| {float(np.abs(got - ref).max()) / scale:.2e}", flush=True)
     assert ratio <= 1.0, f"{what}: beyond {rtol} |ref| + {atol_frac} max|ref|"
+
+
+def check_dtype(got, ref, what, dtype):
+    """fp32: per element (check_elementwise with the fp32 floor); bf16 inputs: normwise 2e-2."""
+    if dtype == "f32":
+        check_elementwise(got, ref, what, atol_frac=F32_FLOOR)
+    else:
+        e = err(got, ref)
+        print(f"  {what}: err {e:.2e}", flush=True)
+        assert e <= BF16_TOL, f"{what}: {e:.2e} beyond {BF16_TOL}"
 
 
 @pytest.mark.parametrize("B,L,H,h0", [(2, 1000, 8, True), (1, 4096, 4, False)])
@@ -321,9 +333,8 @@ def test_ssd_negative_dt_without_softplus(dtype):
                            None, False, dt_min=-float("inf"), hT=hd)
     yh = host(y)
     assert np.isfinite(yh).all()
-    tol = F32_TOL if dtype == "f32" else BF16_TOL
-    assert err(yh, ref) <= tol
-    assert err(host(hd), hT) <= tol
+    check_dtype(yh, ref, "y", dtype)
+    check_dtype(host(hd), hT, "final state", dtype)
 
 
 @pytest.mark.parametrize("H,L", [(2, 64 * 40 + 17), (32, 64 * 48 + 5), (64, 64 * 24)])
@@ -347,10 +358,8 @@ def test_ssd_long_sequence_segments(dtype, H, L):
     hd = torch.zeros(B, H, P, N, device="cuda")
     y = K().ssd_chunk_scan(dev(x, tdt), dev(dt), dev(A), dev(Bm, tdt), dev(Cm, tdt), dev(Dk),
                            None, True, h0=dev(h0a), hT=hd)
-    tol = F32_TOL if dtype == "f32" else BF16_TOL
-    e1, e2 = err(host(y), ref), err(host(hd), hT)
-    print(f"  y err {e1:.2e}  state err {e2:.2e}")
-    assert e1 <= tol and e2 <= tol
+    check_dtype(host(y), ref, "y", dtype)
+    check_dtype(host(hd), hT, "final state", dtype)
 
 
 @pytest.mark.parametrize("B,L,H,G,N,P,path", [
@@ -377,8 +386,8 @@ def test_ssd_fallback_shapes(B, L, H, G, N, P, path):
     ws = torch.empty(1, dtype=torch.uint8, device="cuda") if path == "sequential" else None
     y = K().ssd_chunk_scan(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), None, True,
                            dt_min=lim[0], dt_max=lim[1], h0=dev(h0a), hT=hd, workspace=ws)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), hT) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), hT, "final state", atol_frac=F32_FLOOR)
 
 
 @pytest.mark.parametrize("P,N", [(64, 128), (16, 16), (128, 16)])
@@ -419,8 +428,8 @@ def test_ssd_chunk_equals_decode_steps():
         ys.append(K().m2_state_update(dev(x[:, t]), dev(dt[:, t]), dev(A), dev(Bm[:, t]),
                                       dev(Cm[:, t]), dev(Dk), None, hs))
     ys = torch.stack(ys, 1)
-    assert err(host(ys), host(yp)) <= F32_TOL
-    assert err(host(hs), host(hd)) <= F32_TOL
+    check_elementwise(host(ys), host(yp), "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hs), host(hd), "final state", atol_frac=F32_FLOOR)
 
 
 @pytest.mark.parametrize("P", [64, 40])
@@ -439,8 +448,8 @@ def test_m2_state_update(P):
     ref, href = O.m2_state_update(x, dt, A, Bm, Cm, Dk, db, h0, z=z)
     hd = dev(h0)
     y = K().m2_state_update(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(db), hd, z=dev(z))
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), href) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), href, "final state", atol_frac=F32_FLOOR)
 
 
 # ------------------------------------------------------------------------- norms
@@ -450,10 +459,10 @@ def test_rmsnorm_and_gated():
     r = rng(14)
     x, z = r.standard_normal((7, 300)).astype(np.float32), r.standard_normal((7, 300)).astype(np.float32)
     w = r.uniform(0.5, 1.5, 300).astype(np.float32)
-    assert err(host(K().rmsnorm(dev(x), dev(w))), O.rmsnorm(x, w)) <= F32_TOL
+    check_elementwise(host(K().rmsnorm(dev(x), dev(w))), O.rmsnorm(x, w), "rmsnorm", atol_frac=F32_FLOOR)
     for g in (1, 3):
         ref = O.gated_rmsnorm(x, z, w, groups=g)
-        assert err(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=g)), ref) <= F32_TOL
+        check_elementwise(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=g)), ref, "gated rmsnorm", atol_frac=F32_FLOOR)
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
@@ -489,7 +498,7 @@ def test_linear_rows(mode, M, N, Kd, strided):
             K().linear_rows(xd, Wd, mode, g=gd, z=zd if mode == 2 else None, out=out, beta=beta,
                             workspace=wsp)
             outs.append(host(out))
-            assert err(outs[-1], ref + beta * y0) <= F32_TOL
+            check_elementwise(outs[-1], ref + beta * y0, "y", atol_frac=F32_FLOOR)
         assert np.array_equal(outs[1], outs[2])
 
 
@@ -667,5 +676,5 @@ def test_m2_state_update_decode_shape():
     ref, href = O.m2_state_update(x, dt, A, Bm, Cm, Dk, db, h0)
     hd = dev(h0)
     y = K().m2_state_update(dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(db), hd)
-    assert err(host(y), ref) <= F32_TOL
-    assert err(host(hd), href) <= F32_TOL
+    check_elementwise(host(y), ref, "y", atol_frac=F32_FLOOR)
+    check_elementwise(host(hd), href, "final state", atol_frac=F32_FLOOR)
