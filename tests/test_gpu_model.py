@@ -1,7 +1,8 @@
 """GPU parity of the model-level C ABI (forward / prefill / decode / greedy generate) against
 the CPU oracle and the HF golden fixtures, plus its error contract.
 
-Greedy ids are compared bit-exactly. The models used for greedy runs scale the embedding so
+Logits and states are compared per element (1e-4 relative plus a floor of 1e-5 of the
+tensor's largest magnitude). Greedy ids are compared bit-exactly. The models used for greedy runs scale the embedding so
 that the oracle's top-1/top-2 logit margin stays far above the fp32 summation-order noise;
 each test asserts that minimum margin, so a pass is not luck on near-ties.
 """
@@ -14,7 +15,10 @@ torch = pytest.importorskip("torch")
 from oracle import oracle as O  # noqa: E402
 
 pytestmark = pytest.mark.gpu
-F32_TOL = 2e-4
+# per element: |gpu - oracle| <= RTOL |oracle| + ATOL_FRAC max|oracle| (north_star: max rel
+# err <= 1e-4 fp32; the floor is the fp32 rounding of the model's K-term sums)
+RTOL = 1e-4
+ATOL_FRAC = 1e-5
 
 
 @pytest.fixture(scope="module")
@@ -32,9 +36,14 @@ def case(msg):
     sys.stdout.flush()
 
 
-def err(a, b):
-    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
-    return float(np.abs(a - b).max()) / max(1.0, float(np.abs(b).max()))
+def close(got, ref, what):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
+    assert np.isfinite(got).all(), f"{what}: non-finite values"
+    scale = float(np.abs(ref).max())
+    ratio = float((np.abs(got - ref) / (RTOL * np.abs(ref) + ATOL_FRAC * scale)).max())
+    print(f"  {what}: worst |err|/bound {ratio:.3f}", flush=True)
+    assert ratio <= 1.0, f"{what}: beyond {RTOL} |ref| + {ATOL_FRAC} max|ref|"
 
 
 def cfg_of(dims):
@@ -54,8 +63,8 @@ def test_hf_fixture_logits(device, golden, kind):
     m = backend.Model(device, cfg_of(dims))
     m.load_weights(blob)
     out = m.forward(g["ids"])
-    assert err(out, g["logits"]) <= F32_TOL
-    assert err(out, O.Model(blob).forward(g["ids"])) <= F32_TOL
+    close(out, g["logits"], "logits")
+    close(out, O.Model(blob).forward(g["ids"]), "logits")
     m.destroy()
 
 
@@ -83,9 +92,7 @@ def test_forward_matches_oracle(device, layers, N, H):
     ids = np.random.default_rng(1).integers(0, 512, (2, 150)).astype(np.uint32)
     out = m.forward(ids)
     ref = O.Model(blob).forward(ids)
-    e = err(out, ref)
-    print(f"  logits err {e:.2e}")
-    assert e <= F32_TOL
+    close(out, ref, "logits")
     m.destroy()
 
 
@@ -106,12 +113,12 @@ def test_prefill_decode_state_matches_oracle(device, layers, N, H, R):
     st = m.new_state(3)
     ost = om.new_state(3)
     lg, _ = st.prefill(ids[:, :33])
-    assert err(lg, ost.prefill(ids[:, :33])) <= F32_TOL
-    assert err(st.read(), ost.read()) <= F32_TOL
+    close(lg, ost.prefill(ids[:, :33]), "logits")
+    close(st.read(), ost.read(), "state")
     for t in range(33, 40):
         lg, _ = st.decode(ids[:, t])
-        assert err(lg, ost.decode(ids[:, t])) <= F32_TOL
-    assert err(st.read(), ost.read()) <= F32_TOL
+        close(lg, ost.decode(ids[:, t]), "logits")
+    close(st.read(), ost.read(), "state")
     st.destroy()
     m.destroy()
 
