@@ -269,7 +269,10 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
     auto load_raw = [&](int c, int cd) {
         const int qv = rows_of(c);
         const long r0 = (long)c * Q;
-        const auto rd = rsrc(d0 + (long)cd * Q * a.lddt, span(rows_of(cd), a.lddt, 1, 4));
+        // dt: one strided 4-byte value per step (a cache line per lane); in the full pass only
+        // the wave that scans fetches it, the others get an empty descriptor (no traffic)
+        const auto rd = rsrc(d0 + (long)cd * Q * a.lddt,
+                             (FULL && wl != 0) ? 0u : span(rows_of(cd), a.lddt, 1, 4));
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         raw.dt = bload4(rd, od);
@@ -593,6 +596,163 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
     }
 }
 
+// State-only pass of the segmented mode (long sequences with few batch x heads): a workgroup
+// reads x, B and dt of one (batch, segment, head) once and returns the segment's local final
+// state (from a zero state) and its total decay sum(dt' A). Per chunk: wave 0 scans the next
+// chunk's dt (dt', its prefix sum of dt' A, w_j = exp(acum_end - acum_j) dt'_j) into LDS; every
+// wave stages X w and B into LDS; one barrier; then S = exp(acum_end) S + (X w)^T B (wave w:
+// state rows p = 16w .. 16w + 15). dt is one strided 4-byte value per step, a cache line per
+// lane, so only wave 0 fetches it (the others' descriptor is empty). The loads run kStateDepth
+// chunks ahead in a ring of register sets (the chunk loop is unrolled by the ring size, so each
+// set keeps fixed registers), and the LDS tiles are double-buffered: a wave writes a buffer two
+// chunks after it was read, with a barrier between.
+constexpr int kStateDepth = 4;
+
+template <int NN>
+__global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
+    using TIN = __bf16;
+    using RW = Raw<NN, false, 1>;
+    using v8 = typename RW::v8;
+    constexpr int XP = P + 8, BP = NN + 16, NB = NN / 16, DEPTH = kStateDepth;
+    static_assert(DEPTH % 2 == 0, "the LDS buffer of ring slot k is k % 2");
+    __shared__ __attribute__((aligned(16))) __bf16 sxw[2][Q][XP];   // X w_j  (j, p)
+    __shared__ __attribute__((aligned(16))) __bf16 sb[2][Q][BP];    // B      (j, n)
+    __shared__ float sw[2][Q];    // w_j = exp(acum_end - acum_j) dt'_j
+    __shared__ float sae[2];      // acum_end
+
+    int wg = blockIdx.x;
+    if (a.remap) {
+        const int per = gridDim.x / 8;
+        wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    }
+    // segment-major: the heads of one (batch, segment) are adjacent and share B through one L2
+    const int seg = wg / (a.B * a.H);
+    const int bh = wg % (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H;
+    const int g = h / (a.H / a.G);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);
+    const float Ah = a.A[h];
+    const float dtb = a.dt_bias ? a.dt_bias[h] : 0.f;
+    const int c_begin = seg * a.chunks_per_seg;
+    const int c_end = min(c_begin + a.chunks_per_seg, a.nchunks);
+
+    constexpr unsigned SZ = sizeof(TIN);
+    const long brow = (long)b * a.L;
+    const TIN* x0 = reinterpret_cast<const TIN*>(a.x) + brow * a.ldx + (long)h * P;
+    const TIN* b0 = reinterpret_cast<const TIN*>(a.Bm) + brow * a.ldb + (long)g * a.N;
+    const float* d0 = a.dt + brow * a.lddt + h;
+    const int xr = lane / RW::XL, xc = RW::XE * (lane % RW::XL);
+    const unsigned ox = (unsigned)((16 * w + xr) * a.ldx + xc) * SZ;
+    const unsigned oxk = (unsigned)(RW::XR * a.ldx) * SZ;
+    const unsigned ob = (unsigned)(br * a.ldb + bc) * SZ;
+    const unsigned obk = (unsigned)(RW::BR * a.ldb) * SZ;
+    const unsigned od = (unsigned)(lane * a.lddt) * 4u;
+    auto rows_of = [&](int c) { return c < c_end ? min(Q, a.L - c * Q) : 0; };
+    auto span = [](int qv, long ld, int width, unsigned esz) {
+        return qv > 0 ? (unsigned)(((long)(qv - 1) * ld + width) * esz) : 0u;
+    };
+    // x, B and dt of chunk c (a chunk past the segment has an empty range: zeros, no traffic)
+    auto load_raw = [&](RW& r, int c) {
+        const int qv = rows_of(c);
+        const long r0 = (long)c * Q;
+        // dt: one strided 4-byte value per step (a cache line per lane), so only wave 0, which
+        // scans, fetches it; the other waves' descriptor is empty (no memory traffic)
+        const auto rd = rsrc(d0 + r0 * a.lddt, w == 0 ? span(qv, a.lddt, 1, 4) : 0u);
+        const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
+        const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
+        r.dt = bload4(rd, od);
+#pragma unroll
+        for (int k = 0; k < RW::XK; ++k) r.x[k] = bload16<v8>(rx, ox + k * oxk);
+#pragma unroll
+        for (int k = 0; k < RW::BPASS; ++k) r.b[k] = bload16<v8>(rb, ob + k * obk);
+    };
+
+    RW raw[DEPTH];
+#pragma unroll
+    for (int k = 0; k < DEPTH; ++k) {
+        load_raw(raw[k], c_begin + k);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    floatx4 S[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) S[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float decay_sum = 0.f;   // wave 0
+    // wave 0: dt' of chunk cc (0 past the segment), its prefix sum of dt' A, the weights w_j and
+    // acum_end into buffer bf (lane = step)
+    auto scan_put = [&](int cc, float raw_dt, int bf) {
+        const int qv = rows_of(cc);
+        float dv = raw_dt + dtb;
+        if (a.softplus) dv = ssm::softplus_sel(dv);
+        dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
+        const float sc = wave_prefix_sum(dv * Ah);
+        const float ae = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
+        sw[bf][lane] = ssm::ex2((ae - sc) * ssm::kLog2e) * dv;
+        if (lane == 0) sae[bf] = ae;
+        decay_sum += ae;
+    };
+    if (w == 0) scan_put(c_begin, raw[0].dt, 0);
+    __syncthreads();
+
+    // Whole groups of DEPTH chunks with no exit inside a group, so that the loads in flight at
+    // the loop head are the same on entry and on the back edge and the compiler's vmcnt waits
+    // stay exact. A chunk past the segment reads zeros (dt' = 0, w = 0, decay 1): it leaves
+    // the state and the decay sum unchanged.
+    for (int c0 = c_begin; c0 < c_end; c0 += DEPTH) {
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) {
+            const int c = c0 + k;
+            const int buf = k & 1;
+            // wave 0 scans the next chunk (its dt is the first load of the next ring slot) into
+            // the other buffer, which every wave last read before the previous barrier
+            if (w == 0) scan_put(c + 1, raw[(k + 1) % DEPTH].dt, buf ^ 1);
+            const float acend = sae[buf];
+#pragma unroll
+            for (int kx = 0; kx < RW::XK; ++kx) {
+                const int j = 16 * w + RW::XR * kx + xr;
+                const float wj = sw[buf][j];
+                bf16x8 wh;
+#pragma unroll
+                for (int e = 0; e < RW::XE; ++e) wh[e] = hi_of((float)raw[k].x[kx][e] * wj);
+                *reinterpret_cast<bf16x8*>(&sxw[buf][j][xc]) = wh;
+            }
+#pragma unroll
+            for (int kb = 0; kb < RW::BPASS; ++kb)
+                *reinterpret_cast<bf16x8*>(&sb[buf][br + RW::BR * kb][bc]) = raw[k].b[kb];
+            load_raw(raw[k], c + DEPTH);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+
+            const float e = ssm::ex2(acend * ssm::kLog2e);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) S[nb] *= e;
+#pragma unroll
+            for (int ks = 0; ks < Q / 32; ++ks) {
+                const int j0 = 32 * ks + 8 * q4;
+                const bf16x8 xh = cat(tr_read<XP>(&sxw[buf][0][0], j0, 16 * w, l16),
+                                      tr_read<XP>(&sxw[buf][0][0], j0 + 4, 16 * w, l16));
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const bf16x8 bv = cat(tr_read<BP>(&sb[buf][0][0], j0, 16 * nb, l16),
+                                          tr_read<BP>(&sb[buf][0][0], j0 + 4, 16 * nb, l16));
+                    S[nb] = mfma(xh, bv, S[nb]);
+                }
+            }
+        }
+    }
+
+    float* out = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
+    if (w == 0 && lane == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) out[(long)(16 * w + 4 * q4 + r) * NN + 16 * nb + l16] = S[nb][r];
+}
+
 // Segment entering states: slot[s] <- carry; carry = exp(decay[s]) carry + local[s].
 __global__ void ssd_seg_prefix(SsdArgs a, int PN) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -620,7 +780,7 @@ ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
         SsdArgs s1 = a;
         const int nwg1 = a.B * a.H * (a.nseg - 1);
         s1.remap = (nwg1 % 8 == 0) ? 1 : 0;
-        ssd_kernel<NN, false, 1><<<nwg1, 256, 0, st>>>(s1);
+        ssd_state_kernel<NN><<<nwg1, 256, 0, st>>>(s1);
         ssm_status e = ssm::check_launch("ssd_state_pass");
         if (e != SSM_OK) return e;
         const long n = (long)a.B * a.H * P * NN;

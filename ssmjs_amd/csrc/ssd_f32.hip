@@ -171,6 +171,11 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         return qv > 0 ? (unsigned)(((long)(qv - 1) * ld + width) * 4) : 0u;
     };
 
+    // C B^T tiles rotate over the waves from one workgroup to the next, so that no SIMD always
+    // gets the wave with the most (or no) tiles; the wave without a tile scans the next chunk
+    const int rot = blockIdx.x & 3;
+    const int scan_wave = (NCB + rot) & 3;
+
     // raw inputs of one chunk: X[j = 16 jb + 4 q4 + s][p0 + l16], B and C staging rows, dt
     struct Raw {
         float x[QB][4];
@@ -183,7 +188,10 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     auto load_raw = [&](int c, int cd) {
         const int qv = rows_of(c);
         const long r0 = (long)c * QF;
-        const auto rd = rsrc(d0 + (long)cd * QF * a.lddt, span(rows_of(cd), a.lddt, 1));
+        // dt: one strided 4-byte value per step (a cache line per lane); in the full pass only
+        // the wave that scans fetches it, the others get an empty descriptor (no traffic)
+        const auto rd = rsrc(d0 + (long)cd * QF * a.lddt,
+                             (FULL && w != scan_wave) ? 0u : span(rows_of(cd), a.lddt, 1));
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, 16));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN));
         raw.dt = bload4(rd, (unsigned)(lane * a.lddt) * 4u);
@@ -221,9 +229,6 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     }
     bool state_live = init != nullptr;
     float decay_sum = 0.f;
-    // C B^T tiles rotate over the waves from one workgroup to the next, so that no SIMD always
-    // gets the wave with the most (or no) tiles
-    const int rot = blockIdx.x & 3;
     // dt' of chunk cc (0 past the segment), its running sum times A_h and the weights w_t into
     // LDS buffer bf (lane = time step)
     auto scan_put = [&](int cc, float raw_dt, int bf) {
@@ -307,7 +312,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
             // ---- M^T tiles of C B^T (this wave's share of the causal tiles)
             // the wave without a tile scans chunk c + 1 into the other buffers (the last reads
             // of those, chunk c - 1's, came before barrier 1)
-            if (((NCB + rot) & 3) == w) scan_put(c + 1, dnext, buf ^ 1);
+            if (w == scan_wave) scan_put(c + 1, dnext, buf ^ 1);
 #pragma unroll
             for (int t = 0; t < NCB; ++t) {
                 if (((t + rot) & 3) != w) continue;
