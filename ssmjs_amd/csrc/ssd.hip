@@ -6,8 +6,9 @@
 // waves per head; two heads when heads pair up in a group) and walks the segment's chunks in
 // order with each head's P x N state held in MFMA accumulator registers, so the chunk-state
 // tensor is never written to HBM. Per chunk of Q = 64 steps:
-//   dt/decay  every wave computes dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix
-//             sum of dt' * A_h over the chunk with a 64-lane DPP scan.
+//   dt/decay  dt' = clamp(softplus(dt + dt_bias)) and the inclusive prefix sum of dt' * A_h
+//             over the chunk with a 64-lane DPP scan, formed a chunk ahead by one wave per
+//             head and read from LDS by the others.
 //   staging   X, X * w with w_j = exp(acum_end - acum_j) dt'_j, and B go to LDS as bf16. C
 //             goes to LDS too when two heads share it; with one head each wave keeps its 16
 //             rows of C in registers.
@@ -81,7 +82,7 @@ __device__ __forceinline__ __bf16 hi_of(float v) { return (__bf16)v; }
 // are conflict-free at pitch 144; the transposed reads over rows j0 + 8 q4 (+4) meet 2-way
 // bank conflicts at every pitch (SQ_LDS_BANK_CONFLICT). A layout without them (k-slot rows
 // 4 q4 apart, pitches of 16 mod 32) ran no faster: LDS is not what bounds this kernel.
-template <int NN, bool FULL, int HPW>
+template <int NN, int HPW>
 struct Smem {
     static constexpr int XP = P + 8;                   // X / Xw row pitch (bf16)
     static constexpr int BP = NN + 16;                 // B / C row pitch
@@ -90,10 +91,10 @@ struct Smem {
     // are staged once for the HPW heads of the workgroup; the other tiles are per head.
     alignas(16) __bf16 xw[HPW][Q][XP];                 // X * w_j   (j, p)
     alignas(16) __bf16 b[Q][BP];                       // B         (j, n)
-    static constexpr bool CST = FULL && HPW > 1;       // C staged (shared by two heads)
+    static constexpr bool CST = HPW > 1;               // C staged (shared by two heads)
     alignas(16) __bf16 c[CST ? Q : 1][BP];             // C   (i, n)
-    alignas(16) __bf16 x[HPW][FULL ? Q : 1][XP];       // X   (j, p)
-    alignas(16) __bf16 s[HPW][FULL ? NN : 1][XP];      // state^T (n, p)
+    alignas(16) __bf16 x[HPW][Q][XP];                  // X   (j, p)
+    alignas(16) __bf16 s[HPW][NN][XP];                 // state^T (n, p)
     // two chunks' worth (the full pass scans a chunk ahead)
     alignas(16) float dv[2][HPW][Q];   // dt'_j
     alignas(16) float ac[2][HPW][Q];   // acum_j log2(e)
@@ -189,14 +190,14 @@ __device__ __forceinline__ V vzero() {
 // Launch shape: HPW heads of one group per workgroup (4 waves per head). When heads pair up
 // in a group, two heads per workgroup (8 waves, one workgroup per CU): B and C are loaded and
 // staged once for both heads, which halves their share of the memory instructions.
-template <int NN, bool FULL, int HPW>
-__global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kernel(SsdArgs a) {
+template <int NN, int HPW>
+__global__ __launch_bounds__(256 * HPW, HPW > 1 ? 1 : 2) void ssd_kernel(SsdArgs a) {
     using TIN = __bf16;
-    __shared__ __attribute__((aligned(16))) Smem<NN, FULL, HPW> sm;
-    using SM = Smem<NN, FULL, HPW>;
+    __shared__ __attribute__((aligned(16))) Smem<NN, HPW> sm;
+    using SM = Smem<NN, HPW>;
     constexpr int NB = NN / 16;   // state n-blocks per wave
     constexpr int KS = NN / 32;   // k-steps over n
-    using RW = Raw<NN, FULL, HPW>;
+    using RW = Raw<NN, true, HPW>;
     constexpr bool CST = SM::CST;       // C staged in LDS (two heads) or loaded per wave
 
     int wg = blockIdx.x;
@@ -269,10 +270,9 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
     auto load_raw = [&](int c, int cd) {
         const int qv = rows_of(c);
         const long r0 = (long)c * Q;
-        // dt: one strided 4-byte value per step (a cache line per lane); in the full pass only
-        // the wave that scans fetches it, the others get an empty descriptor (no traffic)
-        const auto rd = rsrc(d0 + (long)cd * Q * a.lddt,
-                             (FULL && wl != 0) ? 0u : span(rows_of(cd), a.lddt, 1, 4));
+        // dt: one strided 4-byte value per step (a cache line per lane); only the wave that
+        // scans fetches it, the others get an empty descriptor (no traffic)
+        const auto rd = rsrc(d0 + (long)cd * Q * a.lddt, wl != 0 ? 0u : span(rows_of(cd), a.lddt, 1, 4));
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         raw.dt = bload4(rd, od);
@@ -288,9 +288,9 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
     };
     // Without C staging: C rows of the wave's strip, row ic, n = 32ks + 8q4 + 0..7 (MFMA
     // B-operand fragments), prefetched after their last use in the previous chunk
-    v8 craw[FULL && !CST ? KS : 1];
+    v8 craw[!CST ? KS : 1];
     auto load_c = [&](int c) {
-        if constexpr (FULL && !CST) {
+        if constexpr (!CST) {
             const int qv = rows_of(c);
             const auto rc = rsrc(cm0 + (long)c * Q * a.ldc, span(qv, a.ldc, NN, SZ));
             // craw[2h + sel]: row 16wl + (l16 & ~1) + sel, n = 64h + 32 (l16 & 1) + 8 q4 + 0..7
@@ -309,10 +309,8 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
 
     // ---- entering state -> accumulators (wave wl: rows p = 16wl + 4*q4 + r, cols 16nb + l16)
     const float* init = nullptr;
-    if (FULL) {
-        if (a.nseg > 1) init = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
-        else if (a.h0) init = a.h0 + (long)bh * P * NN;
-    }
+    if (a.nseg > 1) init = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
+    else if (a.h0) init = a.h0 + (long)bh * P * NN;
     floatx4 S[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -320,7 +318,6 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         for (int r = 0; r < 4; ++r)
             S[nb][r] = init ? init[(long)(16 * wl + 4 * q4 + r) * NN + 16 * nb + l16] : 0.f;
     bool state_live = init != nullptr;
-    float decay_sum = 0.f;
 
     // The accumulators hold S[p = 16wl + 4q4 + r][n = 16nb + l16] for r = 0..3: four
     // consecutive p of one n, i.e. one 8-byte run of the state^T tile.
@@ -333,7 +330,7 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
             *reinterpret_cast<bf16x4*>(&sm.s[hw][16 * nb + l16][16 * wl + 4 * q4]) = hv;
         }
     };
-    if (FULL && state_live) write_state_lds();
+    if (state_live) write_state_lds();
     // dt' of chunk cc (0 past the segment), acum in log2 units, the weights w_j and acum_end of
     // the wave's head into LDS buffer bf (lane = time step)
     auto scan_put = [&](int cc, float raw_dt, int bf) {
@@ -351,20 +348,16 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         sm.wj[bf][hw][lane] = ssm::ex2((ae - sc) * ssm::kLog2e) * dv;
         if (lane == 0) sm.ae[bf][hw] = ae;
     };
-    if constexpr (FULL) {
-        // the first chunk's scan (in the loop, each head's wave with the lightest Y_diag scans
-        // the next chunk while the others work); dt of the second chunk comes with the inputs
-        if (wl == 0) {
-            const auto rd0 = rsrc(d0 + (long)c_begin * Q * a.lddt, span(rows_of(c_begin), a.lddt, 1, 4));
-            scan_put(c_begin, bload4(rd0, od), c_begin & 1);
-        }
-        __syncthreads();
-        load_raw(c_begin, c_begin + 1);
-    } else {
-        load_raw(c_begin, c_begin);
+    // the first chunk's scan (in the loop, each head's wave with the lightest Y_diag scans the
+    // next chunk while the others work); dt of the second chunk comes with the inputs
+    if (wl == 0) {
+        const auto rd0 = rsrc(d0 + (long)c_begin * Q * a.lddt, span(rows_of(c_begin), a.lddt, 1, 4));
+        scan_put(c_begin, bload4(rd0, od), c_begin & 1);
     }
+    __syncthreads();
+    load_raw(c_begin, c_begin + 1);
     load_c(c_begin);
-    if constexpr (FULL) {
+    {
         // Four stores into an empty range (dropped by the range check) make the memory
         // instructions in flight at loop entry match the back edge (the prefetches, then the
         // four y stores), so the wait for a prefetch never includes the previous chunk's stores.
@@ -379,35 +372,20 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         const long row0 = (long)b * a.L + t0;
 
         const int buf = c & 1;
-        // ---- dt' and the inclusive prefix of dt' * A (state-only pass: every wave, lane =
-        // time step; the full pass formed them a chunk earlier)
-        float acend, wl_ = 0.f;
-        if constexpr (FULL) {
-            acend = sm.ae[buf][hw];
-        } else {
-            float dv = raw.dt + dtb;
-            if (a.softplus) dv = ssm::softplus_fast(dv);
-            dv = lane < qv ? fminf(fmaxf(dv, a.dt_min), a.dt_max) : 0.f;
-            const float sc = wave_prefix_sum(dv * Ah);
-            acend = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
-            decay_sum += acend;
-            wl_ = ssm::ex2((acend - sc) * ssm::kLog2e) * dv;   // w_j for j = lane
-        }
+        // dt', the prefix of dt' * A and w_j of this chunk were formed a chunk earlier
+        const float acend = sm.ae[buf][hw];
 
-        // ---- stage X and X w (rows of the X prefetch; w_j comes from lane j of this wave)
+        // ---- stage X and X w (rows of the X prefetch)
 #pragma unroll
         for (int k = 0; k < RW::XK; ++k) {
             constexpr int E = RW::XE;
             const int j = 16 * wl + RW::XR * k + xr;
-            const float wj = FULL ? sm.wj[buf][hw][j]
-                                  : __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                                  4 * j, __builtin_bit_cast(int, wl_)));
+            const float wj = sm.wj[buf][hw][j];
             bf16x8 wh;
 #pragma unroll
             for (int e = 0; e < E; ++e) wh[e] = hi_of((float)raw.x[k][e] * wj);
             *reinterpret_cast<bf16x8*>(&sm.xw[hw][j][xc]) = wh;
-            if constexpr (FULL) *reinterpret_cast<bf16x8*>(&sm.x[hw][j][xc]) = raw.x[k];
+            *reinterpret_cast<bf16x8*>(&sm.x[hw][j][xc]) = raw.x[k];
         }
         // ---- stage B and C (shared by the workgroup's heads)
 #pragma unroll
@@ -417,8 +395,8 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         }
         // ---- C rows of this wave's strip as MFMA fragments: row ic, n = 32ks + 8q4 + 0..7
         // (from registers here without C staging, from LDS after the barrier with it)
-        bf16x8 cfh[FULL ? KS : 1];
-        if constexpr (FULL && !CST) {
+        bf16x8 cfh[KS];
+        if constexpr (!CST) {
             // fragment ks = 2h + e of row ic: the own load (h, sel = l16 & 1) holds e = l16 & 1,
             // the neighbour's load (h, sel = l16 & 1) the other one
 #pragma unroll
@@ -433,11 +411,10 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
 
         // ---- the next chunk's raw inputs are in flight while this one computes (a chunk past
         // the segment has an empty range: the loads return zeros without touching memory)
-        const float dnext = raw.dt;   // full pass: dt of chunk c + 1
-        if constexpr (FULL) load_raw(c + 1, c + 2);
-        else load_raw(c + 1, c + 1);
+        const float dnext = raw.dt;   // dt of chunk c + 1
+        load_raw(c + 1, c + 2);
 
-        if constexpr (FULL) {
+        {
             if constexpr (CST) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
@@ -577,18 +554,12 @@ __global__ __launch_bounds__(256 * HPW, (FULL && HPW > 1) ? 1 : 2) void ssd_kern
         }
         state_live = true;
         __syncthreads();   // every wave is done reading this chunk's LDS
-        if (FULL && c + 1 < c_end) write_state_lds();
+        if (c + 1 < c_end) write_state_lds();
     }
 
-    // ---- outputs of the state
-    float* out = nullptr;
-    if (FULL) {
-        if (a.hT && seg == a.nseg - 1) out = a.hT + (long)bh * P * NN;
-    } else {
-        out = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
-        if (wl == 0 && lane == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
-    }
-    if (out) {
+    // ---- the final state (last segment)
+    if (a.hT && seg == a.nseg - 1) {
+        float* out = a.hT + (long)bh * P * NN;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -772,11 +743,10 @@ __global__ void ssd_seg_prefix(SsdArgs a, int PN) {
 template <int NN, int HPW>
 ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
     if (a.nseg > 1) {
-        // the state-only pass runs one head per workgroup: with no Y work its B tile is a
-        // small share of the memory instructions, and independent workgroups overlap better
-        // than two heads in lockstep. The last segment's local state is never combined
-        // (the full pass produces the final state), so only the first nseg - 1 segments run
-        // (the order is segment-major: they are the first B*H*(nseg-1) workgroups).
+        // the state-only pass (ssd_state_kernel, one head per workgroup). The last segment's
+        // local state is never combined (the full pass produces the final state), so only the
+        // first nseg - 1 segments run (the order is segment-major: they are the first
+        // B*H*(nseg-1) workgroups).
         SsdArgs s1 = a;
         const int nwg1 = a.B * a.H * (a.nseg - 1);
         s1.remap = (nwg1 % 8 == 0) ? 1 : 0;
@@ -790,7 +760,7 @@ ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
     }
     const int nwg = a.B * (a.H / HPW) * a.nseg;
     a.remap = (nwg % 8 == 0) ? 1 : 0;
-    ssd_kernel<NN, true, HPW><<<nwg, 256 * HPW, 0, st>>>(a);
+    ssd_kernel<NN, HPW><<<nwg, 256 * HPW, 0, st>>>(a);
     return ssm::check_launch("ssd_chunk_scan");
 }
 
