@@ -568,41 +568,48 @@ __global__ __launch_bounds__(256 * HPW, HPW > 1 ? 1 : 2) void ssd_kernel(SsdArgs
 }
 
 // State-only pass of the segmented mode (long sequences with few batch x heads): a workgroup
-// reads x, B and dt of one (batch, segment, head) once and returns the segment's local final
-// state (from a zero state) and its total decay sum(dt' A). Per chunk: wave 0 scans the next
-// chunk's dt (dt', its prefix sum of dt' A, w_j = exp(acum_end - acum_j) dt'_j) into LDS; every
-// wave stages X w and B into LDS; one barrier; then S = exp(acum_end) S + (X w)^T B (wave w:
-// state rows p = 16w .. 16w + 15). dt is one strided 4-byte value per step, a cache line per
-// lane, so only wave 0 fetches it (the others' descriptor is empty). The loads run kStateDepth
+// reads x, B and dt of one (batch, segment) and HPW heads of one group once and returns each
+// head's local final state of the segment (from a zero state) and its total decay sum(dt' A).
+// B is staged once for the HPW heads. Per chunk: each head's wave 0 scans the next chunk's dt
+// (dt', its prefix sum of dt' A, w_j = exp(acum_end - acum_j) dt'_j) into LDS; every wave
+// stages X w (and its share of B) into LDS; one barrier; then S = exp(acum_end) S + (X w)^T B
+// (wave 4 hw + wl: head hw, state rows p = 16 wl .. 16 wl + 15). dt is one strided 4-byte value
+// per step, a cache line per lane, so only the scanning waves fetch it (the others' descriptor
+// is empty). The loads run kStateDepth
 // chunks ahead in a ring of register sets (the chunk loop is unrolled by the ring size, so each
 // set keeps fixed registers), and the LDS tiles are double-buffered: a wave writes a buffer two
 // chunks after it was read, with a barrier between.
 constexpr int kStateDepth = 4;
 
-template <int NN>
-__global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
+template <int NN, int HPW>
+__global__ __launch_bounds__(256 * HPW, HPW > 1 ? 1 : 2) void ssd_state_kernel(SsdArgs a) {
     using TIN = __bf16;
-    using RW = Raw<NN, false, 1>;
+    using RW = Raw<NN, false, HPW>;
     using v8 = typename RW::v8;
     constexpr int XP = P + 8, BP = NN + 16, NB = NN / 16, DEPTH = kStateDepth;
     static_assert(DEPTH % 2 == 0, "the LDS buffer of ring slot k is k % 2");
-    __shared__ __attribute__((aligned(16))) __bf16 sxw[2][Q][XP];   // X w_j  (j, p)
-    __shared__ __attribute__((aligned(16))) __bf16 sb[2][Q][BP];    // B      (j, n)
-    __shared__ float sw[2][Q];    // w_j = exp(acum_end - acum_j) dt'_j
-    __shared__ float sae[2];      // acum_end
+    __shared__ __attribute__((aligned(16))) __bf16 sxw[2][HPW][Q][XP];   // X w_j  (j, p)
+    __shared__ __attribute__((aligned(16))) __bf16 sb[2][Q][BP];         // B      (j, n)
+    __shared__ float sw[2][HPW][Q];    // w_j = exp(acum_end - acum_j) dt'_j
+    __shared__ float sae[2][HPW];      // acum_end
 
     int wg = blockIdx.x;
     if (a.remap) {
         const int per = gridDim.x / 8;
         wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
     }
-    // segment-major: the heads of one (batch, segment) are adjacent and share B through one L2
-    const int seg = wg / (a.B * a.H);
-    const int bh = wg % (a.B * a.H);
-    const int b = bh / a.H, h = bh % a.H;
-    const int g = h / (a.H / a.G);
+    // segment-major: the head groups of one (batch, segment) are adjacent and share B through
+    // one L2. Wave w works on head hw = w / 4 of the workgroup, state rows 16 wl .. 16 wl + 15.
+    const int HW = a.H / HPW;
+    const int seg = wg / (a.B * HW);
+    const int bhw = wg % (a.B * HW);
+    const int b = bhw / HW;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hw = w >> 2, wl = w & 3;
+    const int h = HPW * (bhw % HW) + hw;
+    const int bh = b * a.H + h;
+    const int g = h / (a.H / a.G);
     const int l16 = lane & 15, q4 = lane >> 4;
     const int br = tid / RW::BL, bc = 8 * (tid % RW::BL);
     const float Ah = a.A[h];
@@ -616,7 +623,7 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
     const TIN* b0 = reinterpret_cast<const TIN*>(a.Bm) + brow * a.ldb + (long)g * a.N;
     const float* d0 = a.dt + brow * a.lddt + h;
     const int xr = lane / RW::XL, xc = RW::XE * (lane % RW::XL);
-    const unsigned ox = (unsigned)((16 * w + xr) * a.ldx + xc) * SZ;
+    const unsigned ox = (unsigned)((16 * wl + xr) * a.ldx + xc) * SZ;
     const unsigned oxk = (unsigned)(RW::XR * a.ldx) * SZ;
     const unsigned ob = (unsigned)(br * a.ldb + bc) * SZ;
     const unsigned obk = (unsigned)(RW::BR * a.ldb) * SZ;
@@ -629,9 +636,9 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
     auto load_raw = [&](RW& r, int c) {
         const int qv = rows_of(c);
         const long r0 = (long)c * Q;
-        // dt: one strided 4-byte value per step (a cache line per lane), so only wave 0, which
-        // scans, fetches it; the other waves' descriptor is empty (no memory traffic)
-        const auto rd = rsrc(d0 + r0 * a.lddt, w == 0 ? span(qv, a.lddt, 1, 4) : 0u);
+        // dt: one strided 4-byte value per step (a cache line per lane), so only each head's
+        // wave 0, which scans, fetches it; the other waves' descriptor is empty (no traffic)
+        const auto rd = rsrc(d0 + r0 * a.lddt, wl == 0 ? span(qv, a.lddt, 1, 4) : 0u);
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         r.dt = bload4(rd, od);
@@ -651,9 +658,9 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
     floatx4 S[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) S[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float decay_sum = 0.f;   // wave 0
-    // wave 0: dt' of chunk cc (0 past the segment), its prefix sum of dt' A, the weights w_j and
-    // acum_end into buffer bf (lane = step)
+    float decay_sum = 0.f;   // each head's wave 0
+    // each head's wave 0: dt' of chunk cc (0 past the segment), its prefix sum of dt' A, the
+    // weights w_j and acum_end into buffer bf (lane = step)
     auto scan_put = [&](int cc, float raw_dt, int bf) {
         const int qv = rows_of(cc);
         float dv = raw_dt + dtb;
@@ -662,11 +669,11 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
         const float sc = wave_prefix_sum(dv * Ah);
         const float ae = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 63));
-        sw[bf][lane] = ssm::ex2((ae - sc) * ssm::kLog2e) * dv;
-        if (lane == 0) sae[bf] = ae;
+        sw[bf][hw][lane] = ssm::ex2((ae - sc) * ssm::kLog2e) * dv;
+        if (lane == 0) sae[bf][hw] = ae;
         decay_sum += ae;
     };
-    if (w == 0) scan_put(c_begin, raw[0].dt, 0);
+    if (wl == 0) scan_put(c_begin, raw[0].dt, 0);
     __syncthreads();
 
     // Whole groups of DEPTH chunks with no exit inside a group, so that the loads in flight at
@@ -680,16 +687,16 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
             const int buf = k & 1;
             // wave 0 scans the next chunk (its dt is the first load of the next ring slot) into
             // the other buffer, which every wave last read before the previous barrier
-            if (w == 0) scan_put(c + 1, raw[(k + 1) % DEPTH].dt, buf ^ 1);
-            const float acend = sae[buf];
+            if (wl == 0) scan_put(c + 1, raw[(k + 1) % DEPTH].dt, buf ^ 1);
+            const float acend = sae[buf][hw];
 #pragma unroll
             for (int kx = 0; kx < RW::XK; ++kx) {
-                const int j = 16 * w + RW::XR * kx + xr;
-                const float wj = sw[buf][j];
+                const int j = 16 * wl + RW::XR * kx + xr;
+                const float wj = sw[buf][hw][j];
                 bf16x8 wh;
 #pragma unroll
                 for (int e = 0; e < RW::XE; ++e) wh[e] = hi_of((float)raw[k].x[kx][e] * wj);
-                *reinterpret_cast<bf16x8*>(&sxw[buf][j][xc]) = wh;
+                *reinterpret_cast<bf16x8*>(&sxw[buf][hw][j][xc]) = wh;
             }
 #pragma unroll
             for (int kb = 0; kb < RW::BPASS; ++kb)
@@ -704,8 +711,8 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
 #pragma unroll
             for (int ks = 0; ks < Q / 32; ++ks) {
                 const int j0 = 32 * ks + 8 * q4;
-                const bf16x8 xh = cat(tr_read<XP>(&sxw[buf][0][0], j0, 16 * w, l16),
-                                      tr_read<XP>(&sxw[buf][0][0], j0 + 4, 16 * w, l16));
+                const bf16x8 xh = cat(tr_read<XP>(&sxw[buf][hw][0][0], j0, 16 * wl, l16),
+                                      tr_read<XP>(&sxw[buf][hw][0][0], j0 + 4, 16 * wl, l16));
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     const bf16x8 bv = cat(tr_read<BP>(&sb[buf][0][0], j0, 16 * nb, l16),
@@ -717,40 +724,32 @@ __global__ __launch_bounds__(256, 2) void ssd_state_kernel(SsdArgs a) {
     }
 
     float* out = a.seg_state + ((long)bh * a.nseg + seg) * P * NN;
-    if (w == 0 && lane == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
+    if (wl == 0 && lane == 0) a.seg_decay[(long)bh * a.nseg + seg] = decay_sum;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) out[(long)(16 * w + 4 * q4 + r) * NN + 16 * nb + l16] = S[nb][r];
+        for (int r = 0; r < 4; ++r) out[(long)(16 * wl + 4 * q4 + r) * NN + 16 * nb + l16] = S[nb][r];
 }
 
 // Segment entering states: slot[s] <- carry; carry = exp(decay[s]) carry + local[s].
 __global__ void ssd_seg_prefix(SsdArgs a, int PN) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)a.B * a.H * PN) return;
-    const int e = (int)(i % PN);
-    const long bh = i / PN;
-    float carry = a.h0 ? a.h0[bh * PN + e] : 0.f;
-    for (int s = 0; s < a.nseg; ++s) {
-        float* p = a.seg_state + (bh * a.nseg + s) * PN + e;
-        const float loc = (s + 1 < a.nseg) ? *p : 0.f;
-        *p = carry;
-        if (s + 1 < a.nseg)
-            carry = fmaf(ssm::ex2(a.seg_decay[bh * a.nseg + s] * ssm::kLog2e), carry, loc);
-    }
+    ssm::seg_prefix_elem(a.seg_state, a.seg_decay, a.h0, a.nseg, PN, i / PN, (int)(i % PN),
+                         ssm::kLog2e);
 }
 
 template <int NN, int HPW>
 ssm_status launch_ssd(SsdArgs& a, hipStream_t st) {
     if (a.nseg > 1) {
-        // the state-only pass (ssd_state_kernel, one head per workgroup). The last segment's
+        // the state-only pass (ssd_state_kernel, HPW heads per workgroup). The last segment's
         // local state is never combined (the full pass produces the final state), so only the
         // first nseg - 1 segments run (the order is segment-major: they are the first
-        // B*H*(nseg-1) workgroups).
+        // B*(H/HPW)*(nseg-1) workgroups).
         SsdArgs s1 = a;
-        const int nwg1 = a.B * a.H * (a.nseg - 1);
+        const int nwg1 = a.B * (a.H / HPW) * (a.nseg - 1);
         s1.remap = (nwg1 % 8 == 0) ? 1 : 0;
-        ssd_state_kernel<NN><<<nwg1, 256, 0, st>>>(s1);
+        ssd_state_kernel<NN, HPW><<<nwg1, 256 * HPW, 0, st>>>(s1);
         ssm_status e = ssm::check_launch("ssd_state_pass");
         if (e != SSM_OK) return e;
         const long n = (long)a.B * a.H * P * NN;

@@ -27,4 +27,35 @@ bool ssd_gated_ok(int Pd, int G, int N, long ldx, long lddt, long ldb, long ldc,
                   long ldz, const void* x, const void* Bm, const void* Cm, const float* y,
                   const float* z, const float* gn);
 
+// Segment entering states of the segmented SSD, one thread per element e of a (b, h) state of
+// PN elements: slot[s] <- carry, carry = 2^(decay2[s]) carry + local[s], carry starting at h0
+// (or 0). decay2[s] is the segment's sum of dt' A in log2 units (the caller passes its own
+// decays times dscale to get there). The last slot's local state is never read by the result:
+// the state-only pass does not produce it. The slots' loads are issued in groups of 16 before
+// their stores, so that each group waits for memory once (a loop that stored slot s before
+// loading slot s + 1 waited for every load in turn).
+__device__ __forceinline__ void seg_prefix_elem(float* seg_state, const float* seg_decay,
+                                                const float* h0, int nseg, int PN, long bh,
+                                                int e, float dscale) {
+    constexpr int GS = 16;
+    float carry = h0 ? h0[bh * PN + e] : 0.f;
+    float* st = seg_state + bh * nseg * (long)PN + e;
+    const float* dc = seg_decay + bh * nseg;
+    for (int s0 = 0; s0 < nseg; s0 += GS) {
+        float loc[GS], dec[GS];
+#pragma unroll
+        for (int j = 0; j < GS; ++j) {
+            const int s = min(s0 + j, nseg - 1);   // past nseg: an in-range slot, not used
+            loc[j] = st[(long)s * PN];
+            dec[j] = dc[s];
+        }
+#pragma unroll
+        for (int j = 0; j < GS; ++j) {
+            if (s0 + j >= nseg) break;
+            st[(long)(s0 + j) * PN] = carry;
+            carry = fmaf(ex2(dec[j] * dscale), carry, loc[j]);
+        }
+    }
+}
+
 }  // namespace ssm

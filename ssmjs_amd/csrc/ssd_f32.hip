@@ -493,15 +493,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 __global__ void ssd_f32_seg_prefix(F32Args a, int PN) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)a.B * a.H * PN) return;
-    const int e = (int)(i % PN);
-    const long bh = i / PN;
-    float carry = a.h0 ? a.h0[bh * PN + e] : 0.f;
-    for (int s = 0; s < a.nseg; ++s) {
-        float* p = a.seg_state + (bh * a.nseg + s) * PN + e;
-        const float loc = (s + 1 < a.nseg) ? *p : 0.f;
-        *p = carry;
-        if (s + 1 < a.nseg) carry = fmaf(ssm::ex2(a.seg_decay[bh * a.nseg + s]), carry, loc);
-    }
+    ssm::seg_prefix_elem(a.seg_state, a.seg_decay, a.h0, a.nseg, PN, i / PN, (int)(i % PN), 1.f);
 }
 
 void plan_f32(int B, int L, int H, int& nchunks, int& nseg, int& per) {
