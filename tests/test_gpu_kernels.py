@@ -362,6 +362,33 @@ def test_ssd_long_sequence_segments(dtype, H, L):
     check_dtype(host(hd), hT, "final state", dtype)
 
 
+@pytest.mark.parametrize("B,H,G,N,L", [
+    (1, 3, 1, 128, 64 * 200 + 9),   # three heads in a group: one head per workgroup
+    (1, 4, 2, 128, 64 * 90 + 33),   # two groups of two heads
+    (2, 2, 1, 64, 64 * 70 + 1),     # d_state 64, two sequences
+])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ssd_segments_head_groups(dtype, B, H, G, N, L):
+    """The segmented mode with the other workgroup shapes of its passes: an odd number of heads
+    per group (the bf16 passes then take one head per workgroup), several groups, d_state 64,
+    more than one sequence; segments of one to a few chunks, partial last chunk."""
+    case(f"ssd segmented groups {dtype} B={B} H={H} G={G} N={N} L={L}")
+    r = rng(4100 + 10 * H + G + N)
+    P = 64
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N, bc_scale=N ** -0.25)
+    h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32)
+    tdt = torch.float32
+    if dtype == "bf16":
+        x, Bm, Cm = _bf(x), _bf(Bm), _bf(Cm)
+        tdt = torch.bfloat16
+    ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, h0=h0a, return_state=True)
+    hd = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x, tdt), dev(dt), dev(A), dev(Bm, tdt), dev(Cm, tdt), dev(Dk),
+                           None, True, h0=dev(h0a), hT=hd)
+    check_dtype(host(y), ref, "y", dtype)
+    check_dtype(host(hd), hT, "final state", dtype)
+
+
 @pytest.mark.parametrize("B,L,H,G,N,P,path", [
     (2, 45, 4, 1, 16, 16, "chunked"),      # one group, d_state <= 64: Mamba-1 chunked scan
     (1, 700, 4, 1, 16, 64, "chunked"),     # the presets' Mamba-2 shape, many scan chunks
