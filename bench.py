@@ -25,8 +25,11 @@ Workloads (--workload picks one line; the default is cfg3 with the extras):
   decode_m1  the cfg4 decode step through 24 Mamba-1 layers (the reference's default layer
         type) with cfg2's block dimensions (d=768 D=1536 N=16 R=48), V=32000, 64 sequences
 A step is one pass of the path over one batch of synthetic input that is already resident in
-HBM. Timing: W untimed warmup steps, then K steps between HIP events on the stream the
-library launches on (torch's current stream, handed to the library context).
+HBM. Timing: at least 0.1 s of untimed steps (the GPU's clocks settle over the first 10-20 ms
+of sustained work), W untimed warmup steps, then K steps between HIP events on the stream the
+library launches on (torch's current stream, handed to the library context). A second pass of
+max(K, 20) steps with an event after each step gives the per-step median, minimum and maximum
+reported beside the mean.
 
 The roofline object names the dominant kernel (stage) of the step, its algorithmic FLOPs or
 bytes per launch, and its average duration from HIP events on that stream (for multi-stage
@@ -100,7 +103,36 @@ def log(*a):
 
 # ---------------------------------------------------------------- timing helpers
 
+# per-step times of the last timed() call's second pass (ms)
+STEP_TIMES = []
+
+
+SPIN_UP_S = 0.1   # untimed sustained work before the warmup steps (seconds)
+
+
+def spin_up(torch, fn):
+    """Run the step for at least SPIN_UP_S seconds. The GPU raises its clocks over the first
+    10-20 ms of sustained work: timed right after a few warmup steps, the cfg3 SSD averaged
+    0.851 ms per step, against 0.758-0.761 ms after 20 or 100 warmup steps and 0.767 ms over
+    200 timed steps (same box, same build). The timed region that follows is unchanged."""
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= SPIN_UP_S:
+                return
+
+
 def timed(torch, fn, steps, warmup):
+    """Mean ms per step over `steps` steps between two HIP events on the library's stream (the
+    reported figure), after the spin-up and `warmup` untimed steps. A second pass of
+    max(steps, 20) steps with an event between consecutive steps gives the per-step
+    distribution (STEP_TIMES, its median reported beside the mean); it is kept out of the
+    first pass so that the event records there add nothing."""
+    spin_up(torch, fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -111,7 +143,27 @@ def timed(torch, fn, steps, warmup):
         fn()
     e1.record(s)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps   # ms per step
+    mean = e0.elapsed_time(e1) / steps
+    n2 = max(steps, 20)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n2 + 1)]
+    ev[0].record(s)
+    for i in range(n2):
+        fn()
+        ev[i + 1].record(s)
+    torch.cuda.synchronize()
+    STEP_TIMES[:] = [ev[i].elapsed_time(ev[i + 1]) for i in range(n2)]
+    return mean   # ms per step
+
+
+def step_stats():
+    """Median and spread of the last timed() call's per-step times (ms)."""
+    t = sorted(STEP_TIMES)
+    if not t:
+        return {}
+    n = len(t)
+    med = t[n // 2] if n % 2 else 0.5 * (t[n // 2 - 1] + t[n // 2])
+    return {"ms_per_step_median": round(med, 5), "ms_per_step_min": round(t[0], 5),
+            "ms_per_step_max": round(t[-1], 5), "per_step_samples": n}
 
 
 def profiled_stages(dev, torch, fn, steps):
@@ -690,6 +742,7 @@ def main():
                                        "bf16"),
     }
     r = runs[args.workload or "cfg3"](args)
+    stats = step_stats()
     extra = {}
     if args.workload is None and not args.no_extras:
         # the other configurations, each with its own default steps, no CPU baseline
@@ -707,6 +760,7 @@ def main():
             rl = e["roofline"]
             extra[key] = {"workload": e["config"]["workload"], "value": round(e["value"], 3),
                           "unit": "tokens/s", "ms_per_step": round(e["ms_per_step"], 5),
+                          **step_stats(),
                           "steps": e["steps"], "dtype": e["dtype"],
                           "roofline": {k: rl[k] for k in ("kernel", "bound", "achieved", "peak",
                                                           "unit", "frac", "avg_ms", "traffic")}}
@@ -722,6 +776,7 @@ def main():
             "ms_per_step": round(r.pop("ms_per_step"), 5), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": r.pop("dtype"),
             "data": "synthetic (seeded; random-init weights of the named architecture)"}
+    line.update(stats)
     line.update(r)
     if extra:
         line["extra"] = extra
