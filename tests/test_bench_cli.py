@@ -47,3 +47,24 @@ def test_no_device_is_a_clear_error():
     r = run("--workload", "cfg1")
     assert r.returncode == 1
     assert "needs a HIP device" in r.stderr
+
+
+def _bench_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_step_stats_median_and_spread():
+    """The per-step summary beside the mean: median of an even and an odd count, min, max."""
+    b = _bench_module()
+    b.STEP_TIMES[:] = [0.9, 0.7, 0.8, 1.3]
+    s = b.step_stats()
+    assert s == {"ms_per_step_median": 0.85, "ms_per_step_min": 0.7, "ms_per_step_max": 1.3,
+                 "per_step_samples": 4}
+    b.STEP_TIMES[:] = [2.0, 0.5, 1.0]
+    assert b.step_stats()["ms_per_step_median"] == 1.0
+    b.STEP_TIMES[:] = []
+    assert b.step_stats() == {}
