@@ -6,6 +6,7 @@ over their full length, and one property that holds at any size is checked on th
   sequences and their final states against the oracle, per element; the sequence run as two
   halves, the second seeded with the first half's final state, gives the same y and final state
   as one run (the chunk recurrence carried across launches).
+- SSD, config 3 with bf16 inputs: two sampled (batch, head) sequences and their final states.
 - SSD, config 5 (B=1 L=65536 H=32, bf16 inputs; the segmented path: state-only pass, combine,
   full pass): two sampled heads and their final states against the oracle.
 - Mamba-1 scan, config 2 (B=4 L=2048 D=1536 N=16, the single-pass kernel): 48 sampled channels
@@ -117,6 +118,22 @@ def test_ssd_config3_full_size_f32():
                             h0=hm, hT=h2)
     check_f32(np.concatenate([host(y1), host(y2)], axis=1), yh, "y from two halves")
     check_f32(host(h2), hTh, "final state from two halves")
+
+
+def test_ssd_config3_full_size_bf16():
+    B, L, H, P, N = 8, 4096, 64, 64, 128
+    case(f"ssd full size cfg3 bf16 B={B} L={L} H={H}")
+    r = np.random.default_rng(3103)
+    x, dt, A, Bm, Cm, Dk = ssd_inputs(r, B, L, H, P, N, 1.0)
+    x, Bm, Cm = bf16_round(x), bf16_round(Bm), bf16_round(Cm)
+    hT = torch.zeros(B, H, P, N, device="cuda")
+    y = K().ssd_chunk_scan(dev(x, torch.bfloat16), dev(dt), dev(A), dev(Bm, torch.bfloat16),
+                           dev(Cm, torch.bfloat16), dev(Dk), None, True, hT=hT)
+    yh, hTh = host(y), host(hT)
+    for b, h in ((1, 2), (6, 51)):
+        ry, rh = oracle_head(x, dt, A, Bm, Cm, Dk, b, h)
+        check_bf16(yh[b, :, h], ry, f"y (b={b}, h={h})")
+        check_bf16(hTh[b, h], rh, f"final state (b={b}, h={h})")
 
 
 def test_ssd_config5_full_size_bf16():
