@@ -36,9 +36,10 @@ bytes per launch, and its average duration from HIP events on that stream (for m
 workloads, events the library records around each stage during a second, profiled pass of K
 steps; cfg4's state update is timed on its own, back to back over the 24 layers' states).
 The cpu_baseline object times the restatements of the reference path on the host: the C
-oracle (oracle/) with OpenMP on every host core, and a single-threaded JavaScript
-restatement (oracle/ssm_ref.js, the reference's own execution model), on a bounded slice of
-the same workload.
+oracle (oracle/) with OpenMP on every host core, over a bounded sample of the same workload
+repeated for about 10 s (for the SSD lines, the whole workload), and a single-threaded
+JavaScript restatement (oracle/ssm_ref.js, the reference's own execution model) over one
+whole sequence.
 """
 from __future__ import annotations
 
@@ -200,16 +201,16 @@ def roofline(name, avg_ms, flops=None, nbytes=None, prec="f32", bound=None, traf
     return out
 
 
-def cpu_time(fn, budget_s=20.0, min_runs=3):
-    """Run fn at least once and until ~budget (at most min_runs if the budget allows more);
-    return seconds per call."""
+def cpu_time(fn, budget_s=10.0):
+    """Run fn at least once and again until budget_s seconds of host work have passed (a bounded
+    sample of about 10 s, as the measurement asks); return seconds per call."""
     t0 = time.perf_counter()
     n = 0
     while True:
         fn()
         n += 1
         el = time.perf_counter() - t0
-        if el > budget_s or n >= min_runs:
+        if el >= budget_s:
             return el / n
 
 
@@ -428,31 +429,43 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, wit
         rl["issued_mfma_flops"] = per_chunk_head * 2048.0 * (T / QF) * H
     if with_cpu and not args.no_cpu_baseline:
         from oracle import oracle as O
-        Ls = 2048
-        xs = x[:1, :Ls].float().cpu().numpy()
-        smp = (xs, dt[:1, :Ls].cpu().numpy(), A.cpu().numpy(), Bm[:1, :Ls].float().cpu().numpy(),
-               Cm[:1, :Ls].float().cpu().numpy(), Dk.cpu().numpy())
-        sec = cpu_time(lambda: O.ssd(*smp), 20.0)
-        cb = {"value": Ls / sec, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
-              "sample": f"B=1, L={Ls}, all {H} heads of the same inputs (fp32); C oracle "
+        # the whole workload (every sequence and head, the same inputs as fp32), repeated
+        # until about 10 s of host work have passed
+        smp = (x.float().cpu().numpy(), dt.cpu().numpy(), A.cpu().numpy(),
+               Bm.float().cpu().numpy(), Cm.float().cpu().numpy(), Dk.cpu().numpy())
+        runs = [0]
+
+        def cpu_run():
+            O.ssd(*smp)
+            runs[0] += 1
+        sec = cpu_time(cpu_run, 10.0)
+        cb = {"value": T / sec, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+              "sample": f"the whole workload (B={B}, L={L}, all {H} heads, the same inputs "
+                        f"as fp32), {runs[0]} runs in {sec * runs[0]:.1f} s; C oracle "
                         "(oracle/ssm_oracle.c, sequential SSD recurrence, fp64 accumulate), "
-                        "OpenMP over heads"}
+                        "OpenMP over (batch, head)"}
         cb.update(host_info())
-        # the reference's execution model: one JS thread (8 of the heads, scaled to all)
-        Lj, Hj = 256, 8
-        sub = tuple(np.ascontiguousarray(a) for a in (smp[0][:, :Lj, :Hj], smp[1][:, :Lj, :Hj],
-                                                       smp[2][:Hj], smp[3][:, :Lj],
-                                                       smp[4][:, :Lj], smp[5][:Hj]))
+        # the reference's execution model: one JS thread, one whole sequence with all heads
+        Lj = min(L, 4096)
+        sub = tuple(np.ascontiguousarray(a) for a in (smp[0][:1, :Lj], smp[1][:1, :Lj], smp[2],
+                                                       smp[3][:1, :Lj], smp[4][:1, :Lj],
+                                                       smp[5]))
         js = js_ssd_baseline(np, *sub)
         if js is not None:
             sec_js, y_js = js
             ref = O.ssd(*sub)
             cb["js_single_thread"] = {
-                "value": Lj / (sec_js * H / Hj), "unit": "tokens/s", "cores": 1,
-                "kind": "port",
-                "sample": f"B=1, L={Lj}, {Hj} of {H} heads, scaled to all heads; "
-                          "oracle/ssm_ref.js under Node (double arithmetic, float32 storage)",
-                "agrees_with_c_oracle": bool(np.array_equal(y_js, ref))}
+                "value": Lj / sec_js, "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"B=1, L={Lj}, all {H} heads ({sec_js:.1f} s); oracle/ssm_ref.js "
+                          "under Node (double arithmetic, float32 storage)",
+                # both compute in double and store float32; Node's Math.exp and the C
+                # library's exp may differ in the last bit, so an output can land on the other
+                # side of a float32 rounding: agreement is within 1e-6 of the output's scale
+                "max_diff_vs_c_oracle": float(np.abs(y_js.astype(np.float64) - ref).max()
+                                              / max(1.0, float(np.abs(ref).max()))),
+                "bitwise_equal_to_c_oracle": bool(np.array_equal(y_js, ref))}
+            cb["js_single_thread"]["agrees_with_c_oracle"] = (
+                cb["js_single_thread"]["max_diff_vs_c_oracle"] <= 1e-6)
         out["cpu_baseline"] = cb
     return out
 
