@@ -21,9 +21,9 @@
 //
 // The internal chunk (Q = 64) is independent of the model's chunkLen: the chunked algorithm
 // is exact for any chunk length. Long single sequences are cut into segments so that
-// B*H*segments workgroups fill the chip: a state-only pass gives each segment's local final
-// state and total decay, a combine pass turns them into each segment's entering state, and
-// the full pass starts each segment from it.
+// B*H*segments workgroups fill the chip: a state-only pass (ssd_state_kernel) gives each
+// segment's local final state and total decay, a combine pass (ssd_seg_prefix) turns them into
+// each segment's entering state, and the full pass (ssd_kernel) starts each segment from it.
 #include <algorithm>
 #include <type_traits>
 
