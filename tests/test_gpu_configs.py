@@ -9,7 +9,8 @@ through the C ABI, against the CPU oracle on the same seeded inputs and weights.
         conv over the 4352 xBC channels -> SSD -> gated RMSNorm -> out_proj.
   cfg4  the recurrent decode step of a Mamba-2 model with cfg4's layer and vocabulary
         dimensions (d_model 1024, 32 heads x 64, d_state 128, vocab 32000) for 64 cached
-        sequences (state ~ N(0, 0.1)), two layers so the oracle stays fast: the
+        sequences (state ~ N(0, 0.1)), two layers over five steps, and the whole 24-layer
+        model over three steps: the
         model.generate path (src/session/session.ts:421-425) through the fused layer step
         (in_proj with the RMSNorm scale and the conv update in its epilogue, the state update
         with the gated norm's element-wise part, out_proj with the residual add and the next
@@ -175,3 +176,13 @@ def test_mamba1_decode_step(device, monkeypatch, Bsz):
     cfg = {"vocabSize": 8192, "dModel": 768, "numLayers": 2, "dState": 16, "dConv": 4,
            "expand": 2, "nHeads": 12, "dtRank": 48, "layers": [{"type": "mamba1"}] * 2}
     _decode_vs_oracle(device, monkeypatch, cfg, Bsz, 5, 1005)
+
+
+def test_cfg4_decode_step_24_layers(device, monkeypatch):
+    """The whole cfg4 model: 24 Mamba-2 layers, d_model 1024, 32 heads x 64, d_state 128,
+    vocab 32000, 64 cached sequences; three decode steps, eager and graph-replayed, logits and
+    every layer's state against the oracle."""
+    case("cfg4 decode d1024 H32 P64 N128 V32000, 64 sequences, 24 layers")
+    cfg = {"vocabSize": 32000, "dModel": 1024, "numLayers": 24, "dState": 128, "dConv": 4,
+           "expand": 2, "nHeads": 32, "nGroups": 1, "layers": [{"type": "mamba2"}] * 24}
+    _decode_vs_oracle(device, monkeypatch, cfg, 64, 3, 1014)
