@@ -1,12 +1,14 @@
 """GPU parity at the benchmark configurations' own dimensions,
 through the C ABI, against the CPU oracle on the same seeded inputs and weights.
 
-  cfg2  one Mamba-1 block (d_model 768, d_inner 1536, d_state 16, dt_rank 48, conv 4):
+  cfg2  one Mamba-1 block (d_model 768, d_inner 1536, d_state 16, dt_rank 48, conv 4), up
+        to the whole workload (B=4, L=2048):
         ssm_mixer_forward_device = in_proj -> conv1d/SiLU -> x_proj/dt_proj -> selective
         scan (D skip, SiLU(z) gate) -> out_proj; the Linear layers behind model.forward
         (src/session/streaming.ts:31-35).
-  cfg3  one Mamba-2 layer (d_model 2048, 64 heads x 64, d_state 128, one group): in_proj ->
-        conv over the 4352 xBC channels -> SSD -> gated RMSNorm -> out_proj.
+  cfg3  one Mamba-2 layer (d_model 2048, 64 heads x 64, d_state 128, one group), up to the
+        whole workload (B=8, L=4096): in_proj -> conv over the 4352 xBC channels -> SSD ->
+        gated RMSNorm -> out_proj.
   cfg4  the recurrent decode step of a Mamba-2 model with cfg4's layer and vocabulary
         dimensions (d_model 1024, 32 heads x 64, d_state 128, vocab 32000) for 64 cached
         sequences (state ~ N(0, 0.1)), two layers over five steps, and the whole 24-layer
@@ -87,10 +89,11 @@ def _mixer_vs_oracle(device, cfg, B, L, seed):
     return got, ref
 
 
-@pytest.mark.parametrize("B,L", [(2, 700), (4, 300)])
+@pytest.mark.parametrize("B,L", [(2, 700), (4, 300), (4, 2048)])
 def test_cfg2_mamba1_block(device, B, L):
     """cfg2's block dimensions. B = 2, L = 700: the scan cuts time into many chunks (too few
-    channels for one wave per SIMD); B = 4 (cfg2's batch): the single-pass scan."""
+    channels for one wave per SIMD); B = 4 (cfg2's batch): the single-pass scan; B = 4,
+    L = 2048: the whole cfg2 workload."""
     case(f"cfg2 Mamba-1 block d768 D1536 N16 R48 K4, B={B} L={L}")
     cfg = {"vocabSize": 16, "dModel": 768, "numLayers": 1, "dState": 16, "dConv": 4,
            "expand": 2, "nHeads": 12, "dtRank": 48, "layers": [{"type": "mamba1"}]}
@@ -98,13 +101,15 @@ def test_cfg2_mamba1_block(device, B, L):
     check_close(got, ref, "block output")
 
 
-def test_cfg3_mamba2_layer(device):
-    """cfg3's layer dimensions (d_model 2048, H 64, P 64, N 128, G 1), B = 1, L = 512: the
-    fp32 layer around the SSD, with the SSD run on fp32 inputs."""
-    case("cfg3 Mamba-2 layer d2048 H64 P64 N128, B=1 L=512")
+@pytest.mark.parametrize("B,L", [(1, 512), (8, 4096)])
+def test_cfg3_mamba2_layer(device, B, L):
+    """cfg3's layer dimensions (d_model 2048, H 64, P 64, N 128, G 1): one sequence of 512 steps
+    and the whole cfg3 workload (8 sequences of 4096). The fp32 layer around the SSD, with the
+    SSD run on fp32 inputs."""
+    case(f"cfg3 Mamba-2 layer d2048 H64 P64 N128, B={B} L={L}")
     cfg = {"vocabSize": 16, "dModel": 2048, "numLayers": 1, "dState": 128, "dConv": 4,
            "expand": 2, "nHeads": 64, "nGroups": 1, "layers": [{"type": "mamba2"}]}
-    got, ref = _mixer_vs_oracle(device, cfg, 1, 512, 1003)
+    got, ref = _mixer_vs_oracle(device, cfg, B, L, 1003)
     check_close(got, ref, "layer output")
 
 
