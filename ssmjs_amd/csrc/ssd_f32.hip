@@ -2,11 +2,14 @@
 // arithmetic on the gfx950 fp32 matrix cores (v_mfma_f32_16x16x4_f32), so every product and
 // sum is an fp32 operation, as in the fp32 WGSL kernels this backend replaces.
 //
-// Work split. One workgroup owns one (batch, segment, head); its four waves own the four
-// 16-row blocks of the head dim (wave w: p = 16w .. 16w+15) and walk the segment's chunks of
-// QF = 32 time steps in order. A small chunk is the cheaper one here: the state never leaves
-// the registers, so nothing is paid per chunk in memory, while the quadratic in-chunk terms
-// (C B^T and its product with X) shrink with the chunk.
+// Work split. One workgroup owns one (batch, segment) and HPW heads of one group (two when
+// the heads per group are even, else one); four waves per head own the four 16-row blocks of
+// the head dim (wave w of a head: p = 16w .. 16w+15) and walk the segment's chunks of
+// QF = 32 time steps in order. B, C and the raw C B^T tiles depend on the group only, so a
+// two-head workgroup stages B and C once and forms each C B^T tile once, scaled into both
+// heads' M^T. A small chunk is the cheaper one here: the state never leaves the registers,
+// so nothing is paid per chunk in memory, while the quadratic in-chunk terms (C B^T and its
+// product with X) shrink with the chunk.
 //
 // Per chunk, with acum_t the running sum of dt' A_h over the chunk (kept in log2 units):
 //   M^T[i][j] = (C B^T)[i][j] * 2^(acum_i - acum_j) * dt'_j  (j <= i),  + D_h on j == i
@@ -74,18 +77,18 @@ struct F32Args {
     float* ssq;
 };
 
-template <int NN, bool FULL, bool GATED>
+template <int NN, bool FULL, bool GATED, int HPW>
 struct SmemF32 {
     static constexpr int BP = NN + 4;    // B / C row pitch (floats): b128 rows conflict-free
     static constexpr int MP = QF + 4;    // M^T row pitch
     float b[2][QF][BP];                                  // B (j, n), two chunks
     float c[FULL ? 2 : 1][FULL ? QF : 1][BP];            // C (i, n), two chunks
-    float m[FULL ? QF : 1][MP];                          // M^T (i, j)
-    float ac[2][QF];    // acum_t in log2 units
-    float dv[2][QF];    // dt'_t
-    float wj[2][QF];    // w_t = 2^(acum_end - acum_t) dt'_t
-    float ae[2];        // acum_end
-    float sq[GATED ? 2 : 1][GATED ? 4 : 1][GATED ? QF : 1];   // per-wave sums of u^2 per row
+    float m[HPW][FULL ? QF : 1][MP];                     // M^T (i, j) per head
+    float ac[2][HPW][QF];    // acum_t in log2 units
+    float dv[2][HPW][QF];    // dt'_t
+    float wj[2][HPW][QF];    // w_t = 2^(acum_end - acum_t) dt'_t
+    float ae[2][HPW];        // acum_end
+    float sq[GATED ? 2 : 1][HPW][GATED ? 4 : 1][GATED ? QF : 1];   // per-wave sums of u^2 per row
 };
 
 using ssm::bload16;
@@ -113,16 +116,17 @@ __device__ __forceinline__ float wave_prefix_sum(float v) {
 
 __device__ __forceinline__ float4 as_f4(floatx4 v) { return make_float4(v[0], v[1], v[2], v[3]); }
 
-template <int NN, bool FULL, bool GATED = false>
-__global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
-    __shared__ __attribute__((aligned(16))) SmemF32<NN, FULL, GATED> sm;
-    using SM = SmemF32<NN, FULL, GATED>;
+template <int NN, bool FULL, bool GATED = false, int HPW = 1>
+__global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
+    static_assert(FULL || HPW == 1, "the state-only pass takes one head per workgroup");
+    __shared__ __attribute__((aligned(16))) SmemF32<NN, FULL, GATED, HPW> sm;
+    using SM = SmemF32<NN, FULL, GATED, HPW>;
     constexpr int NB = NN / 16;          // n blocks (state tiles per wave, k groups of C B^T)
     constexpr int QB = QF / 16;          // time blocks per chunk
     constexpr int NCB = QB * (QB + 1) / 2;   // causal C B^T tiles per chunk
     static_assert(NCB == 3, "three tiles over four waves: one wave per chunk has no tile");
     constexpr int RL = NN / 4;           // lanes per staged B / C row (one float4 each)
-    constexpr int RPP = 256 / RL;        // rows per staging pass
+    constexpr int RPP = 256 * HPW / RL;  // rows per staging pass
     constexpr int SP = QF / RPP;         // staging passes
 
     int wg = blockIdx.x;
@@ -131,20 +135,30 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         wg = (blockIdx.x % 8) * per + blockIdx.x / 8;
     }
     // segment-major: the heads of one (batch, segment) are adjacent and, after the remap, on
-    // one XCD, where they share that segment's B and C rows through L2
-    const int seg = wg / (a.B * a.H);
-    const int bh = wg % (a.B * a.H);
-    const int b = bh / a.H, h = bh % a.H;
-    const int g = h / (a.H / a.G);
+    // one XCD, where they share that segment's B and C rows through L2. With HPW = 2 the
+    // workgroup takes heads 2k and 2k + 1 of one group: wave w works on head w / 4 of the
+    // workgroup (its state rows p = 16 (w % 4) .. + 15), and B, C and the C B^T tiles serve
+    // both heads.
+    const int HW = a.H / HPW;
+    const int seg = wg / (a.B * HW);
+    const int bhw = wg % (a.B * HW);
+    const int b = bhw / HW;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hw = w >> 2, wl = w & 3;
+    const int h0w = HPW * (bhw % HW);    // the workgroup's first head
+    const int h = h0w + hw;
+    const int bh = b * a.H + h;
+    const int g = h / (a.H / a.G);
     const int l16 = lane & 15, q4 = lane >> 4;
-    const int p0 = 16 * w;
+    const int p0 = 16 * wl;
     const int sr = tid / RL, sc4 = 4 * (tid % RL);   // staging row / column
 
     const float Ah = a.A[h] * ssm::kLog2e;
     const float dtb = a.dt_bias ? a.dt_bias[h] : 0.f;
-    const float Dh = a.Dsk ? a.Dsk[h] : 0.f;
+    float Dh[HPW];   // D of the workgroup's heads (the C B^T tiles serve them all)
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) Dh[k] = a.Dsk ? a.Dsk[h0w + k] : 0.f;
     // gated output: this lane's four norm weights (columns p0 + 4 q4 .. + 3 of the head)
     float4 gw = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (GATED) gw = *reinterpret_cast<const float4*>(a.gn + (long)h * PF + p0 + 4 * q4);
@@ -158,13 +172,15 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     const float* cm0 = a.Cm + brow * a.ldc + (long)g * NN;
     const float* d0 = a.dt + brow * a.lddt + h;
     auto rows_of = [&](int c) { return c < c_end ? min(QF, a.L - c * QF) : 0; };
-    // ssq[(b L + t) H + h] for row tid of chunk c from the four waves' partial sums
+    // ssq[(b L + t) H + h] for row t of chunk c and head h0w + tid / QF from the head's four
+    // waves' partial sums (threads tid < HPW QF)
     auto flush_ssq = [&](int c, int bf) {
-        const int t = c * QF + tid;
+        const int hk = tid / QF, tt = tid % QF;
+        const int t = c * QF + tt;
         if (t < a.L) {
-            const float v = (sm.sq[bf][0][tid] + sm.sq[bf][1][tid]) +
-                            (sm.sq[bf][2][tid] + sm.sq[bf][3][tid]);
-            a.ssq[(brow + t) * a.H + h] = v;
+            const float v = (sm.sq[bf][hk][0][tt] + sm.sq[bf][hk][1][tt]) +
+                            (sm.sq[bf][hk][2][tt] + sm.sq[bf][hk][3][tt]);
+            a.ssq[(brow + t) * a.H + h0w + hk] = v;
         }
     };
     auto span = [](int qv, long ld, int width) {
@@ -172,7 +188,9 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
     };
 
     // C B^T tiles rotate over the waves from one workgroup to the next, so that no SIMD always
-    // gets the wave with the most (or no) tiles; the wave without a tile scans the next chunk
+    // gets the wave with the most (or no) tiles; the wave without a tile scans the next chunk.
+    // With two heads the first head's waves form the tiles (for both heads) and wave
+    // scan_wave of each head scans that head's next chunk.
     const int rot = blockIdx.x & 3;
     const int scan_wave = (NCB + rot) & 3;
 
@@ -191,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         // dt: one strided 4-byte value per step (a cache line per lane); in the full pass only
         // the wave that scans fetches it, the others get an empty descriptor (no traffic)
         const auto rd = rsrc(d0 + (long)cd * QF * a.lddt,
-                             (FULL && w != scan_wave) ? 0u : span(rows_of(cd), a.lddt, 1));
+                             (FULL && wl != scan_wave) ? 0u : span(rows_of(cd), a.lddt, 1));
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, 16));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN));
         raw.dt = bload4(rd, (unsigned)(lane * a.lddt) * 4u);
@@ -240,11 +258,11 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         const float ae = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), QF - 1));
         if (lane < QF) {
-            sm.ac[bf][lane] = sc;
-            sm.dv[bf][lane] = dv;
-            sm.wj[bf][lane] = ssm::ex2(ae - sc) * dv;
+            sm.ac[bf][hw][lane] = sc;
+            sm.dv[bf][hw][lane] = dv;
+            sm.wj[bf][hw][lane] = ssm::ex2(ae - sc) * dv;
         }
-        if (lane == 0) sm.ae[bf] = ae;
+        if (lane == 0) sm.ae[bf][hw] = ae;
     };
 
     if constexpr (FULL) {
@@ -252,7 +270,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         // while the others form their tiles); dt of the second chunk comes with the inputs
         const int qv0 = rows_of(c_begin);
         const auto rd0 = rsrc(d0 + (long)c_begin * QF * a.lddt, span(qv0, a.lddt, 1));
-        if (w == 0) scan_put(c_begin, bload4(rd0, (unsigned)(lane * a.lddt) * 4u), c_begin & 1);
+        if (wl == 0) scan_put(c_begin, bload4(rd0, (unsigned)(lane * a.lddt) * 4u), c_begin & 1);
         load_raw(c_begin, c_begin + 1);
     } else {
         load_raw(c_begin, c_begin);
@@ -282,9 +300,9 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
                 float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), QF - 1));
             decay_sum += acend;
             if (w == 0 && lane < QF) {
-                sm.ac[buf][lane] = sc;
-                sm.dv[buf][lane] = dv;
-                sm.wj[buf][lane] = ssm::ex2(acend - sc) * dv;
+                sm.ac[buf][0][lane] = sc;
+                sm.dv[buf][0][lane] = dv;
+                sm.wj[buf][0][lane] = ssm::ex2(acend - sc) * dv;
             }
         }
         // ---- stage B (and C) rows
@@ -305,17 +323,17 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
         if constexpr (!FULL) load_raw(c + 1, c + 1);
         if constexpr (GATED) {
             // the previous chunk's row sums of u^2, added over the four waves in order
-            if (c > c_begin && tid < QF) flush_ssq(c - 1, buf ^ 1);
+            if (c > c_begin && tid < HPW * QF) flush_ssq(c - 1, buf ^ 1);
         }
 
         if constexpr (FULL) {
             // ---- M^T tiles of C B^T (this wave's share of the causal tiles)
             // the wave without a tile scans chunk c + 1 into the other buffers (the last reads
             // of those, chunk c - 1's, came before barrier 1)
-            if (w == scan_wave) scan_put(c + 1, dnext, buf ^ 1);
+            if (wl == scan_wave) scan_put(c + 1, dnext, buf ^ 1);
 #pragma unroll
             for (int t = 0; t < NCB; ++t) {
-                if (((t + rot) & 3) != w) continue;
+                if (hw != 0 || ((t + rot) & 3) != wl) continue;
                 // tile t -> (ib, jb) with jb <= ib, row-major over the lower triangle
                 int ib = 0, jb = t;
                 while (jb > ib) { jb -= ib + 1; ++ib; }
@@ -346,22 +364,26 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
                     acc0 = mfma4(o[0].w, o[1].w, acc0);
                     acc1 = mfma4(o[2].w, o[3].w, acc1);
                 }
-                // acc[r] = (C B^T)[i = 16 ib + l16][j = 16 jb + 4 q4 + r]
+                // acc[r] = (C B^T)[i = 16 ib + l16][j = 16 jb + 4 q4 + r]; M^T of each head
                 const int i = 16 * ib + l16;
-                const float aci = sm.ac[buf][i];
-                const float4 acj = *reinterpret_cast<const float4*>(&sm.ac[buf][16 * jb + 4 * q4]);
-                const float4 dvj = *reinterpret_cast<const float4*>(&sm.dv[buf][16 * jb + 4 * q4]);
-                const float acja[4] = {acj.x, acj.y, acj.z, acj.w};
-                const float dvja[4] = {dvj.x, dvj.y, dvj.z, dvj.w};
-                float mv[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int j = 16 * jb + 4 * q4 + r;
-                    // the masked (j > i) exponent may overflow: select, never multiply by 0
-                    const float f = (acc0[r] + acc1[r]) * (ssm::ex2(aci - acja[r]) * dvja[r]);
-                    mv[r] = j < i ? f : (j == i ? f + Dh : 0.f);
+                for (int k = 0; k < HPW; ++k) {
+                    const float aci = sm.ac[buf][k][i];
+                    const float4 acj = *reinterpret_cast<const float4*>(&sm.ac[buf][k][16 * jb + 4 * q4]);
+                    const float4 dvj = *reinterpret_cast<const float4*>(&sm.dv[buf][k][16 * jb + 4 * q4]);
+                    const float acja[4] = {acj.x, acj.y, acj.z, acj.w};
+                    const float dvja[4] = {dvj.x, dvj.y, dvj.z, dvj.w};
+                    float mv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int j = 16 * jb + 4 * q4 + r;
+                        // the masked (j > i) exponent may overflow: select, never multiply by 0
+                        const float f = (acc0[r] + acc1[r]) * (ssm::ex2(aci - acja[r]) * dvja[r]);
+                        mv[r] = j < i ? f : (j == i ? f + Dh[k] : 0.f);
+                    }
+                    *reinterpret_cast<float4*>(&sm.m[k][i][16 * jb + 4 * q4]) =
+                        make_float4(mv[0], mv[1], mv[2], mv[3]);
                 }
-                *reinterpret_cast<float4*>(&sm.m[i][16 * jb + 4 * q4]) = make_float4(mv[0], mv[1], mv[2], mv[3]);
             }
             __syncthreads();   // M^T visible
             load_raw(c + 1, c + 2);
@@ -394,13 +416,13 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
                         }
                 }
 #pragma unroll
-                for (int ib = 0; ib < QB; ++ib) Y[ib] *= ssm::ex2(sm.ac[buf][16 * ib + l16]);
+                for (int ib = 0; ib < QB; ++ib) Y[ib] *= ssm::ex2(sm.ac[buf][hw][16 * ib + l16]);
             }
 #pragma unroll
             for (int ib = 0; ib < QB; ++ib)
 #pragma unroll
                 for (int jb = 0; jb <= ib; ++jb) {
-                    const float4 mv = *reinterpret_cast<const float4*>(&sm.m[16 * ib + l16][16 * jb + 4 * q4]);
+                    const float4 mv = *reinterpret_cast<const float4*>(&sm.m[hw][16 * ib + l16][16 * jb + 4 * q4]);
                     Y[ib] = mfma4(xv[jb][0], mv.x, Y[ib]);
                     Y[ib] = mfma4(xv[jb][1], mv.y, Y[ib]);
                     Y[ib] = mfma4(xv[jb][2], mv.z, Y[ib]);
@@ -421,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
                     float ss = (u0 * u0 + u1 * u1) + (u2 * u2 + u3 * u3);
                     ss += __shfl_xor(ss, 16);
                     ss += __shfl_xor(ss, 32);
-                    if (q4 == 0) sm.sq[buf][w][16 * ib + l16] = ss;
+                    if (q4 == 0) sm.sq[buf][hw][wl][16 * ib + l16] = ss;
                     bstore16(make_float4(u0 * gw.x, u1 * gw.y, u2 * gw.z, u3 * gw.w), ry,
                              (unsigned)((16 * ib + l16) * a.ldy + p0 + 4 * q4) * 4u);
                 }
@@ -434,7 +456,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 
         // ---- state: S^T = 2^acum_end S^T + sum_j B[j][n] (X[j][p] w_j)
         {
-            if constexpr (FULL) acend = sm.ae[buf];
+            if constexpr (FULL) acend = sm.ae[buf][hw];
             const float e = ssm::ex2(acend);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) S[nb] *= e;
@@ -444,7 +466,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
             float xw[QB][4];
 #pragma unroll
             for (int jb = 0; jb < QB; ++jb) {
-                const float4 wv = *reinterpret_cast<const float4*>(&sm.wj[buf][16 * jb + 4 * q4]);
+                const float4 wv = *reinterpret_cast<const float4*>(&sm.wj[buf][hw][16 * jb + 4 * q4]);
                 xw[jb][0] = xv[jb][0] * wv.x;
                 xw[jb][1] = xv[jb][1] * wv.y;
                 xw[jb][2] = xv[jb][2] * wv.z;
@@ -470,7 +492,7 @@ __global__ __launch_bounds__(256, 2) void ssd_f32_kernel(F32Args a) {
 
     if constexpr (GATED) {
         __syncthreads();
-        if (c_end > c_begin && tid < QF) flush_ssq(c_end - 1, (c_end - 1) & 1);
+        if (c_end > c_begin && tid < HPW * QF) flush_ssq(c_end - 1, (c_end - 1) & 1);
     }
 
     // ---- outputs of the state
@@ -520,10 +542,17 @@ ssm_status launch(F32Args& a, hipStream_t st) {
         e = ssm::check_launch("ssd_f32_seg_prefix");
         if (e != SSM_OK) return e;
     }
-    const int nwg = a.B * a.H * a.nseg;
+    // two heads per workgroup when heads 2k and 2k + 1 share a group
+    const int hpw = ((a.H / a.G) % 2 == 0) ? 2 : 1;
+    const int nwg = a.B * (a.H / hpw) * a.nseg;
     a.remap = (nwg % 8 == 0) ? 1 : 0;
-    if (a.ssq) ssd_f32_kernel<NN, true, true><<<nwg, 256, 0, st>>>(a);
-    else ssd_f32_kernel<NN, true><<<nwg, 256, 0, st>>>(a);
+    if (hpw == 2) {
+        if (a.ssq) ssd_f32_kernel<NN, true, true, 2><<<nwg, 512, 0, st>>>(a);
+        else ssd_f32_kernel<NN, true, false, 2><<<nwg, 512, 0, st>>>(a);
+    } else {
+        if (a.ssq) ssd_f32_kernel<NN, true, true><<<nwg, 256, 0, st>>>(a);
+        else ssd_f32_kernel<NN, true><<<nwg, 256, 0, st>>>(a);
+    }
     return ssm::check_launch("ssd_f32_chunk_scan");
 }
 
