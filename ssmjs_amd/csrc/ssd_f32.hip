@@ -199,10 +199,11 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
         float x[QB][4];
         float4 b[SP];
         float4 c[FULL ? SP : 1];
+        float4 z[GATED ? QB : 1];   // gated output: z of the lane's y pieces
         float dt;
     } raw;
-    // x, B, C of chunk c and dt of chunk cd (the full pass reads dt one chunk further ahead:
-    // its scan runs a chunk early, below)
+    // x, B, C (and z) of chunk c and dt of chunk cd (the full pass reads dt one chunk further
+    // ahead: its scan runs a chunk early, below)
     auto load_raw = [&](int c, int cd) {
         const int qv = rows_of(c);
         const long r0 = (long)c * QF;
@@ -226,6 +227,13 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
 #pragma unroll
             for (int k = 0; k < SP; ++k)
                 raw.c[k] = bload16<float4>(rc, (unsigned)((sr + RPP * k) * a.ldc + sc4) * 4u);
+        }
+        if constexpr (GATED) {
+            // issued last: the chunk's first wait (for B and C) does not wait for them
+            const auto rz = rsrc(a.z + (brow + r0) * a.ldz + (long)h * PF, span(qv, a.ldz, PF));
+#pragma unroll
+            for (int ib = 0; ib < QB; ++ib)
+                raw.z[ib] = bload16<float4>(rz, (unsigned)((16 * ib + l16) * a.ldz + p0 + 4 * q4) * 4u);
         }
     };
 
@@ -386,6 +394,10 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
                 }
             }
             __syncthreads();   // M^T visible
+            // this chunk's z leaves the prefetch registers before the next chunk's loads
+            float4 zc[GATED ? QB : 1];
+#pragma unroll
+            for (int ib = 0; ib < (GATED ? QB : 1); ++ib) zc[ib] = raw.z[ib];
             load_raw(c + 1, c + 2);
 
             // ---- Y^T[p][i] for the wave's 16 p and the chunk's QF rows i
@@ -433,11 +445,9 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
             if constexpr (GATED) {
                 // u = y silu(z) and u * gn; the row's sum of u^2 over this wave's 16 columns
                 // (lane groups q4 added pairwise with xor shuffles: the same bits in each)
-                const auto rz = rsrc(a.z + row0 * a.ldz + (long)h * PF, span(qv, a.ldz, PF));
 #pragma unroll
                 for (int ib = 0; ib < QB; ++ib) {
-                    const float4 zv =
-                        bload16<float4>(rz, (unsigned)((16 * ib + l16) * a.ldz + p0 + 4 * q4) * 4u);
+                    const float4 zv = zc[ib];
                     const float u0 = Y[ib][0] * ssm::silu(zv.x), u1 = Y[ib][1] * ssm::silu(zv.y);
                     const float u2 = Y[ib][2] * ssm::silu(zv.z), u3 = Y[ib][3] * ssm::silu(zv.w);
                     float ss = (u0 * u0 + u1 * u1) + (u2 * u2 + u3 * u3);
