@@ -389,6 +389,21 @@ def ssd_alg(B, L, H, P, N, esz, Q=256):
     return flops, nbytes
 
 
+def ssd_f32_issued_flops(B, L, H, G, N, P=64):
+    """The MFMA work ssd_f32_kernel issues per launch (16x16x4 fp32 MFMAs, 2048 FLOPs each).
+    Chunks of 32 steps; a workgroup owns HPW heads of one group (2 when the heads per group
+    are even) and forms the group's three causal 16x16 C B^T tiles once for them (N / 4
+    MFMAs each). Each head's four waves (16 rows of the head dim each) then issue, per chunk:
+    state-to-output 2 x (N / 4), diagonal part 3 x 4 (the causal 16-step blocks), state
+    update (N / 16) x 2 x 4."""
+    qf = 32
+    hpw = 2 if (H // G) % 2 == 0 else 1
+    cbt = 3 * (N // 4)                                   # per workgroup and chunk
+    per_wave = 2 * (N // 4) + 3 * 4 + (N // 16) * 2 * 4
+    per_chunk_head = cbt / hpw + (P // 16) * per_wave
+    return per_chunk_head * 2048.0 * (B * L / qf) * H
+
+
 def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, with_cpu=True):
     from ssmjs_amd import kernels
     P, N = 64, 128
@@ -419,14 +434,15 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, wit
            "roofline": roofline(kern, ms, flops, nbytes, prec, traffic=TRAFFIC.get(key),
                                 traffic_key=key)}
     rl = out["roofline"]
+    # mfma_frac: the SURVEY's algorithmic FLOPs (causal count at the config's chunk length
+    # 256) per second against the dense peak, i.e. the algorithmic-equivalent rate
     rl["mfma_frac"] = round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[prec], 4)
+    rl["mfma_frac_basis"] = "algorithmic FLOPs at chunk 256 (SURVEY 8d) / dense peak"
     rl["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     if dtype == "f32":
-        # the kernel's own MFMA work per launch: 32-step chunks, 16x16 tiles (the diagonal
-        # C B^T tiles whole), C B^T once per head
-        QF = 32
-        per_chunk_head = 3 * 32 + 4 * (2 * 32 + 3 * 4 + 2 * 32)   # 16x16x4 MFMAs
-        rl["issued_mfma_flops"] = per_chunk_head * 2048.0 * (T / QF) * H
+        rl["issued_mfma_flops"] = ssd_f32_issued_flops(B, L, H, 1, N)
+        rl["issued_mfma_frac"] = round(rl["issued_mfma_flops"] / (ms * 1e-3) / 1e12
+                                       / PEAK_TFLOPS[prec], 4)
     if with_cpu and not args.no_cpu_baseline:
         from oracle import oracle as O
         # the whole workload (every sequence and head, the same inputs as fp32), repeated

@@ -53,6 +53,14 @@ typedef int ssm_status;
 const char* ssm_last_error(void);
 const char* ssm_status_name(ssm_status s);
 int ssm_abi_version(void);
+/* Failure injection for tests of the error contract (no counterpart in the reference; its
+ * GPU_UNAVAILABLE / CHECKPOINT_INVALID paths are session.ts:262-270,393-401): kind
+ * "nodevice" (ssm_ctx_create finds no device), "alloc" (every device allocation of the
+ * library fails with SSM_ERR_OUT_OF_MEMORY), "launch" (every launch check reports
+ * SSM_ERR_HIP after the kernel ran normally), "" (none). It holds for the whole process until
+ * the next call; NULL hands control back to the environment variable SSM_HIP_FAULT, which
+ * each ssm_ctx_create then reads. Unknown kinds: SSM_ERR_INVALID_ARG. */
+ssm_status ssm_set_fault_injection(const char* kind);
 
 /* ------------------------------------------------------------------ device context */
 typedef struct ssm_ctx ssm_ctx;

@@ -76,6 +76,7 @@ PROTOTYPES = {
     "ssm_last_error": (C.c_char_p, []),
     "ssm_status_name": (C.c_char_p, [_i]),
     "ssm_abi_version": (_i, []),
+    "ssm_set_fault_injection": (_i, [C.c_char_p]),
     "ssm_ctx_create": (_i, [_i, C.POINTER(_vp)]),
     "ssm_ctx_destroy": (_i, [_vp]),
     "ssm_ctx_set_stream": (_i, [_vp, _vp]),

@@ -17,11 +17,9 @@ void set_error(const char* fmt, ...);
 ssm_status fail(ssm_status code, const char* fmt, ...);
 // Map a HIP error from a launch or runtime call to SSM_ERR_HIP (or GPU_UNAVAILABLE / OOM).
 ssm_status from_hip(hipError_t e, const char* what);
-// hipGetLastError after a launch (SSM_HIP_FAULT=launch makes it report a failure).
+// hipGetLastError after a launch (an injected "launch" fault makes it report a failure).
 ssm_status check_launch(const char* what);
-// Whether SSM_HIP_FAULT names `kind` ("nodevice", "alloc", "launch").
-bool fault(const char* kind);
-// hipMalloc, failing with hipErrorOutOfMemory under SSM_HIP_FAULT=alloc.
+// hipMalloc, failing with hipErrorOutOfMemory under an injected "alloc" fault.
 hipError_t dev_malloc(void** p, size_t bytes);
 
 inline long cdiv(long a, long b) { return (a + b - 1) / b; }

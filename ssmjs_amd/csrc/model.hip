@@ -16,6 +16,7 @@
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -60,18 +61,35 @@ ssm_status from_hip(hipError_t e, const char* what) {
     return fail(code, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Fault injection for tests of the error contract (session.ts:262-270,393-401): the
-// environment variable SSM_HIP_FAULT names a failure the library reports as if HIP had
-// returned it. "nodevice": ssm_ctx_create finds no device; "alloc": every device allocation
-// of the library fails (out of memory); "launch": every launch check reports a failed launch
-// after the (normally running) kernel was queued. Read at each use, so a process can switch it.
-bool fault(const char* kind) {
-    const char* f = std::getenv("SSM_HIP_FAULT");
-    return f && std::strcmp(f, kind) == 0;
+// Fault injection for tests of the error contract (session.ts:262-270,393-401): a failure the
+// library reports as if HIP had returned it. "nodevice": ssm_ctx_create finds no device;
+// "alloc": every device allocation of the library fails (out of memory); "launch": every
+// launch check reports a failed launch after the (normally running) kernel was queued.
+// The kind lives in an atomic: ssm_set_fault_injection sets it (and pins it against the
+// environment until it is called with NULL); otherwise each ssm_ctx_create latches the
+// environment variable SSM_HIP_FAULT into it. Nothing reads the environment per launch or
+// allocation (getenv is not safe against a concurrent setenv on another thread).
+enum FaultKind { kFaultNone = 0, kFaultNoDevice, kFaultAlloc, kFaultLaunch, kFaultUnknown };
+std::atomic<int> g_fault{kFaultNone};
+std::atomic<bool> g_fault_pinned{false};
+
+int parse_fault(const char* f) {
+    if (!f || !*f) return kFaultNone;
+    if (std::strcmp(f, "nodevice") == 0) return kFaultNoDevice;
+    if (std::strcmp(f, "alloc") == 0) return kFaultAlloc;
+    if (std::strcmp(f, "launch") == 0) return kFaultLaunch;
+    return kFaultUnknown;
 }
 
+void latch_fault_env() {
+    if (!g_fault_pinned.load(std::memory_order_acquire))
+        g_fault.store(parse_fault(std::getenv("SSM_HIP_FAULT")), std::memory_order_release);
+}
+
+bool fault(int kind) { return g_fault.load(std::memory_order_relaxed) == kind; }
+
 hipError_t dev_malloc(void** p, size_t bytes) {
-    if (fault("alloc")) {
+    if (fault(kFaultAlloc)) {
         *p = nullptr;
         return hipErrorOutOfMemory;
     }
@@ -80,8 +98,8 @@ hipError_t dev_malloc(void** p, size_t bytes) {
 
 ssm_status check_launch(const char* what) {
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && fault("launch"))
-        return fail(SSM_ERR_HIP, "%s: launch failure (injected by SSM_HIP_FAULT=launch)", what);
+    if (e == hipSuccess && fault(kFaultLaunch))
+        return fail(SSM_ERR_HIP, "%s: launch failure (injected fault: launch)", what);
     return e == hipSuccess ? SSM_OK : from_hip(e, what);
 }
 
@@ -106,6 +124,20 @@ extern "C" const char* ssm_status_name(ssm_status s) {
 }
 
 extern "C" int ssm_abi_version(void) { return 1; }
+
+extern "C" ssm_status ssm_set_fault_injection(const char* kind) {
+    if (!kind) {
+        ssm::g_fault_pinned.store(false, std::memory_order_release);
+        ssm::g_fault.store(ssm::kFaultNone, std::memory_order_release);
+        return SSM_OK;
+    }
+    const int k = ssm::parse_fault(kind);
+    if (k == ssm::kFaultUnknown)
+        return ssm::fail(SSM_ERR_INVALID_ARG, "ssm_set_fault_injection: unknown kind '%s'", kind);
+    ssm::g_fault.store(k, std::memory_order_release);
+    ssm::g_fault_pinned.store(true, std::memory_order_release);
+    return SSM_OK;
+}
 
 // ------------------------------------------------------------------ context
 constexpr size_t kLtWorkspace = 32u << 20;   // hipBLASLt workspace per context
@@ -262,8 +294,9 @@ ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, co
 extern "C" ssm_status ssm_ctx_create(int device_ordinal, ssm_ctx** out) {
     if (!out) return ssm::fail(SSM_ERR_INVALID_ARG, "ssm_ctx_create: null out");
     *out = nullptr;
-    if (ssm::fault("nodevice"))
-        return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "no HIP device (SSM_HIP_FAULT=nodevice)");
+    ssm::latch_fault_env();
+    if (ssm::fault(ssm::kFaultNoDevice))
+        return ssm::fail(SSM_ERR_GPU_UNAVAILABLE, "no HIP device (injected fault: nodevice)");
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n == 0)

@@ -334,33 +334,41 @@ __global__ __launch_bounds__(64 * Scan1<N>::W) void scan_single_kernel(ScanArgs 
     const float Dd = (sdok && a.Dsk) ? a.Dsk[sd] : 0.f;
     const float spf = a.softplus ? 1.f : 0.f, gzf = a.z ? 1.f : 0.f;
 
-    // per-sequence descriptors: rows past L read zeros and take no stores
+    // Descriptors of block k (rows k TK .. k TK + TK - 1 of sequence b), rebuilt per block
+    // from wave-uniform values so that every offset stays within 32 bits however long the
+    // sequence is (the host checks TK rows of the widest stride fit): rows past L, and every
+    // row of the block past the last, read zeros and take no stores.
     const long r0 = (long)b * L;
-    const auto ru = ssm::rsrc(a.u + r0 * a.ldu, (unsigned)(((long)(L - 1) * a.ldu + D) * 4));
-    const auto rd = ssm::rsrc(a.dt + r0 * a.lddt, (unsigned)(((long)(L - 1) * a.lddt + D) * 4));
-    const auto rz = ssm::rsrc(a.z ? a.z + r0 * a.ldz : a.u, a.z ? (unsigned)(((long)(L - 1) * a.ldz + D) * 4) : 0u);
-    const auto rb = ssm::rsrc(a.Bm + r0 * a.ldb, (unsigned)(((long)(L - 1) * a.ldb + Nr) * 4));
-    const auto rc = ssm::rsrc(a.Cm + r0 * a.ldc, (unsigned)(((long)(L - 1) * a.ldc + Nr) * 4));
-    const auto ry = ssm::rsrc(a.y + r0 * a.ldy, (unsigned)(((long)(L - 1) * a.ldy + D) * 4));
+    auto blk = [&](const float* p, long ld, int width, int k) {
+        const int rows = min(TK, L - k * TK);
+        return rows > 0 ? ssm::rsrc(p + (r0 + (long)k * TK) * ld,
+                                    (unsigned)(((long)(rows - 1) * ld + width) * 4))
+                        : ssm::rsrc(p, 0u);
+    };
+    const float* zp = a.z ? a.z : a.u;
+    const long ldz = a.z ? a.ldz : 0;
 
     // Block k's values of this thread, loaded one block ahead. The offsets carry no select
     // (a lane-dependent `cond ? offset : out-of-range` was split by the compiler into two
     // branches, each with its own load, whose join waited for every load in flight): rows
-    // are clamped to L, which the descriptors read as zeros, and a channel past D or a state
-    // past Nr reads some in-range value that the staging never uses.
+    // past the block's last read zeros through the descriptor's range, and a channel past D
+    // or a state past Nr reads some in-range value that the staging never uses.
     float uv[UE], dv[UE], zv[UE], bv[BE], cv[BE];
     auto load = [&](int k) {
+        const auto ru = blk(a.u, a.ldu, D, k), rd = blk(a.dt, a.lddt, D, k);
+        const auto rz = a.z ? blk(zp, ldz, D, k) : ssm::rsrc(zp, 0u);
+        const auto rb = blk(a.Bm, a.ldb, Nr, k), rc = blk(a.Cm, a.ldc, Nr, k);
 #pragma unroll
         for (int e = 0; e < UE; ++e) {
-            const unsigned t = (unsigned)min(k * TK + st0 + e * SR, L);
+            const unsigned t = (unsigned)(st0 + e * SR);
             uv[e] = ssm::bload4(ru, (t * (unsigned)a.ldu + (unsigned)sd) * 4u);
             dv[e] = ssm::bload4(rd, (t * (unsigned)a.lddt + (unsigned)sd) * 4u);
-            zv[e] = ssm::bload4(rz, (t * (unsigned)a.ldz + (unsigned)sd) * 4u);
+            zv[e] = ssm::bload4(rz, (t * (unsigned)ldz + (unsigned)sd) * 4u);
         }
 #pragma unroll
         for (int j = 0; j < BE; ++j) {
             const int i = (tid + NT * j) % (TK * N), nn = i % N;
-            const unsigned t = (unsigned)min(k * TK + i / N, L);
+            const unsigned t = (unsigned)(i / N);
             bv[j] = ssm::bload4(rb, (t * (unsigned)a.ldb + (unsigned)nn) * 4u);
             cv[j] = ssm::bload4(rc, (t * (unsigned)a.ldc + (unsigned)nn) * 4u);
         }
@@ -444,11 +452,12 @@ __global__ __launch_bounds__(64 * Scan1<N>::W) void scan_single_kernel(ScanArgs 
             sm.ys[s0 + ot][cl2] = acc * sm.gz[s0 + ot][cl2];
         }
         __syncthreads();
+        const auto ry = blk(a.y, a.ldy, D, k);
 #pragma unroll
         for (int e = 0; e < UE; ++e) {
             // rows past L fall outside the descriptor (dropped); so does a channel past D
             const int st = st0 + e * SR;
-            const unsigned off = ((unsigned)(k * TK + st) * (unsigned)a.ldy + (unsigned)sd) * 4u;
+            const unsigned off = ((unsigned)st * (unsigned)a.ldy + (unsigned)sd) * 4u;
             ssm::bstore4(sm.ys[st][sc], ry, off | (sdok ? 0u : 0x80000000u));
         }
     }
@@ -610,16 +619,22 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
 
 namespace {
 int pad_n(int N) { return N <= 4 ? 4 : N <= 8 ? 8 : N <= 16 ? 16 : N <= 32 ? 32 : 64; }
-// The single pass addresses a sequence's rows of every input through 32-bit offsets.
-bool single_fits(int L, int D, long ld) { return ((long)(L - 1) * ld + D) * 4 < (1L << 31); }
-}  // namespace
-
-extern "C" size_t ssm_selective_scan_workspace(int B, int L, int D, int N) {
-    if (B <= 0 || L <= 0 || D <= 0 || N <= 0) return 0;
-    if (N <= 64 && single_ok(B, D, pad_n(N))) return 0;   // the single pass needs none
+// Both designs address rows through 32-bit offsets from a base they rebuild per block (single
+// pass: 128 rows) or per chunk (chunked passes: T rows), so a stride only has to fit that
+// many rows; the plan itself depends on (B, D, N) alone, and so does the workspace query.
+constexpr long kOffMax = 1L << 31;
+bool rows_fit(long rows, long ld, int D) { return ((rows - 1) * ld + D) * 4 < kOffMax; }
+size_t chunked_workspace(int B, int L, int D, int N) {
     const int T = pick_chunk(B, L, D);
     const long NC = ssm::cdiv(L, T);
     return sizeof(float) * (size_t)B * NC * D * ((size_t)N + 1);
+}
+}  // namespace
+
+extern "C" size_t ssm_selective_scan_workspace(int B, int L, int D, int N) {
+    if (B <= 0 || L <= 0 || D <= 0 || N <= 0 || N > 64) return 0;
+    if (single_ok(B, D, pad_n(N))) return 0;   // the single pass needs none
+    return chunked_workspace(B, L, D, N);
 }
 
 extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* dt, long lddt,
@@ -647,8 +662,11 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
     }
     const int Np = pad_n(N);
     const long ldmax = std::max({ldu, lddt, ldy, z ? ldz : 0L, ldb, ldc});
-    const bool single = single_ok(B, D, Np) && single_fits(L, D, ldmax);
-    const size_t need = single ? 0 : ssm_selective_scan_workspace(B, L, D, N);
+    const bool single = single_ok(B, D, Np);
+    const long rows = single ? std::min<long>(L, 128) : pick_chunk(B, L, D);
+    SSM_REQUIRE(rows_fit(rows, ldmax, D),
+                "ssm_selective_scan: row stride %ld too large for 32-bit block offsets", ldmax);
+    const size_t need = single ? 0 : chunked_workspace(B, L, D, N);
     SSM_REQUIRE(need == 0 || (workspace && workspace_bytes >= need),
                 "ssm_selective_scan: workspace of %zu bytes needed", need);
     ScanArgs a;
