@@ -59,6 +59,7 @@ struct GemmArgs {
     // row scale (RS): Y[m, :] = s[m] (X W^T)[m, :] + ..., s[m] = 1 / sqrt(inv_div *
     // sum_j ssq[m nssq + j] + eps) -- an RMSNorm of X's rows applied after the product
     const float* ssq; int nssq; float inv_div, eps;
+    int gate_c0;   // columns >= gate_c0 (a multiple of 16) are stored as silu(value)
 };
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
@@ -221,6 +222,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
         const int c = 16 * (NJ * wn + j) + i16;
         const unsigned oor = c < cols ? 0u : 0x80000000u;
         const float bv = a.bias && c < cols ? a.bias[n0 + c] : 0.f;
+        // the 16 columns of block j lie on one side of gate_c0: the choice is wave-uniform
+        const bool gate = n0 + 16 * (NJ * wn + j) >= a.gate_c0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -231,6 +234,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
                 if constexpr (RS) v *= rs[row];
                 v += bv;
                 if constexpr (BETA) v += a.beta * ssm::bload4(ry, off);
+                if (gate) v = ssm::silu_fast(v);
                 ssm::bstore4(v, ry, off);
             }
     }
@@ -265,7 +269,8 @@ void launch_nj(const GemmArgs& a, bool beta, hipStream_t st) {
 // ---------------------------------------------------------------- x_proj -> dt_proj
 // The Mamba-1 block's projections between the conv and the scan in one pass over xc:
 //   dbl = xc Wx^T           (T, R + 2N): dt_low | B | C, the scan's B and C operands
-//   dt  = dt_low Wdt^T      (T, D), the scan's dt before its bias and softplus
+//   dt  = dt_low Wdt^T      (T, D), the scan's dt before its bias and softplus, or, given
+//                           the bias, dt' = softplus(dt + bias) itself
 // A workgroup (8 waves) owns 32 rows (time steps). x_proj: wave w sums its eighth of K for
 // the 2 x NCB 16 x 16 tiles of the rows' dbl, with operand fragments read from global
 // memory straight into registers (one b128 per lane) through a ring of PD k blocks in
@@ -285,6 +290,7 @@ struct XdArgs {
     float* dbl; long lddbl;         // (T, RN)
     float* dt; long lddt;           // (T, D)
     int T, D, R, RN;
+    const float* dtb;               // given: dt = softplus(dt_low Wdt^T + dtb)
 };
 
 template <int NCB, int KB2, int PD>
@@ -410,12 +416,16 @@ __global__ __launch_bounds__(XD_ROWS * 16, 1) void xproj_dt_kernel(XdArgs a) {
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb) o[rb] = mfma4(xa[rb][kb][t], wd[buf][kb][t], o[rb]);
         const int c = 16 * cb + i16;
-        const unsigned oor = (cb < cb0 + cper && c < a.D) ? 0u : 0x80000000u;
+        const bool live = cb < cb0 + cper && c < a.D;
+        const unsigned oor = live ? 0u : 0x80000000u;
+        const float bias = (a.dtb && live) ? a.dtb[c] : 0.f;
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                ssm::bstore4(o[rb][r], rdt, ((unsigned)((16 * rb + 4 * q + r) * a.lddt + c) * 4u) | oor);
+            for (int r = 0; r < 4; ++r) {
+                const float v = a.dtb ? ssm::softplus_sel(o[rb][r] + bias) : o[rb][r];
+                ssm::bstore4(v, rdt, ((unsigned)((16 * rb + 4 * q + r) * a.lddt + c) * 4u) | oor);
+            }
     };
 #pragma unroll
     for (int u = 0; u < PD - 1; ++u) wfetch(u, cb0 + u);
@@ -463,13 +473,13 @@ bool xproj_dt_ok(int T, int D, int R, int N, long ldx, long lddbl, long lddt) {
 
 ssm_status launch_xproj_dt(const float* x, long ldx, const float* Wx, const float* Wdt,
                            float* dbl, long lddbl, float* dt, long lddt, int T, int D, int R,
-                           int N, hipStream_t st) {
+                           int N, hipStream_t st, const float* dt_bias) {
     if (!xproj_dt_ok(T, D, R, N, ldx, lddbl, lddt))
         return fail(SSM_ERR_INVALID_ARG, "xproj_dt: unsupported shape T %d D %d R %d N %d", T, D,
                     R, N);
     if (((uintptr_t)x | (uintptr_t)Wx | (uintptr_t)Wdt) & 15)
         return fail(SSM_ERR_INVALID_ARG, "xproj_dt: x, Wx, Wdt must be 16-byte aligned");
-    XdArgs a{x, ldx, Wx, Wdt, dbl, lddbl, dt, lddt, T, D, R, R + 2 * N};
+    XdArgs a{x, ldx, Wx, Wdt, dbl, lddbl, dt, lddt, T, D, R, R + 2 * N, dt_bias};
     // x_proj column tiles: 3, 4, 5, 6 or 8 (7 runs as 8; the extra tile reads zeros)
     const int ncb = (a.RN + 15) / 16, kb2 = (R + 15) / 16;
     if (ncb <= 3) launch_xd_k<3>(a, kb2, st);
@@ -491,7 +501,7 @@ bool gemm_ok(int M, int N, int K, long ldx, long ldw, long ldy) {
 
 ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const float* bias,
                        float* Y, long ldy, int M, int N, int K, float beta, hipStream_t st,
-                       const float* ssq, int nssq, float inv_div, float eps) {
+                       const float* ssq, int nssq, float inv_div, float eps, int gate_c0) {
     if (!gemm_ok(M, N, K, ldx, ldw, ldy))
         return fail(SSM_ERR_INVALID_ARG, "gemm: unsupported shape M %d N %d K %d ld %ld/%ld/%ld",
                     M, N, K, ldx, ldw, ldy);
@@ -499,7 +509,9 @@ ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const
         return fail(SSM_ERR_INVALID_ARG, "gemm: X and W must be 16-byte aligned");
     const int nj = pick_nj(M, N);
     GemmArgs a{X, ldx, W, ldw, Y, ldy, bias, M, N, K, beta, (M + BM - 1) / BM,
-               (N + 32 * nj - 1) / (32 * nj), ssq, nssq, inv_div, eps};
+               (N + 32 * nj - 1) / (32 * nj), ssq, nssq, inv_div, eps, gate_c0};
+    if (gate_c0 < N && gate_c0 % 16)
+        return fail(SSM_ERR_INVALID_ARG, "gemm: gate column %d not a multiple of 16", gate_c0);
     if (ssq && nssq <= 0) return fail(SSM_ERR_INVALID_ARG, "gemm: row scale needs nssq > 0");
     if ((long)a.mt * a.nt > (1L << 30)) return fail(SSM_ERR_INVALID_ARG, "gemm: too many tiles");
     const bool bt = beta != 0.f;

@@ -103,16 +103,26 @@ ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, fl
 // cores; with ssq, s[m] = 1 / sqrt(inv_div * sum_j ssq[m nssq + j] + eps) (a row RMSNorm of
 // X applied after the product), else 1.
 bool gemm_ok(int M, int N, int K, long ldx, long ldw, long ldy);
+// gate_c0 (a multiple of 16): columns n >= gate_c0 are stored as silu(value) (the Mamba-1
+// block's z half of in_proj, the scan's gate).
 ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const float* bias,
                        float* Y, long ldy, int M, int N, int K, float beta, hipStream_t st,
                        const float* ssq = nullptr, int nssq = 0, float inv_div = 0.f,
-                       float eps = 0.f);
+                       float eps = 0.f, int gate_c0 = 0x7fffffff);
 // The Mamba-1 block's x_proj and dt_proj in one pass (gemm.hip): dbl = x Wx^T (T, R + 2N),
-// dt = dbl[:, :R] Wdt^T (T, D).
+// dt = dbl[:, :R] Wdt^T (T, D); given dt_bias, dt = softplus(dbl[:, :R] Wdt^T + dt_bias) (the
+// scan's dt').
 bool xproj_dt_ok(int T, int D, int R, int N, long ldx, long lddbl, long lddt);
 ssm_status launch_xproj_dt(const float* x, long ldx, const float* Wx, const float* Wdt,
                            float* dbl, long lddbl, float* dt, long lddt, int T, int D, int R,
-                           int N, hipStream_t st);
+                           int N, hipStream_t st, const float* dt_bias = nullptr);
+// ssm_selective_scan (scan_m1.hip); zgated = 1: z already holds silu(z).
+ssm_status selective_scan(const float* u, long ldu, const float* dt, long lddt,
+                          const float* dt_bias, int softplus, const float* A, const float* Bm,
+                          long ldb, const float* Cm, long ldc, const float* Dsk, const float* z,
+                          long ldz, int zgated, float* y, long ldy, int B, int L, int D, int N,
+                          const float* h0, float* hT, void* workspace, size_t workspace_bytes,
+                          void* stream);
 // The Mamba-2 one-token state update with the gated RMSNorm's element-wise part:
 // y = (C.h + D x) * silu(z) * gn in fragment order (K = H P), and per workgroup the partial sum
 // of ((C.h + D x) silu(z))^2 into ssq (B, m2_gated_nssq(H, P, N)). ssd.hip.

@@ -756,24 +756,34 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
     if (Ly.type == SSM_LAYER_MAMBA1) {
         float *xz = w.a, *xc = w.b, *dbl = w.c, *dtv = w.d, *y = w.e;
         const int RN = d.R + 2 * d.N;
-        { Stage g(c, "m1.in_proj"); SSM_TRY(gemm(c, T, 2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
+        // With the own kernels on both sides, the scan's element-wise input work moves into
+        // its producers: in_proj stores silu(z) for the z half and x_proj/dt_proj stores
+        // dt' = softplus(dt + bias) (the same functions, so the same values).
+        const bool fused_xd = own_kernels(T) && ssm::xproj_dt_ok(T, d.D, d.R, d.N, d.D, RN, d.D) &&
+                              al16(W + Ly.x_proj) && al16(W + Ly.dt_w);
+        const bool pre = fused_xd && ssm::gemm_ok(T, 2 * d.D, d.d, d.d, d.d, 2 * d.D) &&
+                         al16(x) && al16(W + Ly.in_proj) && d.D % 16 == 0;
+        { Stage g(c, "m1.in_proj");
+          if (pre) SSM_TRY(ssm::launch_gemm(x, d.d, W + Ly.in_proj, d.d, nullptr, xz, 2 * d.D, T,
+                                            2 * d.D, d.d, 0.f, st, nullptr, 0, 0.f, 0.f, d.D));
+          else SSM_TRY(gemm(c, T, 2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
         { Stage g(c, "m1.conv");
           SSM_TRY(ssm_causal_conv1d(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, B, L, d.D,
                                     d.K, 1, conv_st, conv_st, st)); }
-        if (own_kernels(T) && ssm::xproj_dt_ok(T, d.D, d.R, d.N, d.D, RN, d.D) &&
-            al16(W + Ly.x_proj) && al16(W + Ly.dt_w)) {
+        if (fused_xd) {
             // x_proj and dt_proj in one pass (dt_low stays on chip)
             Stage g(c, "m1.x_dt_proj");
             SSM_TRY(ssm::launch_xproj_dt(xc, d.D, W + Ly.x_proj, W + Ly.dt_w, dbl, RN, dtv, d.D,
-                                         T, d.D, d.R, d.N, st));
+                                         T, d.D, d.R, d.N, st, pre ? W + Ly.dt_b : nullptr));
         } else {
             { Stage g(c, "m1.x_proj"); SSM_TRY(gemm(c, T, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
             { Stage g(c, "m1.dt_proj"); SSM_TRY(gemm(c, T, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
         }
         { Stage g(c, "m1.scan");
-          SSM_TRY(ssm_selective_scan(xc, d.D, dtv, d.D, W + Ly.dt_b, 1, A, dbl + d.R, RN,
-                                     dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D, y, d.D, B,
-                                     L, d.D, d.N, ssm_st, ssm_st, w.scan, w.scan_bytes, st)); }
+          SSM_TRY(ssm::selective_scan(xc, d.D, dtv, d.D, pre ? nullptr : W + Ly.dt_b, pre ? 0 : 1,
+                                      A, dbl + d.R, RN, dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D,
+                                      2 * d.D, pre ? 1 : 0, y, d.D, B, L, d.D, d.N, ssm_st, ssm_st,
+                                      w.scan, w.scan_bytes, st)); }
         { Stage g(c, "m1.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, y, d.D, W + Ly.out_proj, out, d.d, beta)); }
     } else {
         float *zx = w.a, *xbc = w.b, *y = w.c, *yn = w.d;

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kWave) void scan_chunk_output(
     const float* __restrict__ dt_bias, int softplus, const float* __restrict__ A,
     const float* __restrict__ Bm, long ldb, const float* __restrict__ Cm, long ldc,
     const float* __restrict__ Dsk, const float* __restrict__ z, long ldz, float* __restrict__ y,
-    long ldy, int L, int D, int Nr, int T, int NC, const float* __restrict__ hc) {
+    long ldy, int L, int D, int Nr, int T, int NC, const float* __restrict__ hc, int zgated) {
     const int d = blockIdx.x * kWave + threadIdx.x;
     const int c = blockIdx.y, b = blockIdx.z;
     if (d >= D) return;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kWave) void scan_chunk_output(
             h[n] = fmaf(ssm::ex2(dl * A2[n]), h[n], du * bc[n]);
             acc = fmaf(h[n], cc[n], acc);
         }
-        if (z) acc *= ssm::silu_fast(zv);
+        if (z) acc *= zgated ? zv : ssm::silu_fast(zv);
         ssm::bstore4(acc, ry, oy);
         oy += sy;
         dtv = dtn;
@@ -231,6 +231,7 @@ struct ScanArgs {
     const float* z; long ldz;
     float* y; long ldy;
     int B, L, D, N, T, NC;
+    int zgated;          // z already holds silu(z) (written so by its producer)
     float* hc;
     float* sdt;
     const float* h0;
@@ -249,7 +250,7 @@ void launch_all(const ScanArgs& a, hipStream_t st) {
     scan_chunk_output<N, EXACT><<<grid, kWave, 0, st>>>(a.u, a.ldu, a.dt, a.lddt, a.dt_bias,
                                                  a.softplus, a.A, a.Bm, a.ldb, a.Cm, a.ldc,
                                                  a.Dsk, a.z, a.ldz, a.y, a.ldy, a.L, a.D, a.N,
-                                                 a.T, a.NC, a.hc);
+                                                 a.T, a.NC, a.hc, a.zgated);
 }
 
 // ---------------------------------------------------------------- single-pass scan
@@ -305,6 +306,13 @@ struct Scan1 {
 template <int J>
 __device__ __forceinline__ float row_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, true));
+}
+
+// Value of lane q ^ X of this lane's quad (DPP quad_perm), folded into its user.
+template <int X>
+__device__ __forceinline__ float quad_xor(float v) {
+    constexpr int ctrl = X == 1 ? 0xB1 : 0x4E;   // quad_perm [1,0,3,2] / [2,3,0,1]
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, true));
 }
 
 template <int N, bool EXACT>
@@ -386,7 +394,7 @@ __global__ __launch_bounds__(64 * Scan1<N>::W) void scan_single_kernel(ScanArgs 
             const float dl = ok * (spf * ssm::softplus_sel(raw) + (1.f - spf) * raw);
             sm.dl[sc][st] = dl;
             sm.du[sc][st] = dl * uv[e];
-            sm.gz[st][sc] = fmaf(gzf, ssm::silu_fast(zv[e]) - 1.f, 1.f);
+            sm.gz[st][sc] = a.zgated ? (a.z ? zv[e] : 1.f) : fmaf(gzf, ssm::silu_fast(zv[e]) - 1.f, 1.f);
             sm.dx[st][sc] = Dd * uv[e];
         }
 #pragma unroll
@@ -462,6 +470,234 @@ __global__ __launch_bounds__(64 * Scan1<N>::W) void scan_single_kernel(ScanArgs 
         }
     }
     if (live && a.hT) a.hT[((long)b * D + d) * Nr + n] = h;
+}
+
+// ---------------------------------------------------------------- single pass, N = 16
+// The same walk for N = 16, laid out for the LDS of gfx950, which serves a ds_read_b128 16
+// lanes (256 bytes, all 64 banks) at a time at about 1 KB per 1.8 ns per CU while writes
+// cost three to four times as much per byte; the design keeps LDS writes to one per staged
+// value and one per state, with every access touching distinct banks:
+//   staging  per block of TK steps the workgroup loads u, dt, z as whole rows of its CW
+//            channels (and B_t, C_t), one block ahead, and writes one float4 {dt', dt' u,
+//            silu(z), D u} per (step, channel), dt' = softplus(dt + bias) (slots XOR-swizzled
+//            by the step so that 16 steps of one channel fall in 16 bank groups). The Mamba-1
+//            block hands over dt' and silu(z) already formed by their producers (zgated, no
+//            bias, no softplus), which takes the transcendentals out of this kernel;
+//   scan     lane (c, j) reads the float4 of step s0 + j of its channel; lane (c, n) then
+//            takes dt' and dt' u of step J from lane J of the channel's row (row_newbcast
+//            inside the multiplies): h = exp2(dt' A log2 e) h + dt' u B_t[n] for 16 steps,
+//            B_t[n] of the 16 steps in four ds_read_b128;
+//   output   the 16 states per lane go to the wave's own LDS region in four ds_write_b128
+//            (4 steps each, slots XOR-swizzled by the step quad so that both the writes and
+//            the reads below touch 64 different banks per 16 lanes); lane (c, tq, nq) reads
+//            the 4 x 4 (step, state) block t = 4 tq .. 4 tq + 3, n = 4 nq .. 4 nq + 3 and the
+//            matching C, forms 4 partial sums (independent FMA chains) and reduces them over
+//            the 4 lanes of its quad (two DPP exchange levels). Lane (c, tq, nq) ends with the
+//            sum of step 4 tq + nq = j: the lane that read that step's gate and skip term,
+//            so y = (sum + D u) silu(z) is formed and stored there.
+// Staging buffers are double-buffered, so a block needs one barrier; within a block each
+// sub-block's output reduction is issued next to the following sub-block's scan. The sum over
+// n runs as four sums of 4 states added pairwise across the quad (the oracle adds the 16 in
+// order; the fp32 rounding differs only).
+template <int W>
+struct ScanW16 {
+    static constexpr int CW = 4 * W;     // channels per workgroup (4 per wave)
+    static constexpr int TK = 64;        // steps per block
+    static constexpr int NSB = TK / 16;  // sub-blocks of 16 steps per block
+    // Every wave stages a share of each block. (Staging on only the two waves that are alone
+    // on a SIMD, waves 2 and 3 of a six-wave group, measured slower: their share became the
+    // block's critical path.)
+    static constexpr int NST = 64 * W;                   // staging threads
+    static constexpr int UE = TK * CW / NST;             // staged (step, channel) per thread
+    static constexpr int BE = (TK * 16 + NST - 1) / NST; // B (and C) values per thread
+    static constexpr int SW = (CW + 15) / 16 * 16;       // slots per staged row
+    static constexpr int PB = TK + 4;    // [n][t] rows: n rows 4 banks apart
+    static constexpr int PC = 20;        // [t][n] rows: t rows 20 banks apart
+    struct Smem {
+        float4 sx[2][TK][SW];            // {dt', dt' u, silu(z), D u}, slot c ^ (t % 16)
+        float bt[2][16][PB];             // B_t[n]
+        float ct[2][TK][PC];             // C_t[n]
+        float hx[W][1024];               // each wave's states of one sub-block
+        float2 par[CW];                  // dt bias, D of the workgroup's channels
+    };
+};
+
+template <int W>
+__global__ __launch_bounds__(64 * W) void scan_w16_kernel(ScanArgs a) {
+    using S = ScanW16<W>;
+    constexpr int TK = S::TK, NSB = S::NSB, NST = S::NST, BE = S::BE, UE = S::UE, CW = S::CW;
+    static_assert((TK * CW) % NST == 0, "staging layout");
+    __shared__ __attribute__((aligned(16))) typename S::Smem sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = lane >> 4, j = lane & 15;
+    const int b = blockIdx.y, c0 = blockIdx.x * CW;
+    const int D = a.D, L = a.L;
+    const int cw = 4 * w + c;            // this lane's channel within the workgroup
+    const int d = c0 + cw;
+    const bool dok = d < D;
+    const unsigned dmask = dok ? 0u : 0x80000000u;   // a channel past D stores nothing
+    const float A2 = a.A[(long)(dok ? d : D - 1) * 16 + j] * ssm::kLog2e;
+    float h = (dok && a.h0) ? a.h0[((long)b * D + d) * 16 + j] : 0.f;
+    if (tid < CW) {
+        const int pd = min(c0 + tid, D - 1);
+        sm.par[tid] = make_float2(a.dt_bias ? a.dt_bias[pd] : 0.f, a.Dsk ? a.Dsk[pd] : 0.f);
+    }
+    // staging thread st: elements i = st + NST e, step i / CW, channel i % CW
+    const int st = tid;
+
+    // rows k TK .. k TK + TK - 1 of sequence b through a descriptor rebuilt per block
+    // (32-bit offsets however long the sequence); rows past L read zeros, take no stores
+    const long r0 = (long)b * L;
+    auto blk = [&](const float* p, long ld, int width, int k) {
+        const int rows = min(TK, L - k * TK);
+        return rows > 0 ? ssm::rsrc(p + (r0 + (long)k * TK) * ld,
+                                    (unsigned)(((long)(rows - 1) * ld + width) * 4))
+                        : ssm::rsrc(p, 0u);
+    };
+    // block k's values of this staging thread, loaded one block ahead (a channel past D reads
+    // the last channel's value, never used; rows past the last read zeros)
+    float uv[UE], dv[UE], zv[UE], bv[BE], cv[BE];
+    auto load = [&](int k) {
+        const auto ru = blk(a.u, a.ldu, D, k), rd = blk(a.dt, a.lddt, D, k);
+        const auto rz = a.z ? blk(a.z, a.ldz, D, k) : ssm::rsrc(a.u, 0u);
+        const auto rb = blk(a.Bm, a.ldb, 16, k), rc = blk(a.Cm, a.ldc, 16, k);
+#pragma unroll
+        for (int e = 0; e < UE; ++e) {
+            const int i = st + NST * e;
+            const unsigned t = (unsigned)(i / CW), sd = (unsigned)min(c0 + i % CW, D - 1);
+            uv[e] = ssm::bload4(ru, (t * (unsigned)a.ldu + sd) * 4u);
+            dv[e] = ssm::bload4(rd, (t * (unsigned)a.lddt + sd) * 4u);
+            zv[e] = ssm::bload4(rz, (t * (unsigned)a.ldz + sd) * 4u);
+        }
+#pragma unroll
+        for (int e = 0; e < BE; ++e) {
+            // value i = step i / 16, state i % 16; threads past the block's values repeat the
+            // first ones (the same value to the same place)
+            const int i = (st + NST * e) % (TK * 16);
+            const unsigned t = (unsigned)(i >> 4), nn = (unsigned)(i & 15);
+            bv[e] = ssm::bload4(rb, (t * (unsigned)a.ldb + nn) * 4u);
+            cv[e] = ssm::bload4(rc, (t * (unsigned)a.ldc + nn) * 4u);
+        }
+    };
+    auto stage = [&](int k, int buf) {
+#pragma unroll
+        for (int e = 0; e < UE; ++e) {
+            const int i = st + NST * e, t = i / CW, sc = i % CW;
+            const float2 pr = sm.par[sc];
+            float dl = dv[e] + pr.x;
+            if (a.softplus) dl = ssm::softplus_sel(dl);
+            dl = (k * TK + t < L) ? dl : 0.f;            // past L: dt' = 0, the state is kept
+            const float gz = a.z ? (a.zgated ? zv[e] : ssm::silu_fast(zv[e])) : 1.f;
+            sm.sx[buf][t][sc ^ (t & 15)] = make_float4(dl, dl * uv[e], gz, pr.y * uv[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < BE; ++e) {
+            const int i = (st + NST * e) % (TK * 16);
+            sm.bt[buf][i & 15][i >> 4] = bv[e];
+            sm.ct[buf][i >> 4][i & 15] = cv[e];
+        }
+    };
+
+    float* hw = sm.hx[w];
+    const int tq = j >> 2, nq = j & 3;
+    const bool x2 = (nq & 2) != 0, x1 = (nq & 1) != 0;
+    const int nblk = (L + TK - 1) / TK;
+    __syncthreads();                     // par
+    load(0);
+    stage(0, 0);
+    load(1);
+    __syncthreads();
+    for (int k = 0; k < nblk; ++k) {
+        const int buf = k & 1;
+        // fill the other buffer (last read in block k - 1, which every wave finished before
+        // the previous barrier) and issue the loads of the block after it
+        stage(k + 1, buf ^ 1);           // past the last block: zeros, never read
+        load(k + 2);
+        const auto ry = blk(a.y, a.ldy, D, k);
+        // Sub-block s: its inputs (the staged float4 of step 16 s + j, B of its 16 steps) are
+        // read one sub-block ahead; its output reduction runs in the next sub-block, next to
+        // that sub-block's scan, so the scan's exp -> FMA chain and the LDS round trips fill
+        // each other's stalls. One wave-scope fence per sub-block orders the transposition's
+        // writes before its reads (other lanes of the same wave read them).
+        float4 in, hv[4], cq[4];
+        float bq[16];
+        auto read_in = [&](int s, float4& iv, float (&bb)[16]) {
+            iv = sm.sx[buf][16 * s + j][cw ^ j];   // (16 s + j) % 16 == j
+#pragma unroll
+            for (int q = 0; q < 16; q += 4) {
+                const float4 b4 = *reinterpret_cast<const float4*>(&sm.bt[buf][j][16 * s + q]);
+                bb[q] = b4.x; bb[q + 1] = b4.y; bb[q + 2] = b4.z; bb[q + 3] = b4.w;
+            }
+        };
+        // reduce sub-block s's products (hv, cq read earlier) and store its outputs
+        auto output = [&](int s, float gz, float dx) {
+            float p[4];
+            p[0] = fmaf(hv[3].x, cq[0].w, fmaf(hv[2].x, cq[0].z, fmaf(hv[1].x, cq[0].y, hv[0].x * cq[0].x)));
+            p[1] = fmaf(hv[3].y, cq[1].w, fmaf(hv[2].y, cq[1].z, fmaf(hv[1].y, cq[1].y, hv[0].y * cq[1].x)));
+            p[2] = fmaf(hv[3].z, cq[2].w, fmaf(hv[2].z, cq[2].z, fmaf(hv[1].z, cq[2].y, hv[0].z * cq[2].x)));
+            p[3] = fmaf(hv[3].w, cq[3].w, fmaf(hv[2].w, cq[3].z, fmaf(hv[1].w, cq[3].y, hv[0].w * cq[3].x)));
+            // sum over the quad: lanes nq and nq ^ 2 exchange halves, then nq and nq ^ 1
+            const float k0 = x2 ? p[2] : p[0], s0 = x2 ? p[0] : p[2];
+            const float k1 = x2 ? p[3] : p[1], s1 = x2 ? p[1] : p[3];
+            const float r0s = k0 + quad_xor<2>(s0), r1s = k1 + quad_xor<2>(s1);
+            const float kk = x1 ? r1s : r0s, ss = x1 ? r0s : r1s;
+            const float ysum = kk + quad_xor<1>(ss);
+            ssm::bstore4((ysum + dx) * gz, ry,
+                         (((unsigned)(16 * s + j) * (unsigned)a.ldy + (unsigned)d) * 4u) | dmask);
+        };
+        read_in(0, in, bq);
+        float gzp = 0.f, dxp = 0.f;
+#pragma unroll
+        for (int s = 0; s < NSB; ++s) {
+            float4 inn;
+            float bqn[16];
+            if (s + 1 < NSB) read_in(s + 1, inn, bqn);
+            const float dl = in.x, du = in.y;
+            float hs[16];
+#define SCANW_STEP(J)                                                                        \
+            h = fmaf(ssm::ex2(row_bcast<J>(dl) * A2), h, row_bcast<J>(du) * bq[J]);          \
+            hs[J] = h;
+            SCANW_STEP(0) SCANW_STEP(1) SCANW_STEP(2) SCANW_STEP(3)
+            SCANW_STEP(4) SCANW_STEP(5) SCANW_STEP(6) SCANW_STEP(7)
+            SCANW_STEP(8) SCANW_STEP(9) SCANW_STEP(10) SCANW_STEP(11)
+            SCANW_STEP(12) SCANW_STEP(13) SCANW_STEP(14) SCANW_STEP(15)
+#undef SCANW_STEP
+            if (s > 0) output(s - 1, gzp, dxp);
+            // states of steps 4 q .. 4 q + 3 to slot (c, n ^ q) of quad q
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<float4*>(&hw[q * 256 + c * 64 + 4 * (j ^ q)]) =
+                    make_float4(hs[4 * q], hs[4 * q + 1], hs[4 * q + 2], hs[4 * q + 3]);
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            // hv[i]: steps 4 tq .. 4 tq + 3 of state 4 nq + i; cq[u]: C of step 4 tq + u,
+            // states 4 nq .. 4 nq + 3
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                hv[i] = *reinterpret_cast<const float4*>(
+                    &hw[tq * 256 + c * 64 + 4 * (4 * nq + (i ^ tq))]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                cq[u] = *reinterpret_cast<const float4*>(&sm.ct[buf][16 * s + 4 * tq + u][4 * nq]);
+            gzp = in.z;
+            dxp = in.w;
+            if (s + 1 < NSB) {
+                in = inn;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) bq[q] = bqn[q];
+            }
+        }
+        output(NSB - 1, gzp, dxp);
+        __syncthreads();
+    }
+    if (dok && a.hT) a.hT[((long)b * D + d) * 16 + j] = h;
+}
+
+// Six waves (24 channels) per workgroup: cfg2's 1536 channels x 4 sequences give one
+// workgroup per CU on all 256 (eight-wave groups leave 64 CUs idle: 108 against 104 us).
+void launch_w16(const ScanArgs& a, hipStream_t st) {
+    constexpr int W = 6;
+    dim3 grid((unsigned)ssm::cdiv(a.D, ScanW16<W>::CW), (unsigned)a.B);
+    scan_w16_kernel<W><<<grid, 64 * W, 0, st>>>(a);
 }
 
 template <int N, bool EXACT>
@@ -637,13 +873,16 @@ extern "C" size_t ssm_selective_scan_workspace(int B, int L, int D, int N) {
     return chunked_workspace(B, L, D, N);
 }
 
-extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* dt, long lddt,
-                                         const float* dt_bias, int softplus, const float* A,
-                                         const float* Bm, long ldb, const float* Cm, long ldc,
-                                         const float* Dsk, const float* z, long ldz, float* y,
-                                         long ldy, int B, int L, int D, int N, const float* h0,
-                                         float* hT, void* workspace, size_t workspace_bytes,
-                                         void* stream) {
+namespace ssm {
+
+// ssm_selective_scan with one more input form: zgated = 1 when z already holds silu(z) (the
+// Mamba-1 block writes it so from in_proj's epilogue).
+ssm_status selective_scan(const float* u, long ldu, const float* dt, long lddt,
+                          const float* dt_bias, int softplus, const float* A, const float* Bm,
+                          long ldb, const float* Cm, long ldc, const float* Dsk, const float* z,
+                          long ldz, int zgated, float* y, long ldy, int B, int L, int D, int N,
+                          const float* h0, float* hT, void* workspace, size_t workspace_bytes,
+                          void* stream) {
     SSM_REQUIRE(u && dt && A && Bm && Cm && y, "ssm_selective_scan: null input");
     SSM_REQUIRE(B >= 0 && L >= 0 && D >= 0 && N >= 1 && N <= 64,
                 "ssm_selective_scan: need 1 <= N <= 64 (got %d)", N);
@@ -673,6 +912,7 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
     a.u = u; a.ldu = ldu; a.dt = dt; a.lddt = lddt; a.dt_bias = dt_bias; a.softplus = softplus;
     a.A = A; a.Bm = Bm; a.ldb = ldb; a.Cm = Cm; a.ldc = ldc; a.Dsk = Dsk; a.z = z; a.ldz = ldz;
     a.y = y; a.ldy = ldy; a.B = B; a.L = L; a.D = D; a.N = N;
+    a.zgated = z ? zgated : 0;
     a.T = pick_chunk(B, L, D);
     a.NC = (int)ssm::cdiv(L, a.T);
     a.hc = (float*)workspace;
@@ -684,7 +924,7 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
         switch (Np) {
             case 4: exact ? launch_single<4, true>(a, st) : launch_single<4, false>(a, st); break;
             case 8: exact ? launch_single<8, true>(a, st) : launch_single<8, false>(a, st); break;
-            case 16: exact ? launch_single<16, true>(a, st) : launch_single<16, false>(a, st); break;
+            case 16: exact ? launch_w16(a, st) : launch_single<16, false>(a, st); break;
             case 32: exact ? launch_single<32, true>(a, st) : launch_single<32, false>(a, st); break;
             default: exact ? launch_single<64, true>(a, st) : launch_single<64, false>(a, st); break;
         }
@@ -703,6 +943,20 @@ extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* 
             else launch_all<64, false>(a, st);
     }
     return ssm::check_launch("selective_scan");
+}
+
+}  // namespace ssm
+
+extern "C" ssm_status ssm_selective_scan(const float* u, long ldu, const float* dt, long lddt,
+                                         const float* dt_bias, int softplus, const float* A,
+                                         const float* Bm, long ldb, const float* Cm, long ldc,
+                                         const float* Dsk, const float* z, long ldz, float* y,
+                                         long ldy, int B, int L, int D, int N, const float* h0,
+                                         float* hT, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+    return ssm::selective_scan(u, ldu, dt, lddt, dt_bias, softplus, A, Bm, ldb, Cm, ldc, Dsk, z,
+                               ldz, 0, y, ldy, B, L, D, N, h0, hT, workspace, workspace_bytes,
+                               stream);
 }
 
 extern "C" ssm_status ssm_m1_state_update(const float* x, long ldx, const float* dt, long lddt,

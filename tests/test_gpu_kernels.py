@@ -162,6 +162,7 @@ def test_scan_shapes(B, L, D, N, h0):
 @pytest.mark.parametrize("B,L,D,N,h0,full", [
     (4, 77, 1040, 16, True, True),     # partial channel tile, tail block of 13 steps
     (4, 100, 1536, 16, False, True),   # cfg2's channels and state size
+    (4, 70, 1024, 16, True, False),    # N = 16 without z, D, dt bias; raw dt
     (8, 40, 1024, 8, True, True),
     (2, 70, 1024, 32, True, False),    # no z, D, dt bias; raw dt
     (1, 130, 1024, 64, True, True),
