@@ -17,7 +17,8 @@ Workloads (--workload picks one line; the default is cfg3 with the extras):
   cfg2  Mamba-1 block forward, fp32, d=768 D=1536 N=16 R=48 K=4, B=4 L=2048 (in_proj ->
         conv/SiLU -> x_proj/dt_proj -> scan (D skip, SiLU(z) gate) -> out_proj)
   cfg3  Mamba-2 SSD prefill core, B=8 L=4096 H=64 P=64 N=128 G=1; --dtype f32 (default) | bf16
-  cfg3layer  the whole fp32 Mamba-2 layer at cfg3's dimensions (d_model 2048), per stage
+  cfg3layer  the whole Mamba-2 layer at cfg3's dimensions (d_model 2048), per stage; --dtype
+             bf16: the bf16-input / fp32-accumulate variant
   cfg4  Mamba-2 24-layer decode, d=1024 H=32 P=64 N=128 V=32000, 64 cached sequences,
         one greedy step (24 layers + LM head + argmax) per bench step, fp32; --sampling
         draws the token with sampleToken on the device instead (T 0.8, topK 50, topP 0.9)
@@ -487,9 +488,11 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, wit
 
 
 def w_cfg3layer(torch, np, dev, args):
-    """The whole cfg3 Mamba-2 layer in fp32 at cfg3's dimensions (d_model 2048, expand 2,
-    64 heads x 64, d_state 128, one group, conv 4; B=8, L=4096), one ssm_mixer_forward_device
-    per step, timed per stage."""
+    """The whole cfg3 Mamba-2 layer at cfg3's dimensions (d_model 2048, expand 2, 64 heads x 64,
+    d_state 128, one group, conv 4; B=8, L=4096), one ssm_mixer_forward_device per step, timed
+    per stage; --dtype bf16: the bf16-input / fp32-accumulate variant
+    (ssm_mixer_forward_device_bf16)."""
+    bf = args.dtype == "bf16"
     from ssmjs_amd import _lib, backend
     B, L, d, H, N, K = 8, 4096, 2048, 64, 128, 4
     D, P = 2 * d, 64
@@ -501,11 +504,13 @@ def w_cfg3layer(torch, np, dev, args):
     x = torch.randn(B, L, d, device="cuda", generator=g)
     y = torch.empty_like(x)
 
+    entry = "ssm_mixer_forward_device_bf16" if bf else "ssm_mixer_forward_device"
+
     def step():
-        _lib.call("ssm_mixer_forward_device", m.handle, 0, x.data_ptr(), y.data_ptr(), B, L)
+        _lib.call(entry, m.handle, 0, x.data_ptr(), y.data_ptr(), B, L)
 
     steps, warm = args.steps or 5, args.warmup if args.warmup is not None else 2
-    steps = min(steps, 10)
+    steps = min(steps, 10) if not bf else min(steps * 4, 40)
     ms = timed(torch, step, steps, warm)
     st = profiled_stages(dev, torch, step, steps)
     cd, nin = D + 2 * N, 2 * D + 2 * N + H
@@ -519,21 +524,31 @@ def w_cfg3layer(torch, np, dev, args):
         # per-head sums of u^2 (y's own bytes are in ssd_alg)
         "m2.ssd_gate": (sf, sb + 4.0 * (T * D + D + T * H)),
         "m2.out_proj": (2.0 * T * D * d, 4.0 * (T * D + d * D + T * d)),
+        # bf16 variant: bf16 operands (2 bytes), fp32 results
+        "m2b.cast_x": (None, 4.0 * T * d + 2.0 * T * d),
+        "m2b.in_proj": (2.0 * T * d * nin, 2.0 * (T * d + nin * d) + 4.0 * T * nin),
+        "m2b.conv": (None, 4.0 * T * cd + 2.0 * T * cd + 4.0 * cd * (K + 1)),
+        "m2b.ssd": ssd_alg(B, L, H, P, N, 2),
+        "m2b.gated_norm": (None, 4.0 * T * D * 2 + 2.0 * T * D + 4.0 * D),
+        "m2b.out_proj": (2.0 * T * D * d, 2.0 * (T * D + d * D) + 4.0 * T * d),
     }
     stages = {}
     for kk, (n, avg) in st.items():
         f, b = alg[kk]
-        stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None)
+        prec = "bf16" if kk.startswith("m2b.") else "f32"
+        stages[kk] = roofline(kk, avg, f, b, prec, "hbm" if f is None else None)
     dom = max(stages.values(), key=lambda r: r["avg_ms"])
     layer_flops = sum(alg[kk][0] for kk in st if alg[kk][0])
     out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
-           "dtype": "f32",
+           "dtype": "bf16" if bf else "f32",
            "config": {"workload": "cfg3 layer: Mamba-2 layer prefill (in_proj, conv1d+SiLU over "
-                                  "x/B/C, SSD, gated RMSNorm, out_proj)",
+                                  "x/B/C, SSD, gated RMSNorm, out_proj)"
+                                  + (", bf16 inputs / fp32 accumulate" if bf else ""),
                       "batch": B, "seq_len": L, "d_model": d, "heads": H, "head_dim": P,
                       "d_state": N, "groups": 1, "tokens_per_step": T},
            "roofline": dom, "stages": stages,
-           "layer_mfma_frac": round(layer_flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4)}
+           "layer_mfma_frac": round(layer_flops / (ms * 1e-3) / 1e12
+                                    / PEAK_TFLOPS["bf16" if bf else "f32"], 4)}
     m.destroy()
     return out
 
@@ -775,7 +790,8 @@ def main():
     extra = {}
     if args.workload is None and not args.no_extras:
         # the other configurations, each with its own default steps, no CPU baseline
-        for key, wl, dtype in (("cfg3_layer_f32", "cfg3layer", None), ("cfg3_bf16", "cfg3", "bf16"),
+        for key, wl, dtype in (("cfg3_layer_f32", "cfg3layer", None),
+                               ("cfg3_layer_bf16", "cfg3layer", "bf16"), ("cfg3_bf16", "cfg3", "bf16"),
                                ("cfg2", "cfg2", None), ("cfg4", "cfg4", None),
                                ("cfg5", "cfg5", None), ("decode_m1", "decode_m1", None)):
             a2 = argparse.Namespace(**vars(args))

@@ -286,6 +286,13 @@ ssm_status ssm_forward_device(ssm_model* m, const uint32_t* d_ids, int B, int L,
 /* One mixer (layer `layer`, no norm / residual) over device hidden states (B,L,d_model). */
 ssm_status ssm_mixer_forward_device(ssm_model* m, int layer, const float* d_x, float* d_y,
                                     int B, int L);
+/* The same Mamba-2 mixer with bf16 operands and fp32 accumulation: x, in_proj and out_proj
+ * weights, the SSD's x / B / C and out_proj's input rounded to bf16 (round to nearest even);
+ * dt, the conv, the state pass and every sum stay fp32. No counterpart in the reference: the
+ * bf16-input variant of the layer prefill that the benchmark configuration asks for, for
+ * tests and benches. */
+ssm_status ssm_mixer_forward_device_bf16(ssm_model* m, int layer, const float* d_x, float* d_y,
+                                         int B, int L);
 
 /* Recurrent decode state (ssm + conv state of every layer) for B sequences. */
 ssm_status ssm_state_create(ssm_model* m, int B, ssm_state** out);

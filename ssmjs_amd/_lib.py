@@ -120,6 +120,7 @@ PROTOTYPES = {
     "ssm_forward": (_i, [_vp, _vp, _i, _i, _vp]),
     "ssm_forward_device": (_i, [_vp, _vp, _i, _i, _vp]),
     "ssm_mixer_forward_device": (_i, [_vp, _i, _vp, _vp, _i, _i]),
+    "ssm_mixer_forward_device_bf16": (_i, [_vp, _i, _vp, _vp, _i, _i]),
     "ssm_state_create": (_i, [_vp, _i, C.POINTER(_vp)]),
     "ssm_state_destroy": (_i, [_vp]),
     "ssm_state_reset": (_i, [_vp]),

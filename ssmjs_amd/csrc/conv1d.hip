@@ -42,18 +42,29 @@ __device__ __forceinline__ void store_v(float* p, const float (&v)[VEC]) {
     }
 }
 
-template <int K, int VEC>
+// bf16 outputs (round to nearest even), for the bf16-input layer's SSD operands
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+template <int VEC>
+__device__ __forceinline__ void store_v(__bf16* p, const float (&v)[VEC]) {
+    if constexpr (VEC == 4) {
+        *reinterpret_cast<bf16x4_t*>(p) = bf16x4_t{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+    } else {
+        *p = (__bf16)v[0];
+    }
+}
+
+template <int K, int VEC, typename OT>
 __global__ __launch_bounds__(256) void conv1d_fwd(const float* __restrict__ x, long ldx,
                                                   const float* __restrict__ w,
                                                   const float* __restrict__ bias,
-                                                  float* __restrict__ y, long ldy, int L, int C,
+                                                  OT* __restrict__ y, long ldy, int L, int C,
                                                   int silu, const float* __restrict__ state_in) {
     const int c0 = (blockIdx.x * kChan + threadIdx.x) * VEC;
     const int t0 = (blockIdx.y * kRuns + threadIdx.y) * kTT;
     const int b = blockIdx.z;
     if (c0 >= C || t0 >= L) return;
     const float* xb = x + (long)b * L * ldx + c0;
-    float* yb = y + (long)b * L * ldy + c0;
+    OT* yb = y + (long)b * L * ldy + c0;
 
     float wk[K][VEC], bv[VEC];
 #pragma unroll
@@ -173,24 +184,43 @@ __global__ void conv1d_update_kernel(const float* __restrict__ x, long ldx,
     y[(long)b * ldy + c] = silu ? ssm::silu_fast(acc) : acc;
 }
 
-template <int K>
-ssm_status launch_fwd(const float* x, long ldx, const float* w, const float* bias, float* y,
+template <int K, typename OT>
+ssm_status launch_fwd(const float* x, long ldx, const float* w, const float* bias, OT* y,
                       long ldy, int B, int L, int C, int silu, const float* state_in,
                       hipStream_t st) {
     const bool v4 = (C % 4 == 0) && (ldx % 4 == 0) && (ldy % 4 == 0) &&
-                    ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+                    ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % (4 * sizeof(OT)) == 0);
     const dim3 block(kChan, kRuns);
     if (v4) {
         dim3 grid((unsigned)ssm::cdiv(C / 4, kChan), (unsigned)ssm::cdiv(L, kRuns * kTT), B);
-        conv1d_fwd<K, 4><<<grid, block, 0, st>>>(x, ldx, w, bias, y, ldy, L, C, silu, state_in);
+        conv1d_fwd<K, 4, OT><<<grid, block, 0, st>>>(x, ldx, w, bias, y, ldy, L, C, silu, state_in);
     } else {
         dim3 grid((unsigned)ssm::cdiv(C, kChan), (unsigned)ssm::cdiv(L, kRuns * kTT), B);
-        conv1d_fwd<K, 1><<<grid, block, 0, st>>>(x, ldx, w, bias, y, ldy, L, C, silu, state_in);
+        conv1d_fwd<K, 1, OT><<<grid, block, 0, st>>>(x, ldx, w, bias, y, ldy, L, C, silu, state_in);
     }
     return ssm::check_launch("conv1d_fwd");
 }
 
 }  // namespace
+
+namespace ssm {
+
+// The forward conv with bf16 outputs and a zero initial state (the bf16-input layer).
+ssm_status launch_conv1d_bf16(const float* x, long ldx, const float* w, const float* bias,
+                              __bf16* y, long ldy, int B, int L, int C, int K, int silu,
+                              hipStream_t st) {
+    SSM_REQUIRE(x && w && y && B >= 0 && L >= 0 && C >= 0 && ldx >= C && ldy >= C,
+                "conv1d_bf16: bad args");
+    if (B == 0 || L == 0 || C == 0) return SSM_OK;
+    switch (K) {
+        case 2: return launch_fwd<2>(x, ldx, w, bias, y, ldy, B, L, C, silu, nullptr, st);
+        case 3: return launch_fwd<3>(x, ldx, w, bias, y, ldy, B, L, C, silu, nullptr, st);
+        case 4: return launch_fwd<4>(x, ldx, w, bias, y, ldy, B, L, C, silu, nullptr, st);
+        default: return fail(SSM_ERR_INVALID_ARG, "conv1d_bf16: kernel width %d", K);
+    }
+}
+
+}  // namespace ssm
 
 extern "C" ssm_status ssm_causal_conv1d(const float* x, long ldx, const float* w,
                                         const float* bias, float* y, long ldy, int B, int L,

@@ -35,14 +35,15 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* __restrict
 
 // y = norm_g(x * silu(z)) * w over G groups of n/G. Row values are staged in LDS-free
 // registers by re-reading x and z (rows are short and L2 resident).
+template <typename OT>
 __global__ __launch_bounds__(kBlock) void gated_rmsnorm_kernel(
     const float* __restrict__ x, long ldx, const float* __restrict__ z, long ldz,
-    const float* __restrict__ w, float* __restrict__ y, long ldy, int n, int G, float eps) {
+    const float* __restrict__ w, OT* __restrict__ y, long ldy, int n, int G, float eps) {
     __shared__ float red[kBlock / 64];
     const int gs = n / G;
     const float* xr = x + (long)blockIdx.x * ldx;
     const float* zr = z + (long)blockIdx.x * ldz;
-    float* yr = y + (long)blockIdx.x * ldy;
+    OT* yr = y + (long)blockIdx.x * ldy;
     for (int g = 0; g < G; ++g) {
         float ss = 0.f;
         for (int i = g * gs + threadIdx.x; i < (g + 1) * gs; i += kBlock) {
@@ -51,7 +52,72 @@ __global__ __launch_bounds__(kBlock) void gated_rmsnorm_kernel(
         }
         const float r = rsqrtf(block_sum(ss, red) / gs + eps);
         for (int i = g * gs + threadIdx.x; i < (g + 1) * gs; i += kBlock)
-            yr[i] = xr[i] * ssm::silu(zr[i]) * r * w[i];
+            yr[i] = (OT)(xr[i] * ssm::silu(zr[i]) * r * w[i]);
+    }
+}
+
+// x (rows, cols) fp32, row stride ldx -> y bf16 (round to nearest even), row stride ldy.
+// V4: cols, ldx, ldy multiples of 4 and 16/8-byte aligned rows, four values per thread.
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+template <bool V4>
+__global__ __launch_bounds__(256) void cast_bf16_kernel(const float* __restrict__ x, long ldx,
+                                                        __bf16* __restrict__ y, long ldy,
+                                                        long rows, int cols) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int cw = V4 ? cols / 4 : cols;
+    if (i >= rows * cw) return;
+    const long r = i / cw;
+    const int c = (int)(i % cw);
+    if constexpr (V4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + r * ldx + 4 * c);
+        *reinterpret_cast<bf16x4_t*>(y + r * ldy + 4 * c) =
+            bf16x4_t{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    } else {
+        y[r * ldy + c] = (__bf16)x[r * ldx + c];
+    }
+}
+
+// One group, rows of n <= 4 * 256 * R floats held in registers: x and z are read once, as
+// float4 (n, ldx, ldz multiples of 4, rows 16-byte aligned); same arithmetic per element as
+// gated_rmsnorm_kernel, the sum of squares added per thread and then across the block.
+template <typename OT, int R>
+__global__ __launch_bounds__(kBlock) void gated_rmsnorm_row_kernel(
+    const float* __restrict__ x, long ldx, const float* __restrict__ z, long ldz,
+    const float* __restrict__ w, OT* __restrict__ y, long ldy, int n, float eps) {
+    __shared__ float red[kBlock / 64];
+    const float* xr = x + (long)blockIdx.x * ldx;
+    const float* zr = z + (long)blockIdx.x * ldz;
+    OT* yr = y + (long)blockIdx.x * ldy;
+    float4 u[R];
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int e = 4 * (threadIdx.x + kBlock * r);
+        u[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e < n) {
+            const float4 xv = *reinterpret_cast<const float4*>(xr + e);
+            const float4 zv = *reinterpret_cast<const float4*>(zr + e);
+            u[r] = make_float4(xv.x * ssm::silu(zv.x), xv.y * ssm::silu(zv.y),
+                               xv.z * ssm::silu(zv.z), xv.w * ssm::silu(zv.w));
+        }
+        ss = fmaf(u[r].x, u[r].x, ss);
+        ss = fmaf(u[r].y, u[r].y, ss);
+        ss = fmaf(u[r].z, u[r].z, ss);
+        ss = fmaf(u[r].w, u[r].w, ss);
+    }
+    const float rs = rsqrtf(block_sum(ss, red) / n + eps);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int e = 4 * (threadIdx.x + kBlock * r);
+        if (e >= n) continue;
+        const float4 wv = *reinterpret_cast<const float4*>(w + e);
+        const float o0 = u[r].x * rs * wv.x, o1 = u[r].y * rs * wv.y, o2 = u[r].z * rs * wv.z,
+                    o3 = u[r].w * rs * wv.w;
+        if constexpr (sizeof(OT) == 2) {
+            *reinterpret_cast<bf16x4_t*>(yr + e) = bf16x4_t{(__bf16)o0, (__bf16)o1, (__bf16)o2, (__bf16)o3};
+        } else {
+            *reinterpret_cast<float4*>(yr + e) = make_float4(o0, o1, o2, o3);
+        }
     }
 }
 
@@ -226,6 +292,30 @@ ssm_status launch_neg_exp(const float* x, float* y, long n, hipStream_t st) {
     return check_launch("neg_exp");
 }
 
+ssm_status launch_cast_bf16(const float* x, long ldx, __bf16* y, long ldy, long rows, int cols,
+                            hipStream_t st) {
+    const long n = rows * cols;
+    if (n == 0) return SSM_OK;
+    const bool v4 = cols % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
+                    ((uintptr_t)y & 7) == 0;
+    if (v4) cast_bf16_kernel<true><<<(unsigned)cdiv(n / 4, 256), 256, 0, st>>>(x, ldx, y, ldy, rows, cols);
+    else cast_bf16_kernel<false><<<(unsigned)cdiv(n, 256), 256, 0, st>>>(x, ldx, y, ldy, rows, cols);
+    return check_launch("cast_bf16");
+}
+
+ssm_status launch_gated_rmsnorm_bf16(const float* x, long ldx, const float* z, long ldz,
+                                     const float* w, __bf16* y, long ldy, int M, int n, int G,
+                                     float eps, hipStream_t st) {
+    if (M == 0) return SSM_OK;
+    const bool rowreg = G == 1 && n % 4 == 0 && n <= 4 * kBlock * 4 && ldx % 4 == 0 &&
+                        ldz % 4 == 0 && ldy % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
+                        ((uintptr_t)z & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                        ((uintptr_t)y & 7) == 0;
+    if (rowreg) gated_rmsnorm_row_kernel<__bf16, 4><<<M, kBlock, 0, st>>>(x, ldx, z, ldz, w, y, ldy, n, eps);
+    else gated_rmsnorm_kernel<<<M, kBlock, 0, st>>>(x, ldx, z, ldz, w, y, ldy, n, G, eps);
+    return check_launch("gated_rmsnorm_bf16");
+}
+
 }  // namespace ssm
 
 extern "C" ssm_status ssm_rmsnorm(const float* x, long ldx, const float* w, float* y, long ldy,
@@ -243,8 +333,15 @@ extern "C" ssm_status ssm_gated_rmsnorm(const float* x, long ldx, const float* z
                     ldz >= n && ldy >= n,
                 "ssm_gated_rmsnorm: bad args");
     if (M == 0) return SSM_OK;
-    gated_rmsnorm_kernel<<<M, kBlock, 0, (hipStream_t)stream>>>(x, ldx, z, ldz, w, y, ldy, n, G,
-                                                                 eps);
+    const bool rowreg = G == 1 && n % 4 == 0 && n <= 4 * kBlock * 4 && ldx % 4 == 0 &&
+                        ldz % 4 == 0 && ldy % 4 == 0 && (((uintptr_t)x | (uintptr_t)z |
+                                                          (uintptr_t)w | (uintptr_t)y) & 15) == 0;
+    if (rowreg)
+        gated_rmsnorm_row_kernel<float, 4><<<M, kBlock, 0, (hipStream_t)stream>>>(
+            x, ldx, z, ldz, w, y, ldy, n, eps);
+    else
+        gated_rmsnorm_kernel<<<M, kBlock, 0, (hipStream_t)stream>>>(x, ldx, z, ldz, w, y, ldy, n,
+                                                                    G, eps);
     return ssm::check_launch("gated_rmsnorm");
 }
 

@@ -116,6 +116,17 @@ bool xproj_dt_ok(int T, int D, int R, int N, long ldx, long lddbl, long lddt);
 ssm_status launch_xproj_dt(const float* x, long ldx, const float* Wx, const float* Wdt,
                            float* dbl, long lddbl, float* dt, long lddt, int T, int D, int R,
                            int N, hipStream_t st, const float* dt_bias = nullptr);
+// The bf16-input layer's element-wise stages: fp32 -> bf16 (round to nearest even) row
+// copies (glue.hip), the forward conv with bf16 outputs and a zero initial state
+// (conv1d.hip), the gated RMSNorm with bf16 outputs (glue.hip).
+ssm_status launch_cast_bf16(const float* x, long ldx, __bf16* y, long ldy, long rows, int cols,
+                            hipStream_t st);
+ssm_status launch_conv1d_bf16(const float* x, long ldx, const float* w, const float* bias,
+                              __bf16* y, long ldy, int B, int L, int C, int K, int silu,
+                              hipStream_t st);
+ssm_status launch_gated_rmsnorm_bf16(const float* x, long ldx, const float* z, long ldz,
+                                     const float* w, __bf16* y, long ldy, int M, int n, int G,
+                                     float eps, hipStream_t st);
 // ssm_selective_scan (scan_m1.hip); zgated = 1: z already holds silu(z).
 ssm_status selective_scan(const float* u, long ldu, const float* dt, long lddt,
                           const float* dt_bias, int softplus, const float* A, const float* Bm,

@@ -158,7 +158,9 @@ struct ssm_ctx {
         hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
         hipblasLtMatmulAlgo_t algo{};
     };
-    std::map<std::tuple<int, int, int, long, long>, LtPlan> lt_plans;
+    // key (M, N, K, ldx, ldy, operand type): HIP_R_32F, or HIP_R_16BF operands with fp32
+    // accumulation and output (the bf16-input layer)
+    std::map<std::tuple<int, int, int, long, long, int>, LtPlan> lt_plans;
     bool destroyed = false;
     // Held by every entry point that uses the context (its stream, BLAS handles, plan cache,
     // profiler record, and the workspaces and graphs of models and states made on it) for the
@@ -220,15 +222,16 @@ ssm_status ctx_enter(ssm_ctx* c, CtxLock& lk) {
 // as a K x Nout column-major matrix (transposed) and B = X^T as K x M (ld ldx), fp32 compute.
 // The heuristic's first algorithm is taken (no timing runs), so the choice, and the bits of
 // the result, are the same in every process. ok = false leaves the shape to rocBLAS.
-ssm_ctx::LtPlan& lt_plan(ssm_ctx* c, int M, int Nout, int K, long ldx, long ldy) {
-    auto& p = c->lt_plans[std::make_tuple(M, Nout, K, ldx, ldy)];
+ssm_ctx::LtPlan& lt_plan(ssm_ctx* c, int M, int Nout, int K, long ldx, long ldy,
+                        hipDataType ab = HIP_R_32F) {
+    auto& p = c->lt_plans[std::make_tuple(M, Nout, K, ldx, ldy, (int)ab)];
     if (p.desc) return p;
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
     bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, K, Nout, K) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_32F, K, M, ldx) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.la, ab, K, Nout, K) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.lb, ab, K, M, ldx) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, Nout, M, ldy) == HIPBLAS_STATUS_SUCCESS;
     if (ok) {
         hipblasLtMatmulPreference_t pref = nullptr;
@@ -287,6 +290,23 @@ ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, co
                                      Nout, M, K, &one, W, K, X, (rocblas_int)ldx, &beta, Y,
                                      (rocblas_int)ldy),
                        "sgemm");
+}
+
+// Y (M, Nout) fp32 [ld ldy] = beta*Y + X W^T with bf16 X (M, K) [ld ldx] and W (Nout, K)
+// row-major, fp32 accumulation: a plain library GEMM (hipBLASLt).
+ssm_status gemm_bf16(ssm_ctx* c, int M, int Nout, int K, const __bf16* X, long ldx,
+                     const __bf16* W, float* Y, long ldy, float beta) {
+    if (M == 0 || Nout == 0) return SSM_OK;
+    if (!c->lt) return ssm::fail(SSM_ERR_HIP, "bf16 GEMM: hipBLASLt unavailable");
+    auto& p = lt_plan(c, M, Nout, K, ldx, ldy, HIP_R_16BF);
+    if (!p.ok) return ssm::fail(SSM_ERR_HIP, "bf16 GEMM: no hipBLASLt algorithm for %d x %d x %d",
+                                M, Nout, K);
+    const float one = 1.f;
+    const hipblasStatus_t s = hipblasLtMatmul(c->lt, p.desc, &one, W, p.la, X, p.lb, &beta, Y,
+                                              p.lc, Y, p.lc, &p.algo, c->lt_ws, kLtWorkspace,
+                                              c->stream);
+    if (s != HIPBLAS_STATUS_SUCCESS) return ssm::fail(SSM_ERR_HIP, "hipblasLtMatmul (bf16): status %d", (int)s);
+    return SSM_OK;
 }
 
 }  // namespace
@@ -504,6 +524,10 @@ struct ssm_model {
     float* wp = nullptr;
     std::vector<long> wp_in, wp_out;   // float offsets into wp per layer (-1: not packed)
     std::vector<long> wp_x, wp_dt;     // Mamba-1 layers: x_proj and dt_proj
+    // bf16 copies of the Mamba-2 layers' in_proj and out_proj for the bf16-input layer, built
+    // at its first call and rebuilt whenever the weights change
+    __bf16* wb = nullptr;
+    std::vector<long> wb_in, wb_out;   // element offsets into wb per layer (-1: none)
     int* d_flag = nullptr;   // out-of-range token id flag
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
@@ -601,6 +625,33 @@ void build_layout(ssm_model* m) {
 
 ssm_status pack_weights(ssm_model* m);
 
+// bf16 (round to nearest even) copies of the Mamba-2 layers' in_proj and out_proj.
+ssm_status build_wb(ssm_model* m) {
+    const Dims& d = m->dm;
+    hipStream_t st = m->ctx->stream;
+    if (!m->wb) {
+        m->wb_in.assign(d.nl, -1);
+        m->wb_out.assign(d.nl, -1);
+        long off = 0;
+        for (int l = 0; l < d.nl; ++l) {
+            if (m->types[l] != SSM_LAYER_MAMBA2) continue;
+            m->wb_in[l] = off; off += ((long)d.nin * d.d + 127) / 128 * 128;
+            m->wb_out[l] = off; off += ((long)d.d * d.D + 127) / 128 * 128;
+        }
+        if (off == 0) return SSM_OK;
+        SSM_HIP_TRY(ssm::dev_malloc((void**)&m->wb, (size_t)off * sizeof(__bf16)));
+    }
+    for (int l = 0; l < d.nl; ++l) {
+        if (m->wb_in[l] < 0) continue;
+        const LayerW& Ly = m->layers[l];
+        SSM_TRY(ssm::launch_cast_bf16(m->w + Ly.in_proj, d.d, m->wb + m->wb_in[l], d.d, d.nin,
+                                      d.d, st));
+        SSM_TRY(ssm::launch_cast_bf16(m->w + Ly.out_proj, d.D, m->wb + m->wb_out[l], d.D, d.d,
+                                      d.D, st));
+    }
+    return SSM_OK;
+}
+
 // Everything derived from the weights: A = -exp(A_log) and, once built, the packed copies.
 ssm_status refresh_A(ssm_model* m) {
     hipStream_t st = m->ctx->stream;
@@ -608,6 +659,7 @@ ssm_status refresh_A(ssm_model* m) {
         const long n = L.type == SSM_LAYER_MAMBA1 ? (long)m->dm.D * m->dm.N : m->dm.H;
         SSM_TRY(ssm::launch_neg_exp(m->w + L.A_log, m->Ab + L.A, n, st));
     }
+    if (m->wb) SSM_TRY(build_wb(m));
     return m->wp ? pack_weights(m) : SSM_OK;
 }
 
@@ -822,6 +874,48 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
             { Stage g(c, "m2.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, beta)); }
         }
     }
+    return SSM_OK;
+}
+
+// The Mamba-2 mixer with bf16 operands and fp32 accumulation (one group, zero initial
+// state): x, in_proj and out_proj weights, the SSD's x / B / C operands and out_proj's input
+// are rounded to bf16 (round to nearest even); dt, the conv and the state pass stay fp32.
+//   x -> bf16; in_proj: bf16 x bf16 -> fp32 zx (hipBLASLt); conv1d + SiLU on xBC -> bf16;
+//   SSD on the bf16 operands (ssd.hip, v_mfma_f32_16x16x32_bf16) -> y fp32; gated RMSNorm
+//   -> bf16; out_proj: bf16 x bf16 -> fp32 (hipBLASLt).
+ssm_status mixer_bf16(ssm_model* m, int l, const float* x, float* out, int B, int L,
+                      const Ws& w) {
+    const Dims& d = m->dm;
+    const LayerW& Ly = m->layers[l];
+    ssm_ctx* c = m->ctx;
+    hipStream_t st = c->stream;
+    const int T = B * L;
+    const float* W = m->w;
+    const float* A = m->Ab + Ly.A;
+    const int GN = d.G * d.N;
+    SSM_REQUIRE(Ly.type == SSM_LAYER_MAMBA2, "bf16 mixer: layer %d is not a Mamba-2 layer", l);
+    if (!m->wb) SSM_TRY(build_wb(m));
+    __bf16* x16 = (__bf16*)w.hid;        // (T, d)
+    float* zx = w.a;                     // (T, nin) fp32
+    __bf16* xbc16 = (__bf16*)w.b;        // (T, cd)
+    float* y = w.c;                      // (T, D) fp32
+    __bf16* yn16 = (__bf16*)w.d;         // (T, D)
+    { Stage g(c, "m2b.cast_x"); SSM_TRY(ssm::launch_cast_bf16(x, d.d, x16, d.d, T, d.d, st)); }
+    { Stage g(c, "m2b.in_proj");
+      SSM_TRY(gemm_bf16(c, T, d.nin, d.d, x16, d.d, m->wb + m->wb_in[l], zx, d.nin, 0.f)); }
+    { Stage g(c, "m2b.conv");
+      SSM_TRY(ssm::launch_conv1d_bf16(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc16, d.cd,
+                                      B, L, d.cd, d.K, 1, st)); }
+    { Stage g(c, "m2b.ssd");
+      SSM_TRY(ssm_ssd_chunk_scan(SSM_BF16, xbc16, d.cd, zx + d.D + d.cd, d.nin, W + Ly.dt_b, 1,
+                                 0.f, INFINITY, A, xbc16 + d.D, d.cd, xbc16 + d.D + GN, d.cd,
+                                 W + Ly.Dsk, y, d.D, B, L, d.H, d.P, d.G, d.N, nullptr, nullptr,
+                                 w.scan, w.scan_bytes, st)); }
+    { Stage g(c, "m2b.gated_norm");
+      SSM_TRY(ssm::launch_gated_rmsnorm_bf16(y, d.D, zx, d.nin, W + Ly.gnorm, yn16, d.D, T, d.D,
+                                             d.G, d.eps, st)); }
+    { Stage g(c, "m2b.out_proj");
+      SSM_TRY(gemm_bf16(c, T, d.d, d.D, yn16, d.D, m->wb + m->wb_out[l], out, d.d, 0.f)); }
     return SSM_OK;
 }
 
@@ -1238,7 +1332,7 @@ extern "C" ssm_status ssm_model_destroy(ssm_model* m) {
         hipSetDevice(m->ctx->device);
         hipStreamSynchronize(m->ctx->stream);
         hipFree(m->w); hipFree(m->Ab); hipFree(m->ws); hipFree(m->d_flag); hipFree(m->d_ids);
-        hipFree(m->rg); hipFree(m->wp);
+        hipFree(m->rg); hipFree(m->wp); hipFree(m->wb);
     }
     m->destroyed = true;
     return SSM_OK;
@@ -1419,6 +1513,18 @@ extern "C" ssm_status ssm_mixer_forward_device(ssm_model* m, int layer, const fl
     Ws w;
     SSM_TRY(ensure_ws(m, B, L, false, &w));
     return mixer(m, m->layers[layer], d_x, d_y, 0.f, B, L, nullptr, nullptr, w);
+}
+
+extern "C" ssm_status ssm_mixer_forward_device_bf16(ssm_model* m, int layer, const float* d_x,
+                                                    float* d_y, int B, int L) {
+    CtxLock lk;
+    SSM_TRY(model_enter(m, lk));
+    SSM_REQUIRE(layer >= 0 && layer < m->dm.nl && d_x && d_y && B >= 0 && L >= 0,
+                "ssm_mixer_forward_device_bf16: bad args");
+    if (B == 0 || L == 0) return SSM_OK;
+    Ws w;
+    SSM_TRY(ensure_ws(m, B, L, false, &w));
+    return mixer_bf16(m, layer, d_x, d_y, B, L, w);
 }
 
 // ------------------------------------------------------------------ state

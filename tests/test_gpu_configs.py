@@ -113,6 +113,41 @@ def test_cfg3_mamba2_layer(device, B, L):
     check_close(got, ref, "layer output")
 
 
+def _bf16_round(a):
+    """float32 -> nearest bfloat16 (ties to even) -> float32, as the GPU's conversions round."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("B,L", [(1, 512), (8, 4096)])
+def test_cfg3_mamba2_layer_bf16(device, B, L):
+    """cfg3's bf16-input variant of the layer (bf16 inputs, fp32
+    accumulate): ssm_mixer_forward_device_bf16 against the oracle's fp32 mixer fed the same
+    bf16-rounded x and projection weights. The GPU path also rounds the conv output (the SSD's
+    x / B / C operands) and the gated norm's output to bf16, so it is held to the bf16 SSD's
+    bound: max |gpu - oracle| / max(1, max |oracle|) <= 2e-2."""
+    from ssmjs_amd import _lib, backend, checkpoint
+    case(f"cfg3 Mamba-2 layer, bf16 inputs, B={B} L={L}")
+    cfg = {"vocabSize": 16, "dModel": 2048, "numLayers": 1, "dState": 128, "dConv": 4,
+           "expand": 2, "nHeads": 64, "nGroups": 1, "layers": [{"type": "mamba2"}]}
+    m = backend.Model(device, cfg, seed=1003)
+    dims, ts = checkpoint.unpack(m.export_weights())
+    for name in ("layers.0.in_proj", "layers.0.out_proj"):
+        ts[name] = _bf16_round(ts[name])
+    x = np.random.default_rng(1003).standard_normal((B, L, 2048)).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty_like(xd)
+    _lib.call("ssm_mixer_forward_device_bf16", m.handle, 0, xd.data_ptr(), yd.data_ptr(), B, L)
+    device.synchronize()
+    got = yd.cpu().numpy()
+    m.destroy()
+    ref = O.Model(checkpoint.pack(dims, ts)).mixer(0, _bf16_round(x))
+    err = float(np.abs(got.astype(np.float64) - ref).max()) / max(1.0, float(np.abs(ref).max()))
+    print(f"  normwise error {err:.3e}", flush=True)
+    assert np.isfinite(got).all() and err <= 2e-2, err
+
+
 def _greedy_rows(am, ref_logits):
     """Rows whose oracle margin is wide enough for an exact id check, and their ids."""
     srt = np.sort(ref_logits.astype(np.float64), axis=1)

@@ -491,6 +491,13 @@ def test_rmsnorm_and_gated():
     for g in (1, 3):
         ref = O.gated_rmsnorm(x, z, w, groups=g)
         check_elementwise(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=g)), ref, "gated rmsnorm", atol_frac=F32_FLOOR)
+    # rows of cfg3's d_inner (4096, the register-resident one-group path) and one past it
+    for n in (4096, 4100):
+        x, z = (r.standard_normal((5, n)).astype(np.float32) for _ in range(2))
+        w = r.uniform(0.5, 1.5, n).astype(np.float32)
+        check_elementwise(host(K().gated_rmsnorm(dev(x), dev(z), dev(w), groups=1)),
+                          O.gated_rmsnorm(x, z, w, groups=1), f"gated rmsnorm n={n}",
+                          atol_frac=F32_FLOOR)
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
