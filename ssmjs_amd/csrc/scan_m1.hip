@@ -530,7 +530,13 @@ __global__ __launch_bounds__(64 * W) void scan_w16_kernel(ScanArgs a) {
     __shared__ __attribute__((aligned(16))) typename S::Smem sm;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane >> 4, j = lane & 15;
-    const int b = blockIdx.y, c0 = blockIdx.x * CW;
+    // Workgroups go to the 8 XCDs round-robin by id; XCD x takes the x-th contiguous run of
+    // (sequence, channel block) tiles, so that the channel blocks sharing a row's 128-byte
+    // lines (CW * 4 bytes need not be a whole line) mostly share one L2.
+    const int nwg = (int)gridDim.x, nb = (a.D + CW - 1) / CW;
+    const int xcd = blockIdx.x % 8, q = nwg / 8, rem = nwg % 8;
+    const int tile = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + blockIdx.x / 8;
+    const int b = tile / nb, c0 = (tile % nb) * CW;
     const int D = a.D, L = a.L;
     const int cw = 4 * w + c;            // this lane's channel within the workgroup
     const int d = c0 + cw;
@@ -696,8 +702,8 @@ __global__ __launch_bounds__(64 * W) void scan_w16_kernel(ScanArgs a) {
 // workgroup per CU on all 256 (eight-wave groups leave 64 CUs idle: 108 against 104 us).
 void launch_w16(const ScanArgs& a, hipStream_t st) {
     constexpr int W = 6;
-    dim3 grid((unsigned)ssm::cdiv(a.D, ScanW16<W>::CW), (unsigned)a.B);
-    scan_w16_kernel<W><<<grid, 64 * W, 0, st>>>(a);
+    const long nwg = ssm::cdiv(a.D, ScanW16<W>::CW) * a.B;
+    scan_w16_kernel<W><<<(unsigned)nwg, 64 * W, 0, st>>>(a);
 }
 
 template <int N, bool EXACT>
