@@ -44,10 +44,24 @@ def _compile(src: str) -> str:
     return obj
 
 
+# host-only C++ (no device code), built with the host compiler
+HOST_SOURCES = ["ssmw.cpp"]
+
+
+def _compile_host(src: str) -> str:
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".host.o")
+    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on {src}:\n{r.stderr[-6000:]}")
+    return obj
+
+
 def build(jobs: int = 8, verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(SOURCES)))) as ex:
         objs = list(ex.map(_compile, SOURCES))
+    objs += [_compile_host(src) for src in HOST_SOURCES]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
            "-L/opt/rocm/lib", "-lrocblas", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]

@@ -29,6 +29,7 @@
 #include "common.hpp"
 #include "glue.hpp"
 #include "ssd.hpp"
+#include "ssmw.hpp"
 
 // ------------------------------------------------------------------ errors
 namespace ssm {
@@ -496,10 +497,6 @@ struct Dims {
     float eps;
     int D, P, cd, nin;
 };
-
-constexpr uint32_t kVersion = 1;
-
-size_t header_bytes(int nl) { return 80 + (size_t)((nl + 15) / 16) * 16; }
 
 }  // namespace
 
@@ -1351,49 +1348,13 @@ extern "C" ssm_status ssm_model_config(ssm_model* m, ssm_config* out) {
 }
 
 namespace {
-void write_header(const ssm_model* m, int f16, unsigned char* p) {
+// The model's expectations of an SSMW image (ssmw.hpp).
+ssmw::Expect ssmw_expect(const ssm_model* m, std::vector<unsigned char>& types) {
     const Dims& d = m->dm;
-    const size_t hb = header_bytes(d.nl);
-    std::memset(p, 0, hb);
-    std::memcpy(p, "SSMW", 4);
-    const uint32_t ver = kVersion, dt = f16 ? 1 : 0, hb32 = (uint32_t)hb;
-    const uint64_t pay = m->nfloats * (f16 ? 2 : 4);
-    std::memcpy(p + 4, &ver, 4); std::memcpy(p + 8, &dt, 4); std::memcpy(p + 12, &hb32, 4);
-    std::memcpy(p + 16, &pay, 8);
-    const int32_t f[9] = {d.V, d.d, d.nl, d.N, d.K, d.expand, d.H, d.G, d.R};
-    std::memcpy(p + 24, f, 36);
-    std::memcpy(p + 60, &d.eps, 4);
-    const int32_t g[3] = {d.chunk, d.eos, d.mimo};
-    std::memcpy(p + 64, g, 12);
-    for (int l = 0; l < d.nl; ++l) p[80 + l] = (unsigned char)m->types[l];
-}
-
-// IEEE binary16 <-> binary32, round to nearest even.
-uint16_t f2h(float f) {
-    uint32_t x; std::memcpy(&x, &f, 4);
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    uint32_t mag = x & 0x7fffffffu;
-    if (mag >= 0x7f800000u) return (uint16_t)(sign | (mag > 0x7f800000u ? 0x7e00u : 0x7c00u));
-    if (mag >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   // rounds to >= 65520 -> inf
-    if (mag < 0x38800000u) {                                      // subnormal or zero in half
-        const float af = std::fabs(f);
-        const float scaled = af * 16777216.0f;                    // * 2^24: half ulp units
-        return (uint16_t)(sign | (uint32_t)std::nearbyint(scaled));
-    }
-    const uint32_t e = ((mag >> 23) - 112) << 10;
-    const uint32_t mant = mag & 0x7fffffu;
-    uint32_t h = e | (mant >> 13);
-    const uint32_t rest = mant & 0x1fffu;
-    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;
-    return (uint16_t)(sign | h);
-}
-float h2f(uint16_t h) {
-    const uint32_t s = (uint32_t)(h >> 15), e = (h >> 10) & 0x1f, mnt = h & 0x3ff;
-    float v;
-    if (e == 0) v = std::ldexp((float)mnt, -24);
-    else if (e == 31) v = mnt ? NAN : INFINITY;
-    else v = std::ldexp((float)(mnt | 0x400), (int)e - 25);
-    return s ? -v : v;
+    types.assign(m->types.begin(), m->types.end());
+    ssmw::Expect e{{d.V, d.d, d.nl, d.N, d.K, d.expand, d.H, d.G, d.R}, types.data(),
+                   (uint64_t)m->nfloats};
+    return e;
 }
 }  // namespace
 
@@ -1401,13 +1362,16 @@ extern "C" ssm_status ssm_model_export_weights(ssm_model* m, int f16, void* buf,
                                                size_t* bytes) {
     CtxLock lk;
     SSM_TRY(model_enter(m, lk));
-    const size_t hb = header_bytes(m->dm.nl);
+    const size_t hb = ssmw::header_bytes(m->dm.nl);
     const size_t total = hb + m->nfloats * (f16 ? 2 : 4);
     if (bytes) *bytes = total;
     if (!buf) return SSM_OK;
     SSM_REQUIRE(cap >= total, "ssm_model_export_weights: buffer of %zu bytes needed", total);
     unsigned char* p = (unsigned char*)buf;
-    write_header(m, f16, p);
+    std::vector<unsigned char> types;
+    const ssmw::Expect e = ssmw_expect(m, types);
+    const Dims& d = m->dm;
+    ssmw::write_header(e.dims, d.eps, d.chunk, d.eos, d.mimo, e.layer_types, e.nfloats, f16, p);
     if (!f16) {
         SSM_HIP_TRY(hipMemcpyAsync(p + hb, m->w, m->nfloats * 4, hipMemcpyDeviceToHost,
                                    m->ctx->stream));
@@ -1418,7 +1382,7 @@ extern "C" ssm_status ssm_model_export_weights(ssm_model* m, int f16, void* buf,
                                    m->ctx->stream));
         SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
         for (size_t i = 0; i < m->nfloats; ++i) {
-            const uint16_t h = f2h(tmp[i]);
+            const uint16_t h = ssmw::f2h(tmp[i]);
             std::memcpy(p + hb + 2 * i, &h, 2);
         }
     }
@@ -1429,39 +1393,18 @@ extern "C" ssm_status ssm_model_load_weights(ssm_model* m, const void* buf, size
     CtxLock lk;
     SSM_TRY(model_enter(m, lk));
     const unsigned char* p = (const unsigned char*)buf;
-    auto bad = [](const char* why) { return ssm::fail(SSM_ERR_CHECKPOINT_INVALID, "%s", why); };
-    if (!p || bytes < 80 || std::memcmp(p, "SSMW", 4) != 0) return bad("bad magic");
-    uint32_t ver, dt, hb;
-    uint64_t pay;
-    std::memcpy(&ver, p + 4, 4); std::memcpy(&dt, p + 8, 4); std::memcpy(&hb, p + 12, 4);
-    std::memcpy(&pay, p + 16, 8);
-    if (ver != kVersion) return bad("unsupported version");
-    if (dt > 1) return bad("unsupported dtype");
-    int32_t f[9];
-    std::memcpy(f, p + 24, 36);
-    const Dims& d = m->dm;
-    if (f[2] != d.nl || hb != header_bytes(d.nl) || (uint64_t)hb + pay != bytes)
-        return bad("size mismatch");
-    const int32_t want[9] = {d.V, d.d, d.nl, d.N, d.K, d.expand, d.H, d.G, d.R};
-    for (int i = 0; i < 9; ++i)
-        if (f[i] != want[i]) return bad("size mismatch: checkpoint dimensions differ from model");
-    for (int l = 0; l < d.nl; ++l)
-        if (p[80 + l] != m->types[l]) return bad("size mismatch: layer types differ from model");
-    if (pay != m->nfloats * (dt ? 2 : 4)) return bad("size mismatch");
-    float eps;
-    std::memcpy(&eps, p + 60, 4);
-    if (eps > 0.f) m->dm.eps = eps;
-    if (dt == 0) {
-        SSM_HIP_TRY(hipMemcpyAsync(m->w, p + hb, m->nfloats * 4, hipMemcpyHostToDevice,
-                                   m->ctx->stream));
+    std::vector<unsigned char> types;
+    ssmw::Header h;
+    if (const char* why = ssmw::validate(buf, bytes, ssmw_expect(m, types), &h))
+        return ssm::fail(SSM_ERR_CHECKPOINT_INVALID, "%s", why);
+    if (h.eps > 0.f) m->dm.eps = h.eps;
+    if (h.dtype == 0) {
+        SSM_HIP_TRY(hipMemcpyAsync(m->w, p + h.header_bytes, m->nfloats * 4,
+                                   hipMemcpyHostToDevice, m->ctx->stream));
         SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     } else {
         std::vector<float> tmp(m->nfloats);
-        for (size_t i = 0; i < m->nfloats; ++i) {
-            uint16_t h;
-            std::memcpy(&h, p + hb + 2 * i, 2);
-            tmp[i] = h2f(h);
-        }
+        ssmw::decode_payload(p + h.header_bytes, h, tmp.data());
         SSM_HIP_TRY(hipMemcpyAsync(m->w, tmp.data(), m->nfloats * 4, hipMemcpyHostToDevice,
                                    m->ctx->stream));
         SSM_HIP_TRY(hipStreamSynchronize(m->ctx->stream));

@@ -1,8 +1,11 @@
 """Host code under AddressSanitizer + UndefinedBehaviorSanitizer (CPU only; SURVEY's auxiliary
-plan): the C oracle's own test file against a sanitizer build of oracle/ssm_oracle.c, and the
-Node-API addon (ssmjs_amd/napi/ssm_napi.cc, built here with g++ and the sanitizers) driven
-through its argument parsing and error paths under Node. The HIP kernels are not built with
-sanitizers (GPU code); any report makes the run fail (halt_on_error)."""
+plan): the C oracle's own test file against a sanitizer build of oracle/ssm_oracle.c, the
+library's checkpoint parser (ssmjs_amd/csrc/ssmw.cpp, the host code behind
+ssm_model_load_weights' CHECKPOINT_INVALID contract) driven with valid, truncated, oversized,
+corrupted and randomly mutated images, and the Node-API addon (ssmjs_amd/napi/ssm_napi.cc,
+built here with g++ and the sanitizers) driven through its argument parsing and error paths
+under Node. The HIP kernels are not built with sanitizers (GPU code); any report makes the run
+fail (halt_on_error)."""
 import json
 import os
 import shutil
@@ -50,6 +53,25 @@ def test_oracle_tests_under_asan_ubsan():
                        capture_output=True, text=True, cwd=ROOT, env=env, timeout=600)
     assert r.returncode == 0, (r.stdout[-3000:], r.stderr[-3000:])
     assert "passed" in r.stdout and "failed" not in r.stdout
+
+
+@needs_asan
+def test_checkpoint_parser_under_asan_ubsan(tmp_path):
+    """The SSMW validator and f16 codec of ssm_model_load_weights (session.ts:393-401: a bad
+    checkpoint must surface as CHECKPOINT_INVALID) over every truncation, one-byte header
+    corruptions, wrapping payload sizes and 40000 random mutations (tests/ssmw_check.cpp)."""
+    exe = tmp_path / "ssmw_check"
+    csrc = os.path.join(ROOT, "ssmjs_amd", "csrc")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer",
+                    "-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-I", csrc,
+                    os.path.join(ROOT, "tests", "ssmw_check.cpp"), os.path.join(csrc, "ssmw.cpp"),
+                    "-o", str(exe)], check=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:halt_on_error=1:verify_asan_link_order=0",
+               UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
+    env.pop("LD_PRELOAD", None)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0, (r.stdout[-3000:], r.stderr[-3000:])
+    assert r.stdout.startswith("ok "), r.stdout
 
 
 NODE = shutil.which("node")
