@@ -72,8 +72,14 @@ struct StepProj {
     // EPI_CONV: the conv outputs also in fragment order (K = C, C % 16 == 0; rows M .. 16 mt - 1
     // written as zeros), the operand of the step's next projection
     float* Yf = nullptr;
+    // EPI_CONV with xpart: the next projection (the Mamba-1 step's x_proj, RN outputs) summed
+    // over each conv tile's 16 channels, xpart[(ct, m, j)] = sum_{c in tile ct} u[m, c]
+    // wxt[c, j] with wxt (C, RN) row-major (RN <= kXpartMaxRN, c0 and C multiples of 16); the
+    // partials, (C / 16, 16 mt, RN), are added by the step's state update
+    const float* wxt = nullptr; int RN = 0; float* xpart = nullptr;
     int mt = 0, nt = 0, rotate = 0;        // tiles and k-start rotation (set by the launcher)
 };
+constexpr int kXpartMaxRN = 128;
 bool stepproj_ok(int M, int N, int K);
 ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st);
 // W (N, K) row stride ldw -> fragment order in out (frag_floats(N, K) floats).
@@ -95,6 +101,18 @@ ssm_status launch_m1_update_frag(const float* x, long ldx, const float* dtr, lon
                                  const float* Bm, long ldb, const float* Cm, long ldc,
                                  const float* Dsk, const float* z, long ldz, float* yf, float* h,
                                  int B, int D, int N, hipStream_t st);
+// The fused Mamba-1 step's x_proj reduction, dt_proj and state update in one launch: x_proj
+// arrives as the conv epilogue's per-tile partials xpart (D / 16, M16, RN) (M16 = B rounded up
+// to 16; RN = R + 2N = (dt_r, B, C)), added per sequence in a fixed order; dt = softplus(dt_r
+// Wdt^T + dt_bias) (Wdt (D, R) row-major); y = (C.h + D x) silu(z) in fragment order (K = D,
+// rows B .. M16-1 zero), the out_proj's operand.
+bool m1_step_update_ok(int D, int N, int R);
+ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, int RN, int M16,
+                                 const float* Wdt, int R, const float* dt_bias, const float* A,
+                                 const float* Dsk, const float* z, long ldz, float* yf, float* h,
+                                 int B, int D, int N, hipStream_t st);
+// W (N, K) row stride ldw -> its transpose (K, N) row-major in out.
+ssm_status launch_pack_t(const float* W, long ldw, int N, int K, float* out, hipStream_t st);
 // xg = x * g in fragment order (K = d) and ssq (M, d / 16) partial sums of x^2: the first
 // RMSNorm of a step.
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,

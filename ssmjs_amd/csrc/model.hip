@@ -521,6 +521,7 @@ struct ssm_model {
     float* wp = nullptr;
     std::vector<long> wp_in, wp_out;   // float offsets into wp per layer (-1: not packed)
     std::vector<long> wp_x, wp_dt;     // Mamba-1 layers: x_proj and dt_proj
+    std::vector<long> wp_xt;           // Mamba-1 layers: x_proj transposed, (D, R + 2N)
     // bf16 copies of the Mamba-2 layers' in_proj and out_proj for the bf16-input layer, built
     // at its first call and rebuilt whenever the weights change
     __bf16* wb = nullptr;
@@ -704,6 +705,9 @@ struct Ws {
     // both in fragment order, and the two norms' partial sums of squares; null for longer
     // sequences
     float *xg, *yf, *ssq_in, *ssq_y;
+    // the Mamba-1 step's x_proj partials (stepproj.hip, xpart); null for longer sequences or
+    // without Mamba-1 layers
+    float* xpart;
     void* scan;
     size_t scan_bytes;
 };
@@ -749,6 +753,8 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
     size_t o_yf = off; off += al(4 * nstep16 * d.D);
     size_t o_sqi = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
     size_t o_sqy = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
+    const size_t nxp = has1 ? (size_t)(d.D / 16) * nstep16 * (d.R + 2 * d.N) : 0;
+    size_t o_xp = off; off += al(4 * nxp);
     if (out) {
         char* base = m->ws;
         out->hid = (float*)(base + o_hid); out->nrm = (float*)(base + o_nrm);
@@ -761,6 +767,7 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
         out->yf = nstep ? (float*)(base + o_yf) : nullptr;
         out->ssq_in = nstep ? (float*)(base + o_sqi) : nullptr;
         out->ssq_y = nstep ? (float*)(base + o_sqy) : nullptr;
+        out->xpart = nxp ? (float*)(base + o_xp) : nullptr;
     }
     return off;
 }
@@ -1064,12 +1071,20 @@ ssm_status pack_weights(ssm_model* m) {
         m->wp_out.assign(d.nl, -1);
         m->wp_x.assign(d.nl, -1);
         m->wp_dt.assign(d.nl, -1);
+        m->wp_xt.assign(d.nl, -1);
+        const bool m1_step = ssm::m1_step_update_ok(d.D, d.N, d.R);
         for (int l = 0; l < d.nl; ++l) {
             if (!fusable(m, m->layers[l])) continue;
             if (m->layers[l].type == SSM_LAYER_MAMBA1) {
                 m->wp_in[l] = off; off += (long)ssm::frag_floats(2 * d.D, d.d);
-                m->wp_x[l] = off; off += (long)ssm::frag_floats(d.R + 2 * d.N, d.D);
                 m->wp_dt[l] = off; off += ((long)d.D * d.R + 63) / 64 * 64;
+                if (m1_step) {   // x_proj rides in in_proj's epilogue: its transpose
+                    m->wp_xt[l] = off;
+                    off += ((long)d.D * (d.R + 2 * d.N) + 63) / 64 * 64;
+                } else {         // x_proj is its own step projection
+                    m->wp_x[l] = off;
+                    off += (long)ssm::frag_floats(d.R + 2 * d.N, d.D);
+                }
             } else {
                 m->wp_in[l] = off; off += (long)ssm::frag_floats(d.nin, d.d);
             }
@@ -1085,11 +1100,16 @@ ssm_status pack_weights(ssm_model* m) {
             const int RN = d.R + 2 * d.N;
             SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, 2 * d.D, d.d,
                                           m->wp + m->wp_in[l], st));
-            SSM_TRY(ssm::launch_pack_frag(m->w + Ly.x_proj, d.D, RN, d.D, m->wp + m->wp_x[l], st));
+            if (m->wp_x[l] >= 0)
+                SSM_TRY(ssm::launch_pack_frag(m->w + Ly.x_proj, d.D, RN, d.D, m->wp + m->wp_x[l],
+                                              st));
             // dt_proj is formed inside the state update from row-major rows: an aligned copy
             SSM_HIP_TRY(hipMemcpyAsync(m->wp + m->wp_dt[l], m->w + Ly.dt_w,
                                        sizeof(float) * (size_t)d.D * d.R,
                                        hipMemcpyDeviceToDevice, st));
+            if (m->wp_xt[l] >= 0)
+                SSM_TRY(ssm::launch_pack_t(m->w + Ly.x_proj, d.D, RN, d.D, m->wp + m->wp_xt[l],
+                                           st));
         } else {
             SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, d.nin, d.d, m->wp + m->wp_in[l],
                                           st));
@@ -1100,17 +1120,21 @@ ssm_status pack_weights(ssm_model* m) {
     return SSM_OK;
 }
 
-// The fused one-token Mamba-1 layer step, four launches:
+// The fused one-token Mamba-1 layer step. Three launches when the state update can add x_proj's
+// partials (ssm::m1_step_update_ok; the transposed x_proj is packed):
 //   in_proj  (row scale 1/rms from w.ssq_in on w.xg = hid * norm) with the conv update of the
-//            x columns in its epilogue: z into w.a (columns D .. 2D), SiLU(conv(x)) into w.b
-//            and, in fragment order, into w.yf;
-//   x_proj   w.yf -> (dt_r, B, C) into w.c;
-//   state update with dt_proj formed per thread (dt_r . W_dt[d], then bias and softplus),
-//            the D skip and the SiLU(z) gate; y in fragment order into w.yf;
+//            x columns in its epilogue: z into w.a (columns D .. 2D), SiLU(conv(x)) into w.b,
+//            and x_proj summed over each 16-channel conv tile into w.xpart;
+//   state update: x_proj's partials added per sequence, dt_proj (dt_r . W_dt[d], then bias and
+//            softplus), the state, the D skip and the SiLU(z) gate; y in fragment order into
+//            w.yf;
 //   out_proj with the residual add into hid, and, given g_next, the next RMSNorm's operand
 //            hid * g_next in w.xg and its partial sums in w.ssq_in.
-// Same arithmetic as mixer_step up to the order of the norm's and dt_proj's sums and where
-// the norm's scale is applied (the row scale multiplies the projected row).
+// Otherwise four: in_proj also writes SiLU(conv(x)) in fragment order into w.yf, x_proj is a
+// step projection of its own into w.c (dt_r, B, C), and the state update forms dt_proj from
+// w.c.
+// Same arithmetic as mixer_step up to the order of the norm's, x_proj's and dt_proj's sums
+// and where the norm's scale is applied (the row scale multiplies the projected row).
 ssm_status mixer_step_fused_m1(ssm_model* m, int l, float* hid, int B, float* ssm_st,
                                float* conv_st, const Ws& w, const float* g_next) {
     const Dims& d = m->dm;
@@ -1119,6 +1143,7 @@ ssm_status mixer_step_fused_m1(ssm_model* m, int l, float* hid, int B, float* ss
     hipStream_t st = c->stream;
     const float* W = m->w;
     const int RN = d.R + 2 * d.N;
+    const bool three = m->wp_xt[l] >= 0 && w.xpart;
     float *xz = w.a, *xc = w.b, *dbl = w.c;
     { Stage g(c, "m1.step.in_proj");
       ssm::StepProj p;
@@ -1126,18 +1151,31 @@ ssm_status mixer_step_fused_m1(ssm_model* m, int l, float* hid, int B, float* ss
       p.ssq = w.ssq_in; p.nssq = d.d / 16; p.inv_div = 1.f / (float)d.d; p.eps = d.eps;
       p.Y = xz; p.ldy = 2 * d.D;
       p.c0 = 0; p.C = d.D; p.Kc = d.K; p.cw = W + Ly.conv_w; p.cb = W + Ly.conv_b;
-      p.cst = conv_st; p.Yc = xc; p.ldyc = d.D; p.Yf = w.yf;
+      p.cst = conv_st; p.Yc = xc; p.ldyc = d.D;
+      if (three) {
+          p.wxt = m->wp + m->wp_xt[l]; p.RN = RN; p.xpart = w.xpart;
+      } else {
+          p.Yf = w.yf;
+      }
       SSM_TRY(ssm::launch_stepproj(ssm::EPI_CONV, p, st)); }
-    { Stage g(c, "m1.step.x_proj");
-      ssm::StepProj p;
-      p.X = w.yf; p.W = m->wp + m->wp_x[l]; p.M = B; p.N = RN; p.K = d.D;
-      p.Y = dbl; p.ldy = RN;
-      SSM_TRY(ssm::launch_stepproj(ssm::EPI_STORE, p, st)); }
-    { Stage g(c, "m1.step.state_update");
-      SSM_TRY(ssm::launch_m1_update_frag(xc, d.D, dbl, RN, m->wp + m->wp_dt[l], d.R,
-                                         W + Ly.dt_b, m->Ab + Ly.A, dbl + d.R, RN,
-                                         dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D, 2 * d.D,
-                                         w.yf, ssm_st, B, d.D, d.N, st)); }
+    if (three) {
+        Stage g(c, "m1.step.state_update");
+        SSM_TRY(ssm::launch_m1_step_update(xc, d.D, w.xpart, RN, (B + 15) / 16 * 16,
+                                           m->wp + m->wp_dt[l], d.R, W + Ly.dt_b, m->Ab + Ly.A,
+                                           W + Ly.Dsk, xz + d.D, 2 * d.D, w.yf, ssm_st, B, d.D,
+                                           d.N, st));
+    } else {
+        { Stage g(c, "m1.step.x_proj");
+          ssm::StepProj p;
+          p.X = w.yf; p.W = m->wp + m->wp_x[l]; p.M = B; p.N = RN; p.K = d.D;
+          p.Y = dbl; p.ldy = RN;
+          SSM_TRY(ssm::launch_stepproj(ssm::EPI_STORE, p, st)); }
+        { Stage g(c, "m1.step.state_update");
+          SSM_TRY(ssm::launch_m1_update_frag(xc, d.D, dbl, RN, m->wp + m->wp_dt[l], d.R,
+                                             W + Ly.dt_b, m->Ab + Ly.A, dbl + d.R, RN,
+                                             dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D,
+                                             2 * d.D, w.yf, ssm_st, B, d.D, d.N, st)); }
+    }
     { Stage g(c, "m1.step.out_proj");
       ssm::StepProj p;
       p.X = w.yf; p.W = m->wp + m->wp_out[l]; p.M = B; p.N = d.d; p.K = d.D;

@@ -857,6 +857,138 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
     else y[(long)b * ldy + d] = acc;
 }
 
+// The fused Mamba-1 step's x_proj reduction, dt_proj and state update (launch_m1_step_update).
+// Workgroup (g, b): sequence b, channels [CPW g, CPW g + CPW), one thread per channel.
+// - The thread's own loads are issued first: its N states and A row (float4), its R-wide
+//   W_dt row (float4), x, z, D, dt_bias.
+// - x_proj of sequence b: dbl[j] = sum over the NP = D / 16 conv tiles of xpart[t, b, j], in a
+//   fixed order that every workgroup of b repeats (Q contiguous runs of tiles, one thread per
+//   (run, j), then the runs in order), into LDS.
+// - dt = softplus(dt_r . W_dt[c] + dt_bias[c]) with dt_r = dbl[0, R) (r in order), then
+//   h = exp(dt A) h + dt x B, y = (C . h + D x) silu(z), with B = dbl[R, R + N) and
+//   C = dbl[R + N, R + 2N) read from LDS.
+// Workgroups of the padding rows (b in [B, M16)) write zeros to their rows of y's fragment
+// order (the out_proj reads whole 16-row tiles) and do nothing else.
+struct M1StepArgs {
+    const float* x; long ldx;
+    const float* xpart; int RN, NP, M16;
+    const float* Wdt; int R;
+    const float* dt_bias; const float* A; const float* Dsk;
+    const float* z; long ldz;
+    float* yf; float* h;
+    int B, D;
+};
+constexpr int kM1StepMaxQ = 8;
+
+template <int N>
+__global__ __launch_bounds__(384) void m1_step_update_kernel(M1StepArgs a) {
+    __shared__ float red[kM1StepMaxQ][ssm::kXpartMaxRN];
+    __shared__ __attribute__((aligned(16))) float dbl[ssm::kXpartMaxRN];
+    const int CPW = blockDim.x;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.y;
+    const int d = blockIdx.x * CPW + tid;
+    const int kb = a.D >> 4;
+    if (b >= a.B) {
+        a.yf[ssm::frag_off(b, d, kb)] = 0.f;
+        return;
+    }
+    // x_proj of sequence b from the partials. Thread (q, j) adds the tiles of run q in order;
+    // its loads are issued before the thread's own (HBM) loads below, in groups of kPer with
+    // clamped indices (a term past the run adds +0), so that one L2 latency covers a group.
+    const int RN = a.RN;
+    // Q runs of at least one tile each (NP = D / 16 >= 4)
+    const int Q = max(1, min(min(kM1StepMaxQ, CPW / RN), a.NP));
+    constexpr int kPer = 32;
+    const long step = (long)a.M16 * RN;
+    const bool red_thread = tid < RN * Q;   // one (q, j) per thread (RN Q <= CPW, else loop)
+    float part = 0.f;
+    int pq = 0, pj = 0, t0 = 0, t1 = 0;
+    if (red_thread) {
+        pj = tid % RN; pq = tid / RN;
+        t0 = pq * a.NP / Q; t1 = (pq + 1) * a.NP / Q;
+    }
+    const float* pbase = a.xpart + (long)b * RN + pj;
+    float pv[kPer];
+    if (red_thread) {
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) pv[u] = pbase[(long)min(t0 + u, t1 - 1) * step];
+    }
+
+    float* hp = a.h + ((long)b * a.D + d) * N;
+    float4 hv[N / 4], av[N / 4];
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+        hv[q] = *reinterpret_cast<const float4*>(hp + 4 * q);
+        av[q] = *reinterpret_cast<const float4*>(a.A + (long)d * N + 4 * q);
+    }
+    const float xx = a.x[(long)b * a.ldx + d];
+    const float zz = a.z[(long)b * a.ldz + d];
+    const float dsk = a.Dsk ? a.Dsk[d] : 0.f;
+    const float bias = a.dt_bias ? a.dt_bias[d] : 0.f;
+
+    if (red_thread) {
+        for (int g = t0;;) {
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) part += g + u < t1 ? pv[u] : 0.f;
+            g += kPer;
+            if (g >= t1) break;
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) pv[u] = pbase[(long)min(g + u, t1 - 1) * step];
+        }
+        red[pq][pj] = part;
+    }
+    // (RN Q > CPW: the remaining (q, j) pairs, with the same order of terms)
+    for (int i = tid + CPW; i < RN * Q; i += CPW) {
+        const int j = i % RN, q = i / RN;
+        const int u0 = q * a.NP / Q, u1 = (q + 1) * a.NP / Q;
+        const float* p = a.xpart + ((long)u0 * a.M16 + b) * RN + j;
+        float sum = 0.f;
+        for (int t = u0; t < u1; ++t, p += step) sum += *p;
+        red[q][j] = sum;
+    }
+    __syncthreads();
+    for (int j = tid; j < RN; j += CPW) {
+        float sum = red[0][j];
+        for (int q = 1; q < Q; ++q) sum += red[q][j];
+        dbl[j] = sum;
+    }
+    __syncthreads();
+
+    // dt_proj, r in order
+    const float* wr = a.Wdt + (long)d * a.R;
+    float raw = 0.f;
+    for (int r = 0; r < a.R; r += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(wr + r);
+        const float4 d4 = *reinterpret_cast<const float4*>(dbl + r);
+        raw = fmaf(d4.x, w4.x, raw);
+        raw = fmaf(d4.y, w4.y, raw);
+        raw = fmaf(d4.z, w4.z, raw);
+        raw = fmaf(d4.w, w4.w, raw);
+    }
+    const float dl = delta_of(raw, bias, 1);
+    const float du = dl * xx;
+    const float* Bv = dbl + a.R;
+    const float* Cv = Bv + N;
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+        float4 v;
+        v.x = fmaf(ssm::ex2(dl * av[q].x * ssm::kLog2e), hv[q].x, du * Bv[4 * q]);
+        v.y = fmaf(ssm::ex2(dl * av[q].y * ssm::kLog2e), hv[q].y, du * Bv[4 * q + 1]);
+        v.z = fmaf(ssm::ex2(dl * av[q].z * ssm::kLog2e), hv[q].z, du * Bv[4 * q + 2]);
+        v.w = fmaf(ssm::ex2(dl * av[q].w * ssm::kLog2e), hv[q].w, du * Bv[4 * q + 3]);
+        *reinterpret_cast<float4*>(hp + 4 * q) = v;
+        acc = fmaf(v.x, Cv[4 * q], acc);
+        acc = fmaf(v.y, Cv[4 * q + 1], acc);
+        acc = fmaf(v.z, Cv[4 * q + 2], acc);
+        acc = fmaf(v.w, Cv[4 * q + 3], acc);
+    }
+    if (a.Dsk) acc = fmaf(dsk, xx, acc);
+    acc *= ssm::silu_fast(zz);
+    a.yf[ssm::frag_off(b, d, kb)] = acc;
+}
+
 }  // namespace
 
 namespace {
@@ -1014,6 +1146,43 @@ ssm_status launch_m1_update_frag(const float* x, long ldx, const float* dtr, lon
                 "m1_update_frag: arguments");
     return launch_m1_update(x, ldx, nullptr, 0, dt_bias, 1, A, Bm, ldb, Cm, ldc, Dsk, z, ldz, yf,
                             0, D / 16, h, B, D, N, st, dtr, lddtr, Wdt, R);
+}
+
+}  // namespace ssm
+
+namespace ssm {
+
+bool m1_step_update_ok(int D, int N, int R) {
+    return D % 64 == 0 && (N == 4 || N == 8 || N == 16 || N == 32 || N == 64) && R >= 4 &&
+           R % 4 == 0 && R + 2 * N <= kXpartMaxRN;
+}
+
+ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, int RN, int M16,
+                                 const float* Wdt, int R, const float* dt_bias, const float* A,
+                                 const float* Dsk, const float* z, long ldz, float* yf, float* h,
+                                 int B, int D, int N, hipStream_t st) {
+    SSM_REQUIRE(x && xpart && Wdt && A && z && yf && h && B >= 1 && M16 >= B && M16 % 16 == 0 &&
+                    RN == R + 2 * N && m1_step_update_ok(D, N, R) &&
+                    ((uintptr_t)Wdt & 15) == 0 && ((uintptr_t)h & 15) == 0 &&
+                    ((uintptr_t)A & 15) == 0,
+                "m1_step_update: arguments");
+    // channels per workgroup: the largest of 384, 256, 192, 128, 64 that divides D
+    int cpw = 64;
+    for (int c : {384, 256, 192, 128})
+        if (D % c == 0) { cpw = c; break; }
+    M1StepArgs a;
+    a.x = x; a.ldx = ldx; a.xpart = xpart; a.RN = RN; a.NP = D / 16; a.M16 = M16;
+    a.Wdt = Wdt; a.R = R; a.dt_bias = dt_bias; a.A = A; a.Dsk = Dsk; a.z = z; a.ldz = ldz;
+    a.yf = yf; a.h = h; a.B = B; a.D = D;
+    const dim3 grid((unsigned)(D / cpw), (unsigned)M16);
+    switch (N) {
+        case 4: m1_step_update_kernel<4><<<grid, cpw, 0, st>>>(a); break;
+        case 8: m1_step_update_kernel<8><<<grid, cpw, 0, st>>>(a); break;
+        case 16: m1_step_update_kernel<16><<<grid, cpw, 0, st>>>(a); break;
+        case 32: m1_step_update_kernel<32><<<grid, cpw, 0, st>>>(a); break;
+        default: m1_step_update_kernel<64><<<grid, cpw, 0, st>>>(a); break;
+    }
+    return check_launch("m1_step_update");
 }
 
 }  // namespace ssm

@@ -12,7 +12,10 @@
 //              operand xg[m, n] = Y[m, n] * g2[n] (in fragment order, below) and the row's
 //              partial sum of squares over the tile's 16 columns, ssq_out[m, n / 16]
 //   Yf         EPI_CONV: the conv outputs also written in fragment order, the operand of the
-//              step's next projection (the Mamba-1 step's x_proj)
+//              step's next projection (the Mamba-1 step's x_proj as its own launch)
+//   xpart      EPI_CONV: that next projection summed over each conv tile's 16 channels (one
+//              partial row per tile and row), so that no launch of its own is needed: the
+//              Mamba-1 step's state update adds the partials
 //
 // The RMSNorms of the step are carried this way: the producer of a row writes x * g and
 // partial sums of x^2 per 16 columns, and the consumer's epilogue applies 1 / rms(x) as the
@@ -56,6 +59,9 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 constexpr int kNW = 4;                  // waves per workgroup
 constexpr unsigned kOOR = 0x80000000u;  // a buffer offset past every descriptor's range
 constexpr int kSsqPer = kStepProjMaxSsq / 16;   // partial sums per epilogue thread
+// EPI_CONV with xpart as a kernel of its own (its B fragments need registers that the plain
+// conv epilogue's occupancy target does not leave)
+constexpr int EPI_CONVX = 3;
 
 __device__ __forceinline__ float sum16(float v) {
 #pragma unroll
@@ -64,7 +70,9 @@ __device__ __forceinline__ float sum16(float v) {
 }
 
 template <int PD, int EPI>
-__global__ __launch_bounds__(64 * kNW, PD <= 4 ? 8 : 5) void stepproj_kernel(StepProj a) {
+__global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD <= 4 ? 8 : 5) void stepproj_kernel(
+    StepProj a) {
+    constexpr bool CONV = EPI == EPI_CONV || EPI == EPI_CONVX;
     __shared__ float red[kNW][16][17];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, q = lane >> 4;
@@ -85,6 +93,27 @@ __global__ __launch_bounds__(64 * kNW, PD <= 4 ? 8 : 5) void stepproj_kernel(Ste
         for (int u = 0; u < kSsqPer; ++u) {
             const int j = u * 16 + ej;
             sp[u] = bload4(rs, j < a.nssq ? (unsigned)(em * a.nssq + j) * 4u : kOOR);
+        }
+    }
+
+    // EPI_CONV with xpart: a tile of conv columns (16 channels; c0 and C are multiples of 16)
+    // also projects its 16 x 16 conv outputs onto the next projection's RN columns on the
+    // matrix cores (the tile's outputs as the A operand, its 16 rows of wxt as B). Wave w takes
+    // the 16-column blocks w, w + 4, ...; its B fragments are loaded here (lane (j, k) of
+    // k-step s: wxt[channel 4s + k][16 block + j]) so that they arrive with the operands.
+    constexpr int kXpBlk = kXpartMaxRN / 16 / kNW;   // column blocks per wave
+    const bool xp_tile = EPI == EPI_CONVX && n0 >= a.c0 && n0 < a.c0 + a.C;
+    float wxb[kXpBlk][4];
+    if constexpr (EPI == EPI_CONVX) {
+        if (xp_tile) {
+#pragma unroll
+            for (int t = 0; t < kXpBlk; ++t) {
+                const int col = 16 * (w + kNW * t) + l16;
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+                    wxb[t][s4] = col < a.RN ? a.wxt[(long)(n0 - a.c0 + 4 * s4 + q) * a.RN + col]
+                                            : 0.f;
+            }
         }
     }
 
@@ -152,33 +181,54 @@ __global__ __launch_bounds__(64 * kNW, PD <= 4 ? 8 : 5) void stepproj_kernel(Ste
             float* y = a.Y + (long)em * a.ldy + en;
             *y = a.beta != 0.f ? v + a.beta * *y : v;
         }
-    } else if constexpr (EPI == EPI_CONV) {
+    } else if constexpr (CONV) {
         const int c = en - a.c0;
         const bool in_conv = c >= 0 && c < a.C;
-        if (!ok) {
-            // padding rows of the fragment-order copy: zeros for the next projection
-            if (a.Yf && in_conv && en < a.N) a.Yf[frag_off(em, c, a.C >> 4)] = 0.f;
-            return;
+        float u = 0.f;   // the conv output; 0 on padding rows
+        if (ok && !in_conv) a.Y[(long)em * a.ldy + en] = v;
+        if (ok && in_conv) {
+            // same arithmetic order as the conv update kernel (conv1d.hip)
+            const int Kc = a.Kc;
+            const float* wc = a.cw + (long)c * Kc;
+            float* s = a.cst + ((long)em * a.C + c) * (Kc - 1);
+            float acc = a.cb ? a.cb[c] : 0.f;
+            for (int k = 0; k < Kc - 1; ++k) {   // taps on the cached inputs, shifting them down
+                const float sv = s[k];
+                acc = fmaf(wc[k], sv, acc);
+                if (k > 0) s[k - 1] = sv;
+            }
+            acc = fmaf(wc[Kc - 1], v, acc);
+            if (Kc > 1) s[Kc - 2] = v;
+            u = silu_fast(acc);
+            a.Yc[(long)em * a.ldyc + c] = u;
         }
-        if (!in_conv) {
-            a.Y[(long)em * a.ldy + en] = v;
-            return;
+        // padding rows of the fragment-order copy get zeros for the next projection
+        if (a.Yf && in_conv && en < a.N) a.Yf[frag_off(em, c, a.C >> 4)] = u;
+        if constexpr (EPI == EPI_CONVX) {
+            if (xp_tile) {   // uniform over the workgroup
+                __shared__ float us[16][17];
+                us[ei][ej] = u;
+                __syncthreads();
+                // D[i][j] = sum_s sum_k u[i][4s + k] wxt[4s + k][j]; lane (j, q) holds
+                // rows 4q .. 4q + 3
+                const int ct = (n0 - a.c0) >> 4;
+#pragma unroll
+                for (int t = 0; t < kXpBlk; ++t) {
+                    const int blk = w + kNW * t;
+                    if (16 * blk >= a.RN) break;   // wave-uniform
+                    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4)
+                        acc = mfma4(us[l16][4 * s4 + q], wxb[t][s4], acc);
+                    const int col = 16 * blk + l16;
+                    if (col < a.RN) {
+                        float* dst = a.xpart + ((long)ct * 16 * a.mt + m0 + 4 * q) * a.RN + col;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) dst[(long)r * a.RN] = acc[r];
+                    }
+                }
+            }
         }
-        // same arithmetic order as the conv update kernel (conv1d.hip)
-        const int Kc = a.Kc;
-        const float* wc = a.cw + (long)c * Kc;
-        float* s = a.cst + ((long)em * a.C + c) * (Kc - 1);
-        float acc = a.cb ? a.cb[c] : 0.f;
-        for (int k = 0; k < Kc - 1; ++k) {   // taps on the cached inputs, shifting them down
-            const float sv = s[k];
-            acc = fmaf(wc[k], sv, acc);
-            if (k > 0) s[k - 1] = sv;
-        }
-        acc = fmaf(wc[Kc - 1], v, acc);
-        if (Kc > 1) s[Kc - 2] = v;
-        const float u = silu_fast(acc);
-        a.Yc[(long)em * a.ldyc + c] = u;
-        if (a.Yf) a.Yf[frag_off(em, c, a.C >> 4)] = u;
     } else {   // EPI_RESID
         float o = 0.f;
         if (ok) {
@@ -232,11 +282,25 @@ __global__ __launch_bounds__(256) void pack_frag_kernel(const float* __restrict_
     reinterpret_cast<float4*>(out)[i] = v;
 }
 
+// W (N, K) row stride ldw -> W^T (K, N) row-major, out[k N + n] = W[n ldw + k]: the conv
+// epilogue's x_proj slice of a tile is then 16 contiguous rows. One thread per element (runs
+// once per weight change).
+__global__ __launch_bounds__(256) void pack_t_kernel(const float* __restrict__ W, long ldw,
+                                                     int N, int K, float* __restrict__ out) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)N * K) return;
+    const int k = (int)(i / N), n = (int)(i % N);
+    out[i] = W[(long)n * ldw + k];
+}
+
 template <int PD>
 ssm_status launch_pd(int epi, const StepProj& a, unsigned grid, hipStream_t st) {
     switch (epi) {
         case EPI_STORE: stepproj_kernel<PD, EPI_STORE><<<grid, 64 * kNW, 0, st>>>(a); break;
-        case EPI_CONV: stepproj_kernel<PD, EPI_CONV><<<grid, 64 * kNW, 0, st>>>(a); break;
+        case EPI_CONV:
+            if (a.xpart) stepproj_kernel<PD, EPI_CONVX><<<grid, 64 * kNW, 0, st>>>(a);
+            else stepproj_kernel<PD, EPI_CONV><<<grid, 64 * kNW, 0, st>>>(a);
+            break;
         default: stepproj_kernel<PD, EPI_RESID><<<grid, 64 * kNW, 0, st>>>(a); break;
     }
     return check_launch("stepproj");
@@ -260,6 +324,13 @@ ssm_status launch_pack_frag(const float* W, long ldw, int N, int K, float* out, 
     return check_launch("pack_frag");
 }
 
+ssm_status launch_pack_t(const float* W, long ldw, int N, int K, float* out, hipStream_t st) {
+    SSM_REQUIRE(W && out && N >= 1 && K >= 1 && ldw >= K, "pack_t: arguments");
+    const long n = (long)N * K;
+    pack_t_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(W, ldw, N, K, out);
+    return check_launch("pack_t");
+}
+
 ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st) {
     SSM_REQUIRE(stepproj_ok(a.M, a.N, a.K) && ((uintptr_t)a.X & 15) == 0 &&
                     ((uintptr_t)a.W & 15) == 0,
@@ -271,6 +342,9 @@ ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st) {
                 "stepproj: residual epilogue arguments");
     SSM_REQUIRE(!a.Yf || (epi == EPI_CONV && a.C % 16 == 0),
                 "stepproj: fragment-order copy arguments");
+    SSM_REQUIRE(!a.xpart || (epi == EPI_CONV && a.wxt && a.RN >= 1 && a.RN <= kXpartMaxRN &&
+                             a.c0 % 16 == 0 && a.C % 16 == 0),
+                "stepproj: x_proj partial arguments");
     a.mt = (a.M + 15) / 16;
     a.nt = (a.N + 15) / 16;
     const unsigned grid = (unsigned)(8L * a.mt * ((a.nt + 7) / 8));
