@@ -104,8 +104,8 @@ ssm_status launch_m1_update_frag(const float* x, long ldx, const float* dtr, lon
 // The fused Mamba-1 step's x_proj reduction, dt_proj and state update in one launch: x_proj
 // arrives as the conv epilogue's per-tile partials xpart (D / 16, M16, RN) (M16 = B rounded up
 // to 16; RN = R + 2N = (dt_r, B, C)), added per sequence in a fixed order; dt = softplus(dt_r
-// Wdt^T + dt_bias) (Wdt (D, R) row-major); y = (C.h + D x) silu(z) in fragment order (K = D,
-// rows B .. M16-1 zero), the out_proj's operand.
+// Wdt^T + dt_bias) with Wdt (D, R) in quads (launch_pack_q4); y = (C.h + D x) silu(z) in
+// fragment order (K = D, rows B .. M16-1 zero), the out_proj's operand.
 bool m1_step_update_ok(int D, int N, int R);
 ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, int RN, int M16,
                                  const float* Wdt, int R, const float* dt_bias, const float* A,
@@ -113,6 +113,8 @@ ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, i
                                  int B, int D, int N, hipStream_t st);
 // W (N, K) row stride ldw -> its transpose (K, N) row-major in out.
 ssm_status launch_pack_t(const float* W, long ldw, int N, int K, float* out, hipStream_t st);
+// W (N, K) row-major (K % 4 == 0) -> quads: out[((k / 4) N + n) 4 + k % 4] = W[n, k].
+ssm_status launch_pack_q4(const float* W, int N, int K, float* out, hipStream_t st);
 // xg = x * g in fragment order (K = d) and ssq (M, d / 16) partial sums of x^2: the first
 // RMSNorm of a step.
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,

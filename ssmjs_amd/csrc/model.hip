@@ -1103,13 +1103,17 @@ ssm_status pack_weights(ssm_model* m) {
             if (m->wp_x[l] >= 0)
                 SSM_TRY(ssm::launch_pack_frag(m->w + Ly.x_proj, d.D, RN, d.D, m->wp + m->wp_x[l],
                                               st));
-            // dt_proj is formed inside the state update from row-major rows: an aligned copy
-            SSM_HIP_TRY(hipMemcpyAsync(m->wp + m->wp_dt[l], m->w + Ly.dt_w,
-                                       sizeof(float) * (size_t)d.D * d.R,
-                                       hipMemcpyDeviceToDevice, st));
-            if (m->wp_xt[l] >= 0)
+            // dt_proj is formed inside the state update: its rows in quads for the three-launch
+            // step's update, else an aligned row-major copy
+            if (m->wp_xt[l] >= 0) {
+                SSM_TRY(ssm::launch_pack_q4(m->w + Ly.dt_w, d.D, d.R, m->wp + m->wp_dt[l], st));
                 SSM_TRY(ssm::launch_pack_t(m->w + Ly.x_proj, d.D, RN, d.D, m->wp + m->wp_xt[l],
                                            st));
+            } else {
+                SSM_HIP_TRY(hipMemcpyAsync(m->wp + m->wp_dt[l], m->w + Ly.dt_w,
+                                           sizeof(float) * (size_t)d.D * d.R,
+                                           hipMemcpyDeviceToDevice, st));
+            }
         } else {
             SSM_TRY(ssm::launch_pack_frag(m->w + Ly.in_proj, d.d, d.nin, d.d, m->wp + m->wp_in[l],
                                           st));

@@ -859,11 +859,12 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
 
 // The fused Mamba-1 step's x_proj reduction, dt_proj and state update (launch_m1_step_update).
 // Workgroup (g, b): sequence b, channels [CPW g, CPW g + CPW), one thread per channel.
-// - The thread's own loads are issued first: its N states and A row (float4), its R-wide
-//   W_dt row (float4), x, z, D, dt_bias.
 // - x_proj of sequence b: dbl[j] = sum over the NP = D / 16 conv tiles of xpart[t, b, j], in a
 //   fixed order that every workgroup of b repeats (Q contiguous runs of tiles, one thread per
-//   (run, j), then the runs in order), into LDS.
+//   (run, j), then the runs in order), into LDS. These loads are issued first (they come from
+//   L2), then the thread's own: its N states and A row (float4), x, z, D, dt_bias, and its W_dt
+//   row, stored in quads (W_dt[c, 4i .. 4i+3] at (i D + c) 4, so that a wave's float4 loads are
+//   contiguous); all are in flight before the first wait.
 // - dt = softplus(dt_r . W_dt[c] + dt_bias[c]) with dt_r = dbl[0, R) (r in order), then
 //   h = exp(dt A) h + dt x B, y = (C . h + D x) silu(z), with B = dbl[R, R + N) and
 //   C = dbl[R + N, R + 2N) read from LDS.
@@ -879,6 +880,7 @@ struct M1StepArgs {
     int B, D;
 };
 constexpr int kM1StepMaxQ = 8;
+constexpr int kM1StepMaxRQ = 16;   // W_dt quads per thread (R <= 64)
 
 template <int N>
 __global__ __launch_bounds__(384) void m1_step_update_kernel(M1StepArgs a) {
@@ -926,6 +928,11 @@ __global__ __launch_bounds__(384) void m1_step_update_kernel(M1StepArgs a) {
     const float zz = a.z[(long)b * a.ldz + d];
     const float dsk = a.Dsk ? a.Dsk[d] : 0.f;
     const float bias = a.dt_bias ? a.dt_bias[d] : 0.f;
+    const int rq = a.R >> 2;
+    float4 wq[kM1StepMaxRQ];   // quads past rq repeat the last one (in bounds, unused)
+#pragma unroll
+    for (int i = 0; i < kM1StepMaxRQ; ++i)
+        wq[i] = *reinterpret_cast<const float4*>(a.Wdt + ((long)min(i, rq - 1) * a.D + d) * 4);
 
     if (red_thread) {
         for (int g = t0;;) {
@@ -956,15 +963,16 @@ __global__ __launch_bounds__(384) void m1_step_update_kernel(M1StepArgs a) {
     __syncthreads();
 
     // dt_proj, r in order
-    const float* wr = a.Wdt + (long)d * a.R;
     float raw = 0.f;
-    for (int r = 0; r < a.R; r += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(wr + r);
-        const float4 d4 = *reinterpret_cast<const float4*>(dbl + r);
-        raw = fmaf(d4.x, w4.x, raw);
-        raw = fmaf(d4.y, w4.y, raw);
-        raw = fmaf(d4.z, w4.z, raw);
-        raw = fmaf(d4.w, w4.w, raw);
+#pragma unroll
+    for (int i = 0; i < kM1StepMaxRQ; ++i) {
+        if (i < rq) {   // (uniform; a break here would send wq to scratch memory)
+            const float4 d4 = *reinterpret_cast<const float4*>(dbl + 4 * i);
+            raw = fmaf(d4.x, wq[i].x, raw);
+            raw = fmaf(d4.y, wq[i].y, raw);
+            raw = fmaf(d4.z, wq[i].z, raw);
+            raw = fmaf(d4.w, wq[i].w, raw);
+        }
     }
     const float dl = delta_of(raw, bias, 1);
     const float du = dl * xx;
@@ -1153,8 +1161,9 @@ ssm_status launch_m1_update_frag(const float* x, long ldx, const float* dtr, lon
 namespace ssm {
 
 bool m1_step_update_ok(int D, int N, int R) {
-    return D % 64 == 0 && (N == 4 || N == 8 || N == 16 || N == 32 || N == 64) && R >= 4 &&
-           R % 4 == 0 && R + 2 * N <= kXpartMaxRN;
+    // (N = 64 would hold 128 state and A registers per thread next to the prefetched rows)
+    return D % 64 == 0 && (N == 4 || N == 8 || N == 16 || N == 32) && R >= 4 &&
+           R % 4 == 0 && R <= 4 * kM1StepMaxRQ && R + 2 * N <= kXpartMaxRN;
 }
 
 ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, int RN, int M16,
@@ -1179,8 +1188,7 @@ ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, i
         case 4: m1_step_update_kernel<4><<<grid, cpw, 0, st>>>(a); break;
         case 8: m1_step_update_kernel<8><<<grid, cpw, 0, st>>>(a); break;
         case 16: m1_step_update_kernel<16><<<grid, cpw, 0, st>>>(a); break;
-        case 32: m1_step_update_kernel<32><<<grid, cpw, 0, st>>>(a); break;
-        default: m1_step_update_kernel<64><<<grid, cpw, 0, st>>>(a); break;
+        default: m1_step_update_kernel<32><<<grid, cpw, 0, st>>>(a); break;
     }
     return check_launch("m1_step_update");
 }

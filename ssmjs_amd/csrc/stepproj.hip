@@ -293,6 +293,18 @@ __global__ __launch_bounds__(256) void pack_t_kernel(const float* __restrict__ W
     out[i] = W[(long)n * ldw + k];
 }
 
+// W (N, K) row-major -> quads, out[((k / 4) N + n) 4 + k % 4] = W[n K + k]: a thread that owns
+// row n reads its quads as float4s that are contiguous across a wave (the Mamba-1 step's
+// dt_proj rows). One thread per quad (runs once per weight change).
+__global__ __launch_bounds__(256) void pack_q4_kernel(const float* __restrict__ W, int N, int K,
+                                                      float4* __restrict__ out) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;   // quad index (k / 4) N + n
+    if (i >= (long)N * (K / 4)) return;
+    const int n = (int)(i % N), k4 = (int)(i / N);
+    const float* r = W + (long)n * K + 4 * k4;
+    out[i] = make_float4(r[0], r[1], r[2], r[3]);
+}
+
 template <int PD>
 ssm_status launch_pd(int epi, const StepProj& a, unsigned grid, hipStream_t st) {
     switch (epi) {
@@ -329,6 +341,14 @@ ssm_status launch_pack_t(const float* W, long ldw, int N, int K, float* out, hip
     const long n = (long)N * K;
     pack_t_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(W, ldw, N, K, out);
     return check_launch("pack_t");
+}
+
+ssm_status launch_pack_q4(const float* W, int N, int K, float* out, hipStream_t st) {
+    SSM_REQUIRE(W && out && N >= 1 && K >= 4 && K % 4 == 0 && ((uintptr_t)out & 15) == 0,
+                "pack_q4: arguments");
+    const long n = (long)N * (K / 4);
+    pack_q4_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(W, N, K, (float4*)out);
+    return check_launch("pack_q4");
 }
 
 ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st) {
