@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_obj")
 LIB = os.path.join(HERE, "libssm_hip.so")
 SOURCES = ["conv1d.hip", "scan_m1.hip", "ssd.hip", "ssd_f32.hip", "glue.hip", "rowgemm.hip",
-           "stepproj.hip", "gemm.hip", "sample.hip", "model.hip"]
+           "stepproj.hip", "head.hip", "gemm.hip", "sample.hip", "model.hip"]
 ARCH = os.environ.get("SSM_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 NAPI_SRC = os.path.join(HERE, "napi", "ssm_napi.cc")

@@ -115,6 +115,15 @@ ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, i
 ssm_status launch_pack_t(const float* W, long ldw, int N, int K, float* out, hipStream_t st);
 // W (N, K) row-major (K % 4 == 0) -> quads: out[((k / 4) N + n) 4 + k % 4] = W[n, k].
 ssm_status launch_pack_q4(const float* W, int N, int K, float* out, hipStream_t st);
+// The one-token LM head (head.hip): y (M, V) [ldy] = s[m] xg E^T with xg (M, K) in fragment
+// order, s[m] = 1 / sqrt(inv_div sum_j ssq[m, j] + eps), Ef the fragment-order copy of E
+// (V, K); with argmax, also the greedy pick per row (largest logit, lowest index among equal
+// maxima). part: head_parts(V) pairs per row of workspace.
+bool head_ok(int M, int V, int K);
+int head_parts(int V);
+ssm_status launch_head(const float* xg, const float* ssq, int nssq, float inv_div, float eps,
+                       const float* Ef, float* y, long ldy, int M, int V, int K, float* part,
+                       uint32_t* argmax, hipStream_t st);
 // xg = x * g in fragment order (K = d) and ssq (M, d / 16) partial sums of x^2: the first
 // RMSNorm of a step.
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,

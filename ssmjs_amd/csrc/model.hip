@@ -522,6 +522,7 @@ struct ssm_model {
     std::vector<long> wp_in, wp_out;   // float offsets into wp per layer (-1: not packed)
     std::vector<long> wp_x, wp_dt;     // Mamba-1 layers: x_proj and dt_proj
     std::vector<long> wp_xt;           // Mamba-1 layers: x_proj transposed, (D, R + 2N)
+    long wp_emb = -1;                  // the tied embedding for the one-token LM head
     // bf16 copies of the Mamba-2 layers' in_proj and out_proj for the bf16-input layer, built
     // at its first call and rebuilt whenever the weights change
     __bf16* wb = nullptr;
@@ -708,6 +709,8 @@ struct Ws {
     // the Mamba-1 step's x_proj partials (stepproj.hip, xpart); null for longer sequences or
     // without Mamba-1 layers
     float* xpart;
+    // the one-token LM head's argmax partials (head.hip); null for longer sequences
+    float* hpart;
     void* scan;
     size_t scan_bytes;
 };
@@ -755,6 +758,8 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
     size_t o_sqy = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
     const size_t nxp = has1 ? (size_t)(d.D / 16) * nstep16 * (d.R + 2 * d.N) : 0;
     size_t o_xp = off; off += al(4 * nxp);
+    const size_t nhp = nstep ? nstep * (size_t)ssm::head_parts(d.V) * 2 : 0;
+    size_t o_hp = off; off += al(4 * nhp);
     if (out) {
         char* base = m->ws;
         out->hid = (float*)(base + o_hid); out->nrm = (float*)(base + o_nrm);
@@ -768,6 +773,7 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
         out->ssq_in = nstep ? (float*)(base + o_sqi) : nullptr;
         out->ssq_y = nstep ? (float*)(base + o_sqy) : nullptr;
         out->xpart = nxp ? (float*)(base + o_xp) : nullptr;
+        out->hpart = nhp ? (float*)(base + o_hp) : nullptr;
     }
     return off;
 }
@@ -1090,6 +1096,10 @@ ssm_status pack_weights(ssm_model* m) {
             }
             m->wp_out[l] = off; off += (long)ssm::frag_floats(d.d, d.D);
         }
+        if (ssm::head_ok(1, d.V, d.d)) {
+            m->wp_emb = off;
+            off += (long)ssm::frag_floats(d.V, d.d);
+        }
         if (off == 0) return SSM_OK;
         SSM_HIP_TRY(ssm::dev_malloc((void**)&m->wp, (size_t)off * sizeof(float)));
     }
@@ -1121,6 +1131,8 @@ ssm_status pack_weights(ssm_model* m) {
         SSM_TRY(ssm::launch_pack_frag(m->w + Ly.out_proj, d.D, d.d, d.D, m->wp + m->wp_out[l],
                                       st));
     }
+    if (m->wp_emb >= 0)
+        SSM_TRY(ssm::launch_pack_frag(m->w + m->emb, d.d, d.V, d.d, m->wp + m->wp_emb, st));
     return SSM_OK;
 }
 
@@ -1235,9 +1247,12 @@ ssm_status mixer_step_fused(ssm_model* m, int l, float* hid, int B, float* ssm_s
 }
 
 // embeddings -> layers; then the final norm into w.nrm unless `final_norm` is false (the
-// one-token path, whose LM head applies it in its prologue: the result stays in w.hid).
+// one-token path, whose LM head applies it in its prologue: the result stays in w.hid). With
+// `head_operand` (one-token steps into the own LM head), the final norm's operand hid * g_f and
+// its partial sums go to w.xg / w.ssq_in instead: written by the last layer's out_proj when
+// that layer takes the fused step, else by xg_ssq_kernel.
 ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s, const Ws& w,
-                 bool final_norm = true) {
+                 bool final_norm = true, bool head_operand = false) {
     const Dims& d = m->dm;
     hipStream_t st = m->ctx->stream;
     const long T = (long)B * L;
@@ -1256,9 +1271,11 @@ ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s
                 if (!pre)
                     SSM_TRY(ssm::launch_xg_ssq(w.hid, d.d, m->w + Ly.norm, w.xg, w.ssq_in, B, d.d,
                                                st));
+                const bool last_op = !nx && head_operand;
                 SSM_TRY(mixer_step_fused(m, l, w.hid, B, ss, cs, w,
-                                         next_fused ? m->w + nx->norm : nullptr));
-                pre = next_fused;
+                                         next_fused ? m->w + nx->norm
+                                                    : last_op ? m->w + m->norm_f : nullptr));
+                pre = next_fused || last_op;
                 normed = false;
             } else {
                 const float* g_next = nx && !next_fused ? m->w + nx->norm : nullptr;
@@ -1269,6 +1286,11 @@ ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s
             SSM_TRY(ssm_rmsnorm(w.hid, d.d, m->w + Ly.norm, w.nrm, d.d, (int)T, d.d, d.eps, st));
             SSM_TRY(mixer(m, Ly, w.nrm, w.hid, 1.f, B, L, ss, cs, w));
         }
+    }
+    if (head_operand) {
+        if (!pre || d.nl == 0)
+            SSM_TRY(ssm::launch_xg_ssq(w.hid, d.d, m->w + m->norm_f, w.xg, w.ssq_in, B, d.d, st));
+        return SSM_OK;
     }
     if (!final_norm) return SSM_OK;
     return ssm_rmsnorm(w.hid, d.d, m->w + m->norm_f, w.nrm, d.d, (int)T, d.d, d.eps, st);
@@ -1690,7 +1712,17 @@ ssm_status decode_body(ssm_model* m, ssm_state* s, const uint32_t* d_ids, float*
     const Dims& d = m->dm;
     Ws w;
     SSM_TRY(ensure_ws(m, s->B, 1, false, &w));
-    SSM_TRY(trunk(m, d_ids, s->B, 1, s, w, false));
+    // the own LM head (head.hip) on the fragment-order embedding, with the final norm's scale
+    // and the greedy pick folded in
+    const bool own_head = w.xg && w.hpart && ssm::head_ok(s->B, d.V, d.d) && d.d % 16 == 0;
+    if (own_head && !m->wp) SSM_TRY(pack_weights(m));   // eager: the first step never replays
+    SSM_TRY(trunk(m, d_ids, s->B, 1, s, w, false, own_head));
+    if (own_head) {
+        Stage g(m->ctx, "head");
+        return ssm::launch_head(w.xg, w.ssq_in, d.d / 16, 1.f / (float)d.d, d.eps,
+                                m->wp + m->wp_emb, lg, d.V, s->B, d.V, d.d, w.hpart, d_argmax,
+                                m->ctx->stream);
+    }
     { Stage g(m->ctx, "head");
       SSM_TRY(proj_rows(m, 1, w.hid, d.d, nullptr, 0, m->w + m->norm_f, m->w + m->emb, lg, d.V,
                         s->B, d.V, d.d, 0.f, w.nrm)); }

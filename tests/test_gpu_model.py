@@ -138,6 +138,44 @@ def test_greedy_ids_bit_exact(device, layers, N):
     m.destroy()
 
 
+@pytest.mark.parametrize("B", [4, 40])
+def test_greedy_exact_ties_pick_lowest_index(device, B):
+    """Every embedding row is +v or -v, so every logit of a row is one of two values, tied
+    across the whole vocabulary: the one-token LM head's per-block picks and their merge must
+    give the lowest index of the larger value, as the oracle's greedy pick does. +v rows start
+    at 130, past the first 128-column block; B = 40 spans three row tiles."""
+    case(f"greedy exact ties, {B} sequences")
+    from ssmjs_amd import backend, checkpoint
+    V = 1024
+    cfg = {"vocabSize": V, "dModel": 128, "numLayers": 2, "dState": 16, "dConv": 4,
+           "expand": 2, "nHeads": 4, "nGroups": 1, "layers": [{"type": "mamba1"}] * 2}
+    m = backend.Model(device, cfg, seed=11)
+    dims, T = checkpoint.unpack(m.export_weights())
+    v = T["embedding"][0] * 40.0
+    plus = (np.arange(V) % 3 == 1) & (np.arange(V) >= 130)
+    T["embedding"] = np.where(plus[:, None], v[None, :], -v[None, :]).astype(np.float32)
+    blob = checkpoint.pack(dims, T)
+    m.load_weights(blob)
+    om = O.Model(blob)
+    prompt = np.random.default_rng(5).integers(0, V, (B, 6)).astype(np.uint32)
+    st = m.new_state(B)
+    ost = om.new_state(B)
+    st.prefill(prompt)
+    ost.prefill(prompt)
+    ids = prompt[:, -1]
+    for _ in range(4):
+        lg, got = st.decode(ids)
+        ref = ost.decode(ids)
+        close(lg, ref, "logits")
+        top = ref.max(axis=1, keepdims=True)
+        want = np.argmax(ref == top, axis=1)     # lowest index among the maxima
+        assert len(np.unique(ref[0])) == 2, "logits are not two tied values"
+        np.testing.assert_array_equal(got, want)
+        ids = want.astype(np.uint32)
+    st.destroy()
+    m.destroy()
+
+
 def test_decode_graph_replay_matches_eager(device, monkeypatch):
     """Repeated one-token steps replay a captured HIP graph (from the second step with the same
     buffers on). Every replayed step must give the same bits as eager launches from the same
