@@ -56,28 +56,26 @@ PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0}   # dense MFMA, TFLOP/s
 
 METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 
-# Measured HBM bytes per launch of each workload's dominant stage: rocprofv3 --pmc FETCH_SIZE
-# and WRITE_SIZE (one counter per run) of `bench.py --workload <w>`, FETCH_SIZE scaled by 2.0
-# and WRITE_SIZE by 1.0 (what `bench.py --workload copy`, 1 GiB read + 1 GiB written, reads on
-# the same counters). The commands and per-kernel counts sit with the rocprof summaries in
-# profiles/. Re-measured when the
-# kernels change; None where not measured.
+# Measured HBM bytes per launch of each workload's dominant stages: rocprofv3 --pmc
+# TCC_EA0_RDREQ_DRAM_32B_sum and TCC_EA0_WRREQ_WRITE_DRAM_32B_sum of `bench.py --workload <w>`
+# (gfx950's DRAM request counters in 32-byte units, a 128-byte request counting 4), times 32:
+# exact bytes, no scale factor (on `bench.py --workload copy`, 1 GiB read + 1 GiB written, they
+# read 1.0000 GiB each way). The commands and per-kernel counts sit with the rocprof summaries
+# in profiles/. Re-measured when the kernels change; None where not measured.
 TRAFFIC = {
-    ("cfg2", "m1.in_proj"): 268_210_726,               # gemm_f32_kernel<4>
-    ("cfg2", "m1.x_dt_proj"): 111_058_521,             # xproj_dt_kernel
-    ("cfg2", "m1.out_proj"): 113_500_326,              # gemm_f32_kernel<3>
-    ("cfg3", "bf16"): 847_867_904,                     # ssd_kernel (two heads per workgroup)
-    ("cfg3", "f32"): 1_132_641_280,                    # ssd_f32_kernel (two heads per workgroup)
-    ("cfg4", "m2.step.state_update"): 136_517_632,     # m2_update_kernel
-    ("cfg5", "bf16"): 1_202_457_600,                   # state pass + combine + full pass
+    ("cfg2", "m1.in_proj"): 345_610_228,               # gemm_f32_kernel<4>
+    ("cfg2", "m1.conv"): 110_209_453,                  # conv1d_fwd
+    ("cfg2", "m1.x_dt_proj"): 111_384_987,             # xproj_dt_kernel
+    ("cfg2", "m1.scan"): 205_000_625,                  # scan_w16_kernel
+    ("cfg2", "m1.out_proj"): 159_900_310,              # gemm_f32_kernel<3>
+    ("cfg3", "bf16"): 847_585_780,                     # ssd_kernel (two heads per workgroup)
+    ("cfg3", "f32"): 1_132_551_840,                    # ssd_f32_kernel (two heads per workgroup)
+    ("cfg4", "m2.step.state_update"): 136_414_806,     # m2_update_kernel (timed on its own)
+    ("cfg5", "bf16"): 1_202_469_259,                   # state pass + combine + full pass
 }
-# The commit of the kernels each TRAFFIC entry was measured on (profiles/hbm_traffic.md);
-# an entry goes stale when its kernel changes after that commit.
-TRAFFIC_MEASURED_AT = {k: "e7034fa" for k in TRAFFIC}
-TRAFFIC_MEASURED_AT.update({("cfg3", "f32"): "8ed3fba", ("cfg3", "bf16"): "885971e",
-                            ("cfg5", "bf16"): "885971e", ("cfg2", "m1.in_proj"): "6da5abd",
-                            ("cfg2", "m1.x_dt_proj"): "6da5abd", ("cfg2", "m1.out_proj"): "6da5abd",
-                            ("cfg4", "m2.step.state_update"): "7c96b77"})
+# The commit of the build each TRAFFIC entry was measured on (profiles/hbm_traffic.md); an
+# entry goes stale when its kernel changes after that commit.
+TRAFFIC_MEASURED_AT = {k: "1b2f2f1" for k in TRAFFIC}
 
 
 def parse():
@@ -648,7 +646,7 @@ def w_cfg4(torch, np, dev, args):
         if kk in alg:
             f, b = alg[kk]
             stages[kk] = roofline(kk, avg, f, b, "f32", "hbm" if f is None else None,
-                                  TRAFFIC.get(("cfg4", kk)))
+                                  TRAFFIC.get(("cfg4", kk)), ("cfg4", kk))
     step_bytes = nl * sum(v[1] for v in alg.values()) + 4.0 * V * d
     dom = max(stages.values(), key=lambda r_: r_["avg_ms"])
     out = {"value": Bsz / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,

@@ -869,7 +869,9 @@ __global__ void m1_update_kernel(const float* __restrict__ x, long ldx,
 //   h = exp(dt A) h + dt x B, y = (C . h + D x) silu(z), with B = dbl[R, R + N) and
 //   C = dbl[R + N, R + 2N) read from LDS.
 // Workgroups of the padding rows (b in [B, M16)) write zeros to their rows of y's fragment
-// order (the out_proj reads whole 16-row tiles) and do nothing else.
+// order (the out_proj reads whole 16-row tiles) and do nothing else. Workgroups go to the 8
+// XCDs round-robin by id; the ids are mapped so that the D / CPW workgroups of a sequence share
+// one XCD, whose L2 then serves its x_proj partials to all of them after the first read.
 struct M1StepArgs {
     const float* x; long ldx;
     const float* xpart; int RN, NP, M16;
@@ -888,8 +890,10 @@ __global__ __launch_bounds__(384) void m1_step_update_kernel(M1StepArgs a) {
     __shared__ __attribute__((aligned(16))) float dbl[ssm::kXpartMaxRN];
     const int CPW = blockDim.x;
     const int tid = threadIdx.x;
-    const int b = blockIdx.y;
-    const int d = blockIdx.x * CPW + tid;
+    const int nq = a.D / CPW;
+    const int id = blockIdx.x, k = id >> 3;
+    const int b = (id & 7) + 8 * (k / nq);
+    const int d = (k % nq) * CPW + tid;
     const int kb = a.D >> 4;
     if (b >= a.B) {
         a.yf[ssm::frag_off(b, d, kb)] = 0.f;
@@ -1183,7 +1187,7 @@ ssm_status launch_m1_step_update(const float* x, long ldx, const float* xpart, i
     a.x = x; a.ldx = ldx; a.xpart = xpart; a.RN = RN; a.NP = D / 16; a.M16 = M16;
     a.Wdt = Wdt; a.R = R; a.dt_bias = dt_bias; a.A = A; a.Dsk = Dsk; a.z = z; a.ldz = ldz;
     a.yf = yf; a.h = h; a.B = B; a.D = D;
-    const dim3 grid((unsigned)(D / cpw), (unsigned)M16);
+    const unsigned grid = (unsigned)(D / cpw) * (unsigned)M16;   // M16 % 8 == 0
     switch (N) {
         case 4: m1_step_update_kernel<4><<<grid, cpw, 0, st>>>(a); break;
         case 8: m1_step_update_kernel<8><<<grid, cpw, 0, st>>>(a); break;
