@@ -76,6 +76,10 @@ TRAFFIC = {
 # The commit of the build each TRAFFIC entry was measured on (profiles/hbm_traffic.md); an
 # entry goes stale when its kernel changes after that commit.
 TRAFFIC_MEASURED_AT = {k: "1b2f2f1" for k in TRAFFIC}
+# rocprofv3's MfmaUtil (matrix-core busy cycles over the dispatch's active cycles) of the SSD
+# launches, averaged over a `--steps 3 --warmup 1` run (profiles/ssd_mfma_util.md)
+MFMA_BUSY = {("cfg3", "f32"): 0.728, ("cfg3", "bf16"): 0.174}
+MFMA_BUSY_MEASURED_AT = "748ef90"
 
 
 def parse():
@@ -388,19 +392,24 @@ def ssd_alg(B, L, H, P, N, esz, Q=256):
     return flops, nbytes
 
 
-def ssd_f32_issued_flops(B, L, H, G, N, P=64):
+def ssd_f32_issued_flops(B, L, H, G, N, P=64, h0=False):
     """The MFMA work ssd_f32_kernel issues per launch (16x16x4 fp32 MFMAs, 2048 FLOPs each).
     Chunks of 32 steps; a workgroup owns HPW heads of one group (2 when the heads per group
     are even) and forms the group's three causal 16x16 C B^T tiles once for them (N / 4
     MFMAs each). Each head's four waves (16 rows of the head dim each) then issue, per chunk:
     state-to-output 2 x (N / 4), diagonal part 3 x 4 (the causal 16-step blocks), state
-    update (N / 16) x 2 x 4."""
+    update (N / 16) x 2 x 4; without an initial state the first chunk of each sequence skips
+    the state-to-output part. At cfg3 this is 81.336 GFLOP, the figure of
+    SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 (profiles/ssd_mfma_util.md)."""
     qf = 32
     hpw = 2 if (H // G) % 2 == 0 else 1
     cbt = 3 * (N // 4)                                   # per workgroup and chunk
     per_wave = 2 * (N // 4) + 3 * 4 + (N // 16) * 2 * 4
     per_chunk_head = cbt / hpw + (P // 16) * per_wave
-    return per_chunk_head * 2048.0 * (B * L / qf) * H
+    total = per_chunk_head * (B * L / qf) * H
+    if not h0:
+        total -= B * H * (P // 16) * 2 * (N // 4)
+    return total * 2048.0
 
 
 def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, with_cpu=True):
@@ -442,6 +451,10 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, wit
         rl["issued_mfma_flops"] = ssd_f32_issued_flops(B, L, H, 1, N)
         rl["issued_mfma_frac"] = round(rl["issued_mfma_flops"] / (ms * 1e-3) / 1e12
                                        / PEAK_TFLOPS[prec], 4)
+    # the matrix cores' busy fraction as the counters read it (rocprofv3 MfmaUtil of this
+    # launch; profiles/ssd_mfma_util.md, with the build it was measured on)
+    rl["mfma_busy_counter"] = MFMA_BUSY.get(key)
+    rl["mfma_busy_measured_at"] = MFMA_BUSY_MEASURED_AT if key in MFMA_BUSY else None
     if with_cpu and not args.no_cpu_baseline:
         from oracle import oracle as O
         # the whole workload (every sequence and head, the same inputs as fp32), repeated
