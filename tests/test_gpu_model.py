@@ -176,6 +176,37 @@ def test_greedy_exact_ties_pick_lowest_index(device, B):
     m.destroy()
 
 
+@pytest.mark.parametrize("V,B", [(1000, 20), (300, 64)])
+def test_decode_logits_ragged_vocab(device, V, B):
+    """One-token steps through the own LM head with a vocabulary that is not a whole number of
+    16-column tiles or 128-column workgroup blocks, and row counts that leave padding rows in
+    the last 16-row tile: logits and greedy picks against the oracle."""
+    case(f"decode logits V={V} B={B}")
+    from ssmjs_amd import backend, checkpoint
+    cfg = {"vocabSize": V, "dModel": 128, "numLayers": 2, "dState": 64, "dConv": 4,
+           "expand": 2, "nHeads": 4, "nGroups": 1,
+           "layers": [{"type": "mamba2"}, {"type": "mamba1"}]}
+    m = backend.Model(device, cfg, seed=13)
+    dims, T = checkpoint.unpack(m.export_weights())
+    T["embedding"] = T["embedding"] * 40.0
+    blob = checkpoint.pack(dims, T)
+    m.load_weights(blob)
+    om = O.Model(blob)
+    ids = np.random.default_rng(9).integers(0, V, (B, 5)).astype(np.uint32)
+    st, ost = m.new_state(B), om.new_state(B)
+    st.prefill(ids[:, :3])
+    ost.prefill(ids[:, :3])
+    for t in range(3, 5):
+        lg, am = st.decode(ids[:, t])
+        ref = ost.decode(ids[:, t])
+        close(lg, ref, "logits")
+        top2 = np.sort(ref, axis=1)[:, -2:]
+        ok = (top2[:, 1] - top2[:, 0]) > 1e-4 * np.abs(ref).max()
+        np.testing.assert_array_equal(am[ok], np.argmax(ref, axis=1)[ok])
+    st.destroy()
+    m.destroy()
+
+
 def test_decode_graph_replay_matches_eager(device, monkeypatch):
     """Repeated one-token steps replay a captured HIP graph (from the second step with the same
     buffers on). Every replayed step must give the same bits as eager launches from the same
