@@ -28,6 +28,16 @@
 // tiles are numbered in groups of 8 row tiles (a group walks its columns), so the tiles in
 // flight on an XCD share X rows and W rows through that XCD's L2.
 //
+// Split K. When the tiles alone leave CUs idle (fewer than 256: prompts of a few hundred
+// tokens), K may be cut into S slices of a multiple of 16 (at least 128 each) and every
+// (tile, slice) pair is a workgroup of its own (slice z of row tile tm is row tile tm + z mt
+// of an S times taller grid, so the ordering above is unchanged); each writes its raw
+// partial tile to a workspace (S, M, N), and a second kernel adds the S partials in slice
+// order (deterministic) and applies the epilogue (row scale, bias, beta, gate) in the same
+// order as the unsplit kernel. S is chosen by a cost model measured on MI355X: a CU running
+// one of these workgroups does 0.44 TFLOP/s, two or more 0.50 (of 0.61 peak), the partials
+// cost their bytes written and read at 5 TB/s, and the finishing launch about 4 us.
+//
 // Measured (MI355X, fp32 TFLOP/s, this kernel / hipBLASLt): M 32768 N 2048 K 4096 150 / 151,
 // M 32768 N 8448 K 2016 148 / 149, M 8192 N 3072 K 768 119 / 118. At a clock of 2.4 GHz the
 // fp32 MFMA peak is 157 TFLOP/s; with the operand loads running the clock drops to about
@@ -60,6 +70,9 @@ struct GemmArgs {
     // sum_j ssq[m nssq + j] + eps) -- an RMSNorm of X's rows applied after the product
     const float* ssq; int nssq; float inv_div, eps;
     int gate_c0;   // columns >= gate_c0 (a multiple of 16) are stored as silu(value)
+    // split K: ks slices of kslice (the last may be shorter); part (ks, M, N) row-major
+    int ks, kslice;
+    float* part;
 };
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
@@ -82,24 +95,31 @@ __device__ __forceinline__ void end_step() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NJ, bool BETA, bool RS>
+template <int NJ, bool BETA, bool RS, bool SPLIT = false>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
     constexpr int BN = 32 * NJ;
+    static_assert(!SPLIT || (!BETA && !RS), "the split kernel stores raw partials");
     __shared__ float rs[RS ? BM : 1];
     __shared__ __attribute__((aligned(16))) float s0[kStage];
     __shared__ __attribute__((aligned(16))) float s1[kStage];
     __shared__ __attribute__((aligned(16))) float s2[kStage];
     __shared__ __attribute__((aligned(16))) float s3[kStage];
 
-    // ---- tile of this workgroup: consecutive ids per XCD, groups of GM row tiles
-    const int T = a.mt * a.nt;
+    // ---- tile of this workgroup: consecutive ids per XCD, groups of GM row tiles (with
+    // split K, over the S times taller grid of (slice, row tile) pairs)
+    const int mtv = SPLIT ? a.mt * a.ks : a.mt;
+    const int T = mtv * a.nt;
     const int b = blockIdx.x;
     const int xcd = b & 7, per = T >> 3, rem = T & 7;
     const int id = xcd * per + min(xcd, rem) + (b >> 3);
     const int gsz = GM * a.nt;
     const int grp = id / gsz, gr = id - grp * gsz;
-    const int gm = min(GM, a.mt - grp * GM);
-    const int tm = grp * GM + gr % gm, tn = gr / gm;
+    const int gm = min(GM, mtv - grp * GM);
+    const int tmv = grp * GM + gr % gm, tn = gr / gm;
+    const int kz = SPLIT ? tmv / a.mt : 0, tm = SPLIT ? tmv - kz * a.mt : tmv;
+    // this workgroup's k range [kbeg, kbeg + K)
+    const int kbeg = SPLIT ? kz * a.kslice : 0;
+    const int K = SPLIT ? min(a.kslice, a.K - kbeg) : a.K;
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -108,8 +128,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
 
     const int m0 = tm * BM, n0 = tn * BN;
     const int rows = min(BM, a.M - m0), cols = min(BN, a.N - n0);
-    const auto rx = ssm::rsrc(a.X + (long)m0 * a.ldx, (unsigned)(((long)(rows - 1) * a.ldx + a.K) * 4));
-    const auto rw = ssm::rsrc(a.W + (long)n0 * a.ldw, (unsigned)(((long)(cols - 1) * a.ldw + a.K) * 4));
+    const auto rx = ssm::rsrc(a.X + (long)m0 * a.ldx + kbeg,
+                              (unsigned)(((long)(rows - 1) * a.ldx + K) * 4));
+    const auto rw = ssm::rsrc(a.W + (long)n0 * a.ldw + kbeg,
+                              (unsigned)(((long)(cols - 1) * a.ldw + K) * 4));
 
     // Loads of wave w in a step: X row blocks 2w, 2w + 1 and W row blocks 2w, 2w + 1 (W row
     // blocks past the tile's BN rows read nothing); lane (q, i16) reads row 16 rb + i16,
@@ -134,8 +156,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
         }
     };
     auto load_tail = [&](float* s, int k0) {
-        const unsigned kk = (unsigned)min(k0, a.K) * 4u;
-        const unsigned oor = k0 + 4 * q < a.K ? 0u : 0x80000000u;
+        const unsigned kk = (unsigned)min(k0, K) * 4u;
+        const unsigned oor = k0 + 4 * q < K ? 0u : 0x80000000u;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             to_lds(rx, s + (2 * w + u) * kFrag, ox[u] | oor, kk);
@@ -169,8 +191,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
     // Steps in blocks of four (one per stage): the main loop while every load of a block is
     // a whole step inside K, then the tail blocks with range-checked loads (a block that
     // runs past K computes on zeros).
-    const int nk = (a.K + BK - 1) / BK;
-    const int nfull = a.K / BK;   // steps that lie wholly inside K
+    const int nk = (K + BK - 1) / BK;
+    const int nfull = K / BK;   // steps that lie wholly inside K
     auto block = [&](int s, auto ld) {
         ld(s3, (s + 3) * BK);
         compute(s0);
@@ -215,6 +237,23 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
     }
 
     // ---- epilogue: acc[i][j][r] is Y[m0 + 16 (4 wm + i) + 4 q + r][n0 + 16 (NJ wn + j) + i16]
+    if constexpr (SPLIT) {   // the raw partial tile of slice kz
+        const auto rp = ssm::rsrc(a.part + ((long)kz * a.M + m0) * a.N + n0,
+                                  (unsigned)(((long)(rows - 1) * a.N + cols) * 4));
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int c = 16 * (NJ * wn + j) + i16;
+            const unsigned oor = c < cols ? 0u : 0x80000000u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * (4 * wm + i) + 4 * q + r;
+                    ssm::bstore4(acc[i][j][r], rp, ((unsigned)(row * a.N + c) * 4u) | oor);
+                }
+        }
+        return;
+    }
     const auto ry = ssm::rsrc(a.Y + (long)m0 * a.ldy + n0,
                               (unsigned)(((long)(rows - 1) * a.ldy + cols) * 4));
 #pragma unroll
@@ -240,6 +279,41 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs a) {
     }
 }
 
+// Split-K finish: Y = epilogue(sum over slices z = 0 .. ks-1 of part[z]), added in slice
+// order; the epilogue in the unsplit kernel's order (row scale, bias, beta, gate). Thread
+// (row m = blockIdx.y, columns 4 c4 .. 4 c4 + 3); N % 4 == 0.
+__global__ __launch_bounds__(256) void gemm_finish_kernel(GemmArgs a) {
+    const int m = blockIdx.y;
+    const int c4 = blockIdx.x * 256 + threadIdx.x;
+    if (4 * c4 >= a.N) return;
+    const long MN = (long)a.M * a.N;
+    const float4* p = reinterpret_cast<const float4*>(a.part + (long)m * a.N) + c4;
+    float4 v = p[0];
+    for (int z = 1; z < a.ks; ++z) {
+        const float4 u = p[z * (MN / 4)];
+        v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+    }
+    float s = 1.f;
+    if (a.ssq) {   // same order as the unsplit kernel's row scales
+        const float* q = a.ssq + (long)m * a.nssq;
+        float sum = 0.f;
+        for (int j = 0; j < a.nssq; ++j) sum += q[j];
+        s = rsqrtf(sum * a.inv_div + a.eps);
+    }
+    float* y = a.Y + (long)m * a.ldy + 4 * c4;
+    float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int n = 4 * c4 + e;
+        float t = o[e];
+        if (a.ssq) t *= s;
+        if (a.bias) t += a.bias[n];
+        if (a.beta != 0.f) t += a.beta * y[e];
+        if (n >= a.gate_c0) t = ssm::silu_fast(t);
+        y[e] = t;
+    }
+}
+
 // Column tile width: the one with the fewest rounds of 512 resident workgroups (two per
 // CU), weighting a tile's cost by its width plus one (the X slice every tile loads).
 int pick_nj(int M, int N) {
@@ -256,7 +330,15 @@ int pick_nj(int M, int N) {
 
 template <int NJ>
 void launch_nj(const GemmArgs& a, bool beta, hipStream_t st) {
-    const dim3 grid((unsigned)(a.mt * a.nt)), block(256);
+    const dim3 block(256);
+    if (a.ks > 1) {
+        gemm_f32_kernel<NJ, false, false, true><<<dim3((unsigned)(a.mt * a.ks * a.nt)), block,
+                                                  0, st>>>(a);
+        gemm_finish_kernel<<<dim3((unsigned)((a.N / 4 + 255) / 256), (unsigned)a.M), block, 0,
+                             st>>>(a);
+        return;
+    }
+    const dim3 grid((unsigned)(a.mt * a.nt));
     if (a.ssq) {
         if (beta) gemm_f32_kernel<NJ, true, true><<<grid, block, 0, st>>>(a);
         else gemm_f32_kernel<NJ, false, true><<<grid, block, 0, st>>>(a);
@@ -499,9 +581,42 @@ bool gemm_ok(int M, int N, int K, long ldx, long ldw, long ldy) {
            (long)BM * ldy * 4 < lim;
 }
 
+// Split of K for a grid of `tiles` tiles of BN columns: the slice count (1: none) with the
+// least modelled time (above), slices at least 128 deep and a multiple of 16, within the
+// workspace (part_floats). No split once the tiles cover every CU.
+int pick_split(int M, int N, int K, int bn, long tiles, size_t part_floats, int* kslice) {
+    *kslice = K;
+    if (tiles >= 256 || N % 4 || K < 256) return 1;
+    const double fl = 2.0 * BM * bn;   // flops of a tile per unit of k
+    auto busy = [&](long wgs, int depth) {   // the most loaded CU's time (s)
+        const long n = (wgs + 255) / 256;
+        return (double)n * fl * depth / (n == 1 ? 0.44e12 : 0.50e12);
+    };
+    double best = busy(tiles, K);
+    int bks = 1, bsl = K;
+    for (int ks = 2; ks <= K / 128; ++ks) {
+        if ((size_t)ks * M * N > part_floats) break;
+        const int sl = ((K + ks - 1) / ks + 15) / 16 * 16;
+        if ((K + sl - 1) / sl != ks) continue;
+        const double t = busy(tiles * ks, sl) + 8.0 * ks * M * N / 5e12 + 4e-6;
+        if (t < best) best = t, bks = ks, bsl = sl;
+    }
+    *kslice = bsl;
+    return bks;
+}
+
+size_t gemm_split_floats(int M, int N, int K) {
+    const int nj = pick_nj(M, N);
+    const long tiles = (long)((M + BM - 1) / BM) * ((N + 32 * nj - 1) / (32 * nj));
+    int sl;
+    const int ks = pick_split(M, N, K, 32 * nj, tiles, (size_t)-1, &sl);
+    return ks > 1 ? (size_t)ks * M * N : 0;
+}
+
 ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const float* bias,
                        float* Y, long ldy, int M, int N, int K, float beta, hipStream_t st,
-                       const float* ssq, int nssq, float inv_div, float eps, int gate_c0) {
+                       const float* ssq, int nssq, float inv_div, float eps, int gate_c0,
+                       float* part, size_t part_floats) {
     if (!gemm_ok(M, N, K, ldx, ldw, ldy))
         return fail(SSM_ERR_INVALID_ARG, "gemm: unsupported shape M %d N %d K %d ld %ld/%ld/%ld",
                     M, N, K, ldx, ldw, ldy);
@@ -509,7 +624,11 @@ ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const
         return fail(SSM_ERR_INVALID_ARG, "gemm: X and W must be 16-byte aligned");
     const int nj = pick_nj(M, N);
     GemmArgs a{X, ldx, W, ldw, Y, ldy, bias, M, N, K, beta, (M + BM - 1) / BM,
-               (N + 32 * nj - 1) / (32 * nj), ssq, nssq, inv_div, eps, gate_c0};
+               (N + 32 * nj - 1) / (32 * nj), ssq, nssq, inv_div, eps, gate_c0, 1, K, nullptr};
+    if (part && ((uintptr_t)part & 15) == 0) {
+        a.ks = pick_split(M, N, K, 32 * nj, (long)a.mt * a.nt, part_floats, &a.kslice);
+        if (a.ks > 1) a.part = part;
+    }
     if (gate_c0 < N && gate_c0 % 16)
         return fail(SSM_ERR_INVALID_ARG, "gemm: gate column %d not a multiple of 16", gate_c0);
     if (ssq && nssq <= 0) return fail(SSM_ERR_INVALID_ARG, "gemm: row scale needs nssq > 0");

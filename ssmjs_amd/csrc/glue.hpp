@@ -134,10 +134,15 @@ ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, fl
 bool gemm_ok(int M, int N, int K, long ldx, long ldw, long ldy);
 // gate_c0 (a multiple of 16): columns n >= gate_c0 are stored as silu(value) (the Mamba-1
 // block's z half of in_proj, the scan's gate).
+// part (part_floats floats, 16-byte aligned): workspace of the split-K mode, used when the
+// tiles alone leave most CUs idle and part holds gemm_split_floats(M, N, K) floats; null
+// runs unsplit.
 ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const float* bias,
                        float* Y, long ldy, int M, int N, int K, float beta, hipStream_t st,
                        const float* ssq = nullptr, int nssq = 0, float inv_div = 0.f,
-                       float eps = 0.f, int gate_c0 = 0x7fffffff);
+                       float eps = 0.f, int gate_c0 = 0x7fffffff, float* part = nullptr,
+                       size_t part_floats = 0);
+size_t gemm_split_floats(int M, int N, int K);
 // The Mamba-1 block's x_proj and dt_proj in one pass (gemm.hip): dbl = x Wx^T (T, R + 2N),
 // dt = dbl[:, :R] Wdt^T (T, D); given dt_bias, dt = softplus(dbl[:, :R] Wdt^T + dt_bias) (the
 // scan's dt').

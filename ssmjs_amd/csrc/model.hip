@@ -253,20 +253,26 @@ ssm_ctx::LtPlan& lt_plan(ssm_ctx* c, int M, int Nout, int K, long ldx, long ldy,
 }
 
 // Y (M, Nout) [ld ldy] = X (M, K) [ld ldx] * W^T, W (Nout, K) row-major; Y = beta*Y + ...
-// Prefill-sized products (M >= kOwnGemmRows) run the fp32 matrix-core kernel of gemm.hip;
-// the few-row products of decode go to hipBLASLt for K >= 128 (below that rocBLAS measured
-// faster) and rocBLAS for the rest and any shape hipBLASLt has no algorithm for.
+// Products of M >= kOwnGemmRows rows run the fp32 matrix-core kernel of gemm.hip (split over
+// K when its tiles leave CUs idle and a workspace is given); the prefill of up to
+// kFewRows tokens runs the row kernel of rowgemm.hip (proj_rows); the rest (prompts of 65 to
+// 255 tokens, the one-token fallbacks) go to hipBLASLt for K >= 128 (below that rocBLAS
+// measured faster) and rocBLAS for the rest and any shape hipBLASLt has no algorithm for.
 // SSM_GEMM=lib sends every product to the libraries, SSM_GEMM=rocblas everything to rocBLAS.
 constexpr int kOwnGemmRows = 256;
-bool own_kernels(int M) {
-    static const bool lib_only = [] {
+constexpr int kFewRows = 64;
+bool lib_only() {
+    static const bool v = [] {
         const char* e = std::getenv("SSM_GEMM");
         return e && (std::strcmp(e, "lib") == 0 || std::strcmp(e, "rocblas") == 0);
     }();
-    return !lib_only && M >= kOwnGemmRows;
+    return v;
 }
+bool own_kernels(int M) { return !lib_only() && M >= kOwnGemmRows; }
+bool few_rows(int M) { return !lib_only() && M >= 1 && M <= kFewRows; }
+// part / part_n: the own kernel's split-K workspace (gemm.hip; null runs unsplit).
 ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, const float* W,
-                float* Y, long ldy, float beta) {
+                float* Y, long ldy, float beta, float* part = nullptr, size_t part_n = 0) {
     if (M == 0 || Nout == 0) return SSM_OK;
     const float one = 1.f;
     static const bool rb_only = [] {
@@ -275,7 +281,8 @@ ssm_status gemm(ssm_ctx* c, int M, int Nout, int K, const float* X, long ldx, co
     }();
     if (own_kernels(M) && ssm::gemm_ok(M, Nout, K, ldx, K, ldy) &&
         (((uintptr_t)X | (uintptr_t)W) & 15) == 0)
-        return ssm::launch_gemm(X, ldx, W, K, nullptr, Y, ldy, M, Nout, K, beta, c->stream);
+        return ssm::launch_gemm(X, ldx, W, K, nullptr, Y, ldy, M, Nout, K, beta, c->stream,
+                                nullptr, 0, 0.f, 0.f, 0x7fffffff, part, part_n);
     if (c->lt && K >= 128 && !rb_only) {
         auto& p = lt_plan(c, M, Nout, K, ldx, ldy);
         if (p.ok) {
@@ -704,13 +711,19 @@ struct Ws {
     float *hid, *nrm, *a, *b, *c, *d, *e, *last, *logits;
     // one-token steps (stepproj.hip): x * g of the next RMSNorm and the gated norm's output,
     // both in fragment order, and the two norms' partial sums of squares; null for longer
-    // sequences
+    // sequences (xg and ssq_in also hold the own LM head's operand, below)
     float *xg, *yf, *ssq_in, *ssq_y;
     // the Mamba-1 step's x_proj partials (stepproj.hip, xpart); null for longer sequences or
     // without Mamba-1 layers
     float* xpart;
-    // the one-token LM head's argmax partials (head.hip); null for longer sequences
+    // the own LM head's argmax partials (head.hip), for its rows: all T positions when
+    // T <= kStepProjMaxRows (one-token steps, short forwards), else a prefill's B last
+    // positions when B <= kStepProjMaxRows; null otherwise
     float* hpart;
+    // split-K partials of the own prefill GEMM (gemm.hip) for the largest split product of
+    // the mixers at T tokens (gpart_n floats); null when none splits
+    float* gpart;
+    size_t gpart_n;
     void* scan;
     size_t scan_bytes;
 };
@@ -752,14 +765,29 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
     size_t o_scan = off; off += al(scan);
     const size_t nstep = L == 1 ? (size_t)B : 0;
     const size_t nstep16 = (nstep + 15) / 16 * 16;   // fragment order pads to 16-row tiles
-    size_t o_xg = off; off += al(4 * nstep16 * d.d);
+    const size_t MR = ssm::kStepProjMaxRows;
+    const size_t nhead = T <= MR ? T : (size_t)B <= MR ? (size_t)B : 0;
+    const size_t nx = std::max(nstep, nhead), nx16 = (nx + 15) / 16 * 16;
+    size_t o_xg = off; off += al(4 * nx16 * d.d);
     size_t o_yf = off; off += al(4 * nstep16 * d.D);
-    size_t o_sqi = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
+    size_t o_sqi = off; off += al(4 * nx * ssm::kStepProjMaxSsq);
     size_t o_sqy = off; off += al(4 * nstep * ssm::kStepProjMaxSsq);
     const size_t nxp = has1 ? (size_t)(d.D / 16) * nstep16 * (d.R + 2 * d.N) : 0;
     size_t o_xp = off; off += al(4 * nxp);
-    const size_t nhp = nstep ? nstep * (size_t)ssm::head_parts(d.V) * 2 : 0;
+    const size_t nhp = nhead * (size_t)ssm::head_parts(d.V) * 2;
     size_t o_hp = off; off += al(4 * nhp);
+    size_t ngp = 0;
+    if (T >= (size_t)kOwnGemmRows && T <= (size_t)INT32_MAX) {
+        const int t = (int)T;
+        if (has1)
+            for (auto nk : {std::pair<int, int>{2 * d.D, d.d}, {d.d, d.D}, {d.R + 2 * d.N, d.D},
+                            {d.D, d.R}})
+                ngp = std::max(ngp, ssm::gemm_split_floats(t, nk.first, nk.second));
+        if (has2)
+            for (auto nk : {std::pair<int, int>{d.nin, d.d}, {d.d, d.D}})
+                ngp = std::max(ngp, ssm::gemm_split_floats(t, nk.first, nk.second));
+    }
+    size_t o_gp = off; off += al(4 * ngp);
     if (out) {
         char* base = m->ws;
         out->hid = (float*)(base + o_hid); out->nrm = (float*)(base + o_nrm);
@@ -768,12 +796,14 @@ size_t plan_ws(ssm_model* m, int B, int L, bool full_logits, Ws* out) {
         out->e = (float*)(base + o_e); out->last = (float*)(base + o_last);
         out->logits = (float*)(base + o_log);
         out->scan = base + o_scan; out->scan_bytes = scan;
-        out->xg = nstep ? (float*)(base + o_xg) : nullptr;
+        out->xg = nx ? (float*)(base + o_xg) : nullptr;
         out->yf = nstep ? (float*)(base + o_yf) : nullptr;
-        out->ssq_in = nstep ? (float*)(base + o_sqi) : nullptr;
+        out->ssq_in = nx ? (float*)(base + o_sqi) : nullptr;
         out->ssq_y = nstep ? (float*)(base + o_sqy) : nullptr;
         out->xpart = nxp ? (float*)(base + o_xp) : nullptr;
         out->hpart = nhp ? (float*)(base + o_hp) : nullptr;
+        out->gpart = ngp ? (float*)(base + o_gp) : nullptr;
+        out->gpart_n = ngp;
     }
     return off;
 }
@@ -805,8 +835,15 @@ ssm_status ensure_ids(ssm_model* m, size_t n) {
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const float* z, long ldz,
+                     const float* g, const float* W, float* y, long ldy, int M, int N, int K,
+                     float beta, float* tmp, const float* g2 = nullptr, float* nout = nullptr,
+                     bool* normed = nullptr, bool rows = false);
+
 // One mixer over (B, L) tokens: reads x (T, d) [normalised], adds its output into out (T, d)
 // with beta (0: overwrite, 1: residual add). ssm/conv state may be null (zero initial state).
+// Its products: up to kFewRows tokens on the row kernel (proj_rows), else gemm() (the own
+// kernel from kOwnGemmRows rows, with the split-K workspace).
 ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, float beta, int B,
                  int L, float* ssm_st, float* conv_st, const Ws& w) {
     const Dims& d = m->dm;
@@ -815,20 +852,32 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
     const int T = B * L;
     const float* W = m->w;
     const float* A = m->Ab + Ly.A;
+    const bool few = few_rows(T);
+    auto proj = [&](int N, int K, const float* X, long ldx, const float* Wt, float* Y, long ldy,
+                    float b) -> ssm_status {
+        if (few)
+            return proj_rows(m, 0, X, ldx, nullptr, 0, nullptr, Wt, Y, ldy, T, N, K, b, nullptr,
+                             nullptr, nullptr, nullptr, true);
+        return gemm(c, T, N, K, X, ldx, Wt, Y, ldy, b, w.gpart, w.gpart_n);
+    };
     if (Ly.type == SSM_LAYER_MAMBA1) {
         float *xz = w.a, *xc = w.b, *dbl = w.c, *dtv = w.d, *y = w.e;
         const int RN = d.R + 2 * d.N;
-        // With the own kernels on both sides, the scan's element-wise input work moves into
-        // its producers: in_proj stores silu(z) for the z half and x_proj/dt_proj stores
-        // dt' = softplus(dt + bias) (the same functions, so the same values).
-        const bool fused_xd = own_kernels(T) && ssm::xproj_dt_ok(T, d.D, d.R, d.N, d.D, RN, d.D) &&
+        // x_proj and dt_proj in one kernel when its workgroups (32 tokens each) cover the CUs;
+        // with fewer tokens, two products (split over K by gemm()). With the fused kernel, the
+        // scan's element-wise input work moves into its producers: in_proj stores silu(z) for
+        // the z half and x_proj/dt_proj stores dt' = softplus(dt + bias) (the same functions,
+        // so the same values).
+        const bool fused_xd = own_kernels(T) && (T + 31) / 32 >= 256 &&
+                              ssm::xproj_dt_ok(T, d.D, d.R, d.N, d.D, RN, d.D) &&
                               al16(W + Ly.x_proj) && al16(W + Ly.dt_w);
         const bool pre = fused_xd && ssm::gemm_ok(T, 2 * d.D, d.d, d.d, d.d, 2 * d.D) &&
                          al16(x) && al16(W + Ly.in_proj) && d.D % 16 == 0;
         { Stage g(c, "m1.in_proj");
           if (pre) SSM_TRY(ssm::launch_gemm(x, d.d, W + Ly.in_proj, d.d, nullptr, xz, 2 * d.D, T,
-                                            2 * d.D, d.d, 0.f, st, nullptr, 0, 0.f, 0.f, d.D));
-          else SSM_TRY(gemm(c, T, 2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
+                                            2 * d.D, d.d, 0.f, st, nullptr, 0, 0.f, 0.f, d.D,
+                                            w.gpart, w.gpart_n));
+          else SSM_TRY(proj(2 * d.D, d.d, x, d.d, W + Ly.in_proj, xz, 2 * d.D, 0.f)); }
         { Stage g(c, "m1.conv");
           SSM_TRY(ssm_causal_conv1d(xz, 2 * d.D, W + Ly.conv_w, W + Ly.conv_b, xc, d.D, B, L, d.D,
                                     d.K, 1, conv_st, conv_st, st)); }
@@ -838,19 +887,19 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
             SSM_TRY(ssm::launch_xproj_dt(xc, d.D, W + Ly.x_proj, W + Ly.dt_w, dbl, RN, dtv, d.D,
                                          T, d.D, d.R, d.N, st, pre ? W + Ly.dt_b : nullptr));
         } else {
-            { Stage g(c, "m1.x_proj"); SSM_TRY(gemm(c, T, RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
-            { Stage g(c, "m1.dt_proj"); SSM_TRY(gemm(c, T, d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
+            { Stage g(c, "m1.x_proj"); SSM_TRY(proj(RN, d.D, xc, d.D, W + Ly.x_proj, dbl, RN, 0.f)); }
+            { Stage g(c, "m1.dt_proj"); SSM_TRY(proj(d.D, d.R, dbl, RN, W + Ly.dt_w, dtv, d.D, 0.f)); }
         }
         { Stage g(c, "m1.scan");
           SSM_TRY(ssm::selective_scan(xc, d.D, dtv, d.D, pre ? nullptr : W + Ly.dt_b, pre ? 0 : 1,
                                       A, dbl + d.R, RN, dbl + d.R + d.N, RN, W + Ly.Dsk, xz + d.D,
                                       2 * d.D, pre ? 1 : 0, y, d.D, B, L, d.D, d.N, ssm_st, ssm_st,
                                       w.scan, w.scan_bytes, st)); }
-        { Stage g(c, "m1.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, y, d.D, W + Ly.out_proj, out, d.d, beta)); }
+        { Stage g(c, "m1.out_proj"); SSM_TRY(proj(d.d, d.D, y, d.D, W + Ly.out_proj, out, d.d, beta)); }
     } else {
         float *zx = w.a, *xbc = w.b, *y = w.c, *yn = w.d;
         const int GN = d.G * d.N;
-        { Stage g(c, "m2.in_proj"); SSM_TRY(gemm(c, T, d.nin, d.d, x, d.d, W + Ly.in_proj, zx, d.nin, 0.f)); }
+        { Stage g(c, "m2.in_proj"); SSM_TRY(proj(d.nin, d.d, x, d.d, W + Ly.in_proj, zx, d.nin, 0.f)); }
         { Stage g(c, "m2.conv");
           SSM_TRY(ssm_causal_conv1d(zx + d.D, d.nin, W + Ly.conv_w, W + Ly.conv_b, xbc, d.cd, B, L,
                                     d.cd, d.K, 1, conv_st, conv_st, st)); }
@@ -871,17 +920,26 @@ ssm_status mixer(ssm_model* m, const LayerW& Ly, const float* x, float* out, flo
                                    d.nin, W + Ly.gnorm, yn)); }
             { Stage g(c, "m2.out_proj");
               SSM_TRY(ssm::launch_gemm(y, d.D, W + Ly.out_proj, d.D, nullptr, out, d.d, T, d.d,
-                                       d.D, beta, st, yn, d.H, 1.f / (float)d.D, d.eps)); }
+                                       d.D, beta, st, yn, d.H, 1.f / (float)d.D, d.eps,
+                                       0x7fffffff, w.gpart, w.gpart_n)); }
         } else {
             { Stage g(c, "m2.ssd");
               SSM_TRY(ssm_ssd_chunk_scan(SSM_F32, xbc, d.cd, dtp, d.nin, W + Ly.dt_b, 1,
                                          0.f, INFINITY, A, xbc + d.D, d.cd, xbc + d.D + GN, d.cd,
                                          W + Ly.Dsk, y, d.D, B, L, d.H, d.P, d.G, d.N, ssm_st,
                                          ssm_st, w.scan, w.scan_bytes, st)); }
-            { Stage g(c, "m2.gated_norm");
-              SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, T, d.D, d.G,
-                                        d.eps, st)); }
-            { Stage g(c, "m2.out_proj"); SSM_TRY(gemm(c, T, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, beta)); }
+            if (few) {   // the gated norm in the row kernel's prologue
+                Stage g(c, "m2.out_proj");
+                SSM_TRY(proj_rows(m, 2, y, d.D, zx, d.nin, W + Ly.gnorm, W + Ly.out_proj, out,
+                                  d.d, T, d.d, d.D, beta, yn, nullptr, nullptr, nullptr, true));
+            } else {
+                { Stage g(c, "m2.gated_norm");
+                  SSM_TRY(ssm_gated_rmsnorm(y, d.D, zx, d.nin, W + Ly.gnorm, yn, d.D, T, d.D, d.G,
+                                            d.eps, st)); }
+                { Stage g(c, "m2.out_proj");
+                  SSM_TRY(gemm(c, T, d.d, d.D, yn, d.D, W + Ly.out_proj, out, d.d, beta, w.gpart,
+                               w.gpart_n)); }
+            }
         }
     }
     return SSM_OK;
@@ -942,14 +1000,15 @@ ssm_status mixer_bf16(ssm_model* m, int l, const float* x, float* out, int B, in
 // (the next layer's normalised input) and sets *normed.
 ssm_status proj_rows(ssm_model* m, int mode, const float* x, long ldx, const float* z, long ldz,
                      const float* g, const float* W, float* y, long ldy, int M, int N, int K,
-                     float beta, float* tmp, const float* g2 = nullptr, float* nout = nullptr,
-                     bool* normed = nullptr) {
+                     float beta, float* tmp, const float* g2, float* nout, bool* normed,
+                     bool rows) {
     if (normed) *normed = false;
     ssm_ctx* c = m->ctx;
     const Dims& d = m->dm;
     // the LM head (RMS mode, wide N) takes RMSNorm + hipBLASLt when there is one (about 42
-    // against 49 us at 64 x 32000 x 1024); the gated out_proj always takes the row kernel
-    const bool wanted = mode == 2 || (mode == 1 && N >= 16384 && !c->lt);
+    // against 49 us at 64 x 32000 x 1024); the gated out_proj always takes the row kernel, and
+    // so does every product when `rows` asks for it (the short prefill's)
+    const bool wanted = rows || mode == 2 || (mode == 1 && N >= 16384 && !c->lt);
     const bool fits = wanted && ssm::rowgemm_ok(M, N, K) && al16(x) && al16(W) && ldx % 4 == 0 &&
                       al16(g) && (mode != 2 || (al16(z) && ldz % 4 == 0 && d.G == 1));
     if (fits) {
@@ -1296,6 +1355,26 @@ ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s
     return ssm_rmsnorm(w.hid, d.d, m->w + m->norm_f, w.nrm, d.d, (int)T, d.d, d.eps, st);
 }
 
+// The own LM head (head.hip) over `rows` final hidden rows x (row stride ldx): the final
+// norm's operand x * g_f in fragment order and its partial sums (xg_ssq_kernel), then the
+// logits on the fragment-order tied embedding with the norm's scale applied per row, and the
+// greedy picks into d_argmax when given. Replaces the final RMSNorm, the library product and
+// the full-row argmax for up to kStepProjMaxRows rows.
+bool own_head_ok(ssm_model* m, const Ws& w, long rows) {
+    return w.xg && w.hpart && rows <= ssm::kStepProjMaxRows &&
+           ssm::head_ok((int)rows, m->dm.V, m->dm.d);
+}
+ssm_status head_rows(ssm_model* m, const Ws& w, const float* x, long ldx, int rows, float* lg,
+                     uint32_t* d_argmax) {
+    const Dims& d = m->dm;
+    hipStream_t st = m->ctx->stream;
+    if (!m->wp) SSM_TRY(pack_weights(m));
+    Stage g(m->ctx, "head");
+    SSM_TRY(ssm::launch_xg_ssq(x, ldx, m->w + m->norm_f, w.xg, w.ssq_in, rows, d.d, st));
+    return ssm::launch_head(w.xg, w.ssq_in, d.d / 16, 1.f / (float)d.d, d.eps,
+                            m->wp + m->wp_emb, lg, d.V, rows, d.V, d.d, w.hpart, d_argmax, st);
+}
+
 ssm_status check_flag(ssm_model* m) {
     int bad = 0;
     SSM_HIP_TRY(hipMemcpyAsync(&bad, m->d_flag, sizeof(int), hipMemcpyDeviceToHost,
@@ -1486,7 +1565,10 @@ extern "C" ssm_status ssm_forward_device(ssm_model* m, const uint32_t* d_ids, in
     if (B == 0 || L == 0) return SSM_OK;
     Ws w;
     SSM_TRY(ensure_ws(m, B, L, false, &w));
-    SSM_TRY(trunk(m, d_ids, B, L, nullptr, w));
+    const long T = (long)B * L;
+    const bool own = own_head_ok(m, w, T);
+    SSM_TRY(trunk(m, d_ids, B, L, nullptr, w, !own));
+    if (own) return head_rows(m, w, w.hid, m->dm.d, (int)T, d_logits, nullptr);
     return gemm(m->ctx, B * L, m->dm.V, m->dm.d, w.nrm, m->dm.d, m->w + m->emb, d_logits,
                 m->dm.V, 0.f);
 }
@@ -1502,9 +1584,11 @@ extern "C" ssm_status ssm_forward(ssm_model* m, const uint32_t* ids, int B, int 
     Ws w;
     SSM_TRY(ensure_ws(m, B, L, true, &w));
     SSM_HIP_TRY(hipMemcpyAsync(m->d_ids, ids, T * 4, hipMemcpyHostToDevice, m->ctx->stream));
-    SSM_TRY(trunk(m, m->d_ids, B, L, nullptr, w));
-    SSM_TRY(gemm(m->ctx, (int)T, m->dm.V, m->dm.d, w.nrm, m->dm.d, m->w + m->emb, w.logits,
-                 m->dm.V, 0.f));
+    const bool own = own_head_ok(m, w, (long)T);
+    SSM_TRY(trunk(m, m->d_ids, B, L, nullptr, w, !own));
+    if (own) SSM_TRY(head_rows(m, w, w.hid, m->dm.d, (int)T, w.logits, nullptr));
+    else SSM_TRY(gemm(m->ctx, (int)T, m->dm.V, m->dm.d, w.nrm, m->dm.d, m->w + m->emb, w.logits,
+                      m->dm.V, 0.f));
     SSM_HIP_TRY(hipMemcpyAsync(logits, w.logits, T * m->dm.V * 4, hipMemcpyDeviceToHost,
                                m->ctx->stream));
     return check_flag(m);
@@ -1660,7 +1744,13 @@ ssm_status prefill_device(ssm_model* m, ssm_state* s, const uint32_t* d_ids, int
     const Dims& d = m->dm;
     Ws w;
     SSM_TRY(ensure_ws(m, s->B, L, false, &w));
-    SSM_TRY(trunk(m, d_ids, s->B, L, s, w));
+    // the own LM head on the B last positions (their final norm folded in), else the final
+    // norm, the library product and the argmax
+    const bool own = own_head_ok(m, w, s->B);
+    SSM_TRY(trunk(m, d_ids, s->B, L, s, w, !own));
+    if (own)
+        return head_rows(m, w, w.hid + (long)(L - 1) * d.d, (long)L * d.d, s->B, s->d_logits,
+                         d_argmax);
     SSM_TRY(ssm::launch_gather_rows(w.nrm, L, L - 1, w.last, s->B, d.d, m->ctx->stream));
     SSM_TRY(gemm(m->ctx, s->B, d.V, d.d, w.last, d.d, m->w + m->emb, s->d_logits, d.V, 0.f));
     if (d_argmax) SSM_TRY(ssm::launch_argmax(s->d_logits, d.V, s->B, d.V, d_argmax, m->ctx->stream));

@@ -123,6 +123,55 @@ def test_prefill_decode_state_matches_oracle(device, layers, N, H, R):
     m.destroy()
 
 
+@pytest.mark.parametrize("layers,N,H", [(["mamba1", "mamba1"], 16, 4),
+                                        (["mamba2", "mamba2"], 128, 4),
+                                        (["mamba1", "mamba2"], 64, 4)])
+@pytest.mark.parametrize("B,L", [(1, 16), (2, 32), (4, 9)])
+def test_short_prefill_matches_oracle(device, layers, N, H, B, L):
+    """Prompts of at most 64 tokens: every product of the mixers on the few-row kernel (the
+    gated norm in its prologue for Mamba-2), the LM head on the B last positions; then a
+    forward of the same B x L tokens (the LM head on all of them, no greedy picks) and two
+    decode steps from the prefilled state."""
+    case(f"short prefill {layers} N={N} B={B} L={L}")
+    m, blob = _model(device, layers, N=N, H=H)
+    om = O.Model(blob)
+    ids = np.random.default_rng(11 + B * L).integers(0, 512, (B, L + 2)).astype(np.uint32)
+    close(m.forward(ids[:, :L]), om.forward(ids[:, :L]), "forward logits")
+    st = m.new_state(B)
+    ost = om.new_state(B)
+    lg, am = st.prefill(ids[:, :L])
+    ref = ost.prefill(ids[:, :L])
+    close(lg, ref, "prefill logits")
+    close(st.read(), ost.read(), "state")
+    for t in range(L, L + 2):
+        lg, _ = st.decode(ids[:, t])
+        close(lg, ost.decode(ids[:, t]), "decode logits")
+    close(st.read(), ost.read(), "state after decode")
+    st.destroy()
+    m.destroy()
+
+
+@pytest.mark.parametrize("layers,N,H", [(["mamba1", "mamba1"], 16, 16),
+                                        (["mamba2", "mamba2"], 128, 16)])
+@pytest.mark.parametrize("B,L", [(1, 300), (3, 200)])
+def test_split_k_prefill_matches_oracle(device, layers, N, H, B, L):
+    """Prompts of a few hundred tokens on a wide model (d_model 512): the own GEMM's tiles
+    leave CUs idle, so its products split K over workgroups (partials added in slice order
+    by the finishing kernel, the residual add and the gated norm's row scale there); the
+    Mamba-1 x_proj / dt_proj as two products. The prefill's logits and state."""
+    case(f"split-K prefill {layers} d=512 N={N} B={B} L={L}")
+    m, blob = _model(device, layers, d=512, N=N, H=H)
+    om = O.Model(blob)
+    ids = np.random.default_rng(5 + L).integers(0, 512, (B, L)).astype(np.uint32)
+    st = m.new_state(B)
+    ost = om.new_state(B)
+    lg, _ = st.prefill(ids)
+    close(lg, ost.prefill(ids), "prefill logits")
+    close(st.read(), ost.read(), "state")
+    st.destroy()
+    m.destroy()
+
+
 @pytest.mark.parametrize("layers,N", [(["mamba1"] * 4, 16), (["mamba2"] * 2, 128)])
 def test_greedy_ids_bit_exact(device, layers, N):
     case(f"greedy {layers}")
