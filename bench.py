@@ -89,12 +89,16 @@ def parse():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default=None,
                     choices=["cfg1", "cfg2", "cfg3", "cfg3layer", "cfg4", "cfg5", "decode_m1",
-                             "copy"],
+                             "prefill", "copy"],
                     help="one line for this workload only (default: cfg3 fp32 plus extras)")
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default run: skip the extra workloads after the cfg3 line")
+    ap.add_argument("--prefill-shapes", default=None,
+                    help="prefill: comma-separated prompt shapes BxL (default: PREFILL_SHAPES)")
+    ap.add_argument("--prefill-models", default="mamba1,mamba2",
+                    help="prefill: comma-separated models (mamba1, mamba2)")
     ap.add_argument("--sampling", action="store_true",
                     help="cfg4: draw each token with sampleToken on the device (temperature "
                          "0.8, topK 50, topP 0.9) instead of the greedy argmax")
@@ -744,6 +748,70 @@ def w_decode_m1(torch, np, dev, args):
             "step_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+PREFILL_SHAPES = ((1, 16), (1, 64), (4, 16), (1, 200), (1, 256), (1, 512), (8, 64), (1, 1024),
+                  (4, 1024))
+
+
+def w_prefill(torch, np, dev, args):
+    """Session prefill latency (MambaSession's prompt pass, ssm_prefill: host ids in, the
+    greedy next id out, so the time includes both copies and the synchronisation) of the two
+    24-layer decode models (decode_m1's Mamba-1 and cfg4's Mamba-2 dimensions, vocabulary
+    32000) at the prompt shapes B x L of PREFILL_SHAPES: the few-row kernel's range (up to 64
+    tokens), the library's (65-255) and the own GEMM's with split K (256 and up). Wall time
+    per call over `steps` calls after the spin-up and `warmup` calls; the line's value is
+    the Mamba-2 model's tokens/s at 1 x 512."""
+    from ssmjs_amd import backend
+    cfgs = {
+        "mamba1": {"vocabSize": 32000, "dModel": 768, "numLayers": 24, "dState": 16, "dConv": 4,
+                   "expand": 2, "nHeads": 12, "dtRank": 48, "layers": [{"type": "mamba1"}] * 24},
+        "mamba2": {"vocabSize": 32000, "dModel": 1024, "numLayers": 24, "dState": 128,
+                   "dConv": 4, "expand": 2, "nHeads": 32, "nGroups": 1,
+                   "layers": [{"type": "mamba2"}] * 24},
+    }
+    steps, warm = args.steps or 30, args.warmup if args.warmup is not None else 5
+    shapes = PREFILL_SHAPES
+    if args.prefill_shapes:
+        shapes = [tuple(int(v) for v in sh.split("x")) for sh in args.prefill_shapes.split(",")]
+    kinds = [k for k in args.prefill_models.split(",") if k]
+    if not kinds or any(k not in cfgs for k in kinds):
+        raise SystemExit(f"--prefill-models: choose from {sorted(cfgs)}")
+    lat = {}
+    for kind in kinds:
+        m = backend.Model(dev, cfgs[kind], seed=1007)
+        lat[kind] = {}
+        for B, L in shapes:
+            st = m.new_state(B)
+            ids = np.random.default_rng(B * 100003 + L).integers(0, 32000, (B, L)).astype(
+                np.uint32)
+
+            def call():
+                st.prefill(ids, want_logits=False)
+
+            spin_up(torch, call)
+            for _ in range(warm):
+                call()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                call()
+            ms = (time.perf_counter() - t0) / steps * 1e3
+            lat[kind][f"{B}x{L}"] = round(ms, 4)
+            log(f"[bench] prefill {kind} B={B} L={L}: {ms:.3f} ms")
+            st.destroy()
+        m.destroy()
+    # the line's value: the Mamba-2 model at 1 x 512 when it ran, else the first case
+    k0 = "mamba2" if "mamba2" in lat and "1x512" in lat["mamba2"] else kinds[0]
+    s0 = "1x512" if "1x512" in lat[k0] else next(iter(lat[k0]))
+    ms = lat[k0][s0]
+    b0, l0 = (int(v) for v in s0.split("x"))
+    return {"value": b0 * l0 / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
+            "dtype": "f32",
+            "config": {"workload": "session prefill latency of the 24-layer decode models "
+                                   "(host ids in, greedy id out), per prompt shape B x L",
+                       "value_at": f"{k0} {s0}"},
+            "latency_ms": lat}
+
+
 def w_copy(torch, args):
     """Counter calibration, not a bench line: one elementwise kernel (y = x * 1) that reads
     and writes exactly 1 GiB each, so FETCH_SIZE / WRITE_SIZE of a rocprofv3 --pmc run can be
@@ -793,6 +861,7 @@ def main():
         "cfg3layer": lambda a: w_cfg3layer(torch, np, dev, a),
         "cfg4": lambda a: w_cfg4(torch, np, dev, a),
         "decode_m1": lambda a: w_decode_m1(torch, np, dev, a),
+        "prefill": lambda a: w_prefill(torch, np, dev, a),
         "cfg5": lambda a: ssd_workload(torch, np, dev, a, 1, 65536, 32, 128 ** -0.25, cfg5_name,
                                        "bf16"),
     }

@@ -28,15 +28,16 @@
 // tiles are numbered in groups of 8 row tiles (a group walks its columns), so the tiles in
 // flight on an XCD share X rows and W rows through that XCD's L2.
 //
-// Split K. When the tiles alone leave CUs idle (fewer than 256: prompts of a few hundred
-// tokens), K may be cut into S slices of a multiple of 16 (at least 128 each) and every
-// (tile, slice) pair is a workgroup of its own (slice z of row tile tm is row tile tm + z mt
-// of an S times taller grid, so the ordering above is unchanged); each writes its raw
-// partial tile to a workspace (S, M, N), and a second kernel adds the S partials in slice
-// order (deterministic) and applies the epilogue (row scale, bias, beta, gate) in the same
-// order as the unsplit kernel. S is chosen by a cost model measured on MI355X: a CU running
-// one of these workgroups does 0.44 TFLOP/s, two or more 0.50 (of 0.61 peak), the partials
-// cost their bytes written and read at 5 TB/s, and the finishing launch about 4 us.
+// Split K. When the tiles alone leave CUs idle (prompts of a few hundred tokens), K may be
+// cut into S slices of a multiple of 16 (at least 128 each) and every (tile, slice) pair is
+// a workgroup of its own (slice z of row tile tm is row tile tm + z mt of an S times taller
+// grid, so the ordering above is unchanged); each writes its raw partial tile to a
+// workspace (S, M, N), and a second kernel adds the S partials in slice order
+// (deterministic) and applies the epilogue (row scale, bias, beta, gate) in the same order
+// as the unsplit kernel. The tile width and S are chosen together by a cost model measured
+// on MI355X: a CU running one of these workgroups does 0.44 TFLOP/s, two or more 0.50 (of
+// 0.61 peak), the partials cost their bytes written and read at 5 TB/s, and the finishing
+// launch about 4 us.
 //
 // Measured (MI355X, fp32 TFLOP/s, this kernel / hipBLASLt): M 32768 N 2048 K 4096 150 / 151,
 // M 32768 N 8448 K 2016 148 / 149, M 8192 N 3072 K 768 119 / 118. At a clock of 2.4 GHz the
@@ -581,36 +582,40 @@ bool gemm_ok(int M, int N, int K, long ldx, long ldw, long ldy) {
            (long)BM * ldy * 4 < lim;
 }
 
-// Split of K for a grid of `tiles` tiles of BN columns: the slice count (1: none) with the
-// least modelled time (above), slices at least 128 deep and a multiple of 16, within the
-// workspace (part_floats). No split once the tiles cover every CU.
-int pick_split(int M, int N, int K, int bn, long tiles, size_t part_floats, int* kslice) {
-    *kslice = K;
-    if (tiles >= 256 || N % 4 || K < 256) return 1;
-    const double fl = 2.0 * BM * bn;   // flops of a tile per unit of k
-    auto busy = [&](long wgs, int depth) {   // the most loaded CU's time (s)
+// Tile width and split of K for a grid under two rounds of resident workgroups (pick_nj's
+// grid has fewer than 512 tiles): the (NJ, slice count) pair with the least modelled time
+// (above), slices at least 128 deep and a multiple of 16, within the workspace
+// (part_floats floats). Larger grids keep pick_nj's width, unsplit.
+struct Plan { int nj, ks, kslice; };
+Plan pick_plan(int M, int N, int K, size_t part_floats) {
+    const long mt = (M + BM - 1) / BM;
+    Plan p{pick_nj(M, N), 1, K};
+    if (mt * ((N + 32 * p.nj - 1) / (32 * p.nj)) >= 512) return p;
+    auto busy = [&](long wgs, int bn, int depth) {   // the most loaded CU's time (s)
         const long n = (wgs + 255) / 256;
-        return (double)n * fl * depth / (n == 1 ? 0.44e12 : 0.50e12);
+        return (double)n * 2.0 * BM * bn * depth / (n == 1 ? 0.44e12 : 0.50e12);
     };
-    double best = busy(tiles, K);
-    int bks = 1, bsl = K;
-    for (int ks = 2; ks <= K / 128; ++ks) {
-        if ((size_t)ks * M * N > part_floats) break;
-        const int sl = ((K + ks - 1) / ks + 15) / 16 * 16;
-        if ((K + sl - 1) / sl != ks) continue;
-        const double t = busy(tiles * ks, sl) + 8.0 * ks * M * N / 5e12 + 4e-6;
-        if (t < best) best = t, bks = ks, bsl = sl;
+    double best = 1e300;
+    for (int nj : {2, 3, 4}) {
+        const int bn = 32 * nj;
+        const long tiles = mt * ((N + bn - 1) / bn);
+        const double t1 = busy(tiles, bn, K);
+        if (t1 < best) best = t1, p = Plan{nj, 1, K};
+        if (tiles >= 256 || N % 4 || K < 256) continue;
+        for (int ks = 2; ks <= K / 128; ++ks) {
+            if ((size_t)ks * M * N > part_floats) break;
+            const int sl = ((K + ks - 1) / ks + 15) / 16 * 16;
+            if ((K + sl - 1) / sl != ks) continue;
+            const double t = busy(tiles * ks, bn, sl) + 8.0 * ks * M * N / 5e12 + 4e-6;
+            if (t < best) best = t, p = Plan{nj, ks, sl};
+        }
     }
-    *kslice = bsl;
-    return bks;
+    return p;
 }
 
 size_t gemm_split_floats(int M, int N, int K) {
-    const int nj = pick_nj(M, N);
-    const long tiles = (long)((M + BM - 1) / BM) * ((N + 32 * nj - 1) / (32 * nj));
-    int sl;
-    const int ks = pick_split(M, N, K, 32 * nj, tiles, (size_t)-1, &sl);
-    return ks > 1 ? (size_t)ks * M * N : 0;
+    const Plan p = pick_plan(M, N, K, (size_t)-1);
+    return p.ks > 1 ? (size_t)p.ks * M * N : 0;
 }
 
 ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const float* bias,
@@ -622,13 +627,13 @@ ssm_status launch_gemm(const float* X, long ldx, const float* W, long ldw, const
                     M, N, K, ldx, ldw, ldy);
     if (((uintptr_t)X | (uintptr_t)W) & 15)
         return fail(SSM_ERR_INVALID_ARG, "gemm: X and W must be 16-byte aligned");
-    const int nj = pick_nj(M, N);
+    // with a workspace, the width and split of pick_plan; without, pick_nj's width unsplit
+    const bool ws = part && ((uintptr_t)part & 15) == 0;
+    const Plan p = ws ? pick_plan(M, N, K, part_floats) : Plan{pick_nj(M, N), 1, K};
+    const int nj = p.nj;
     GemmArgs a{X, ldx, W, ldw, Y, ldy, bias, M, N, K, beta, (M + BM - 1) / BM,
-               (N + 32 * nj - 1) / (32 * nj), ssq, nssq, inv_div, eps, gate_c0, 1, K, nullptr};
-    if (part && ((uintptr_t)part & 15) == 0) {
-        a.ks = pick_split(M, N, K, 32 * nj, (long)a.mt * a.nt, part_floats, &a.kslice);
-        if (a.ks > 1) a.part = part;
-    }
+               (N + 32 * nj - 1) / (32 * nj), ssq, nssq, inv_div, eps, gate_c0, p.ks, p.kslice,
+               p.ks > 1 ? part : nullptr};
     if (gate_c0 < N && gate_c0 % 16)
         return fail(SSM_ERR_INVALID_ARG, "gemm: gate column %d not a multiple of 16", gate_c0);
     if (ssq && nssq <= 0) return fail(SSM_ERR_INVALID_ARG, "gemm: row scale needs nssq > 0");

@@ -36,7 +36,7 @@ def test_unknown_workload_is_rejected():
 def test_workloads_listed_in_help():
     r = run("--help")
     assert r.returncode == 0
-    for w in ("cfg1", "cfg2", "cfg3", "cfg3layer", "cfg4", "cfg5", "decode_m1"):
+    for w in ("cfg1", "cfg2", "cfg3", "cfg3layer", "cfg4", "cfg5", "decode_m1", "prefill"):
         assert w in r.stdout
 
 

@@ -87,16 +87,20 @@ def _scan_call(L, B, Lq, D, N, ld, ws=None, ws_bytes=0):
 
 
 def test_scan_workspace_query_matches_the_plan():
-    """The scan's plan depends on (B, D, N) only, so the workspace query and the launch agree
-    at every length and stride: a single-pass shape needs no workspace even where a whole
-    sequence spans more than 2 GiB of rows, and a chunked shape asks for exactly what the
-    query says."""
+    """The scan's plan depends on (B, D, N) and on whether L is at most 256 (short sequences
+    take the single pass whatever their width), not on strides, so the workspace query and
+    the launch agree: a single-pass shape needs no workspace even where a whole sequence
+    spans more than 2 GiB of rows, and a chunked shape asks for exactly what the query
+    says."""
     L = _lib.lib()
     # single pass (B*D*N/64 >= 1024 waves): (2, 140000, 2048, 16) with a 4096-float stride
     # spans 2.3 GB per sequence; before, the launch fell back to the chunked passes here
     # while the query said 0
     assert L.ssm_selective_scan_workspace(2, 140000, 2048, 16) == 0
     assert L.ssm_selective_scan_workspace(4, 2048, 1536, 16) == 0
+    # one sequence of 512 channels: single pass up to 256 steps, chunked beyond
+    assert L.ssm_selective_scan_workspace(1, 256, 512, 16) == 0
+    assert L.ssm_selective_scan_workspace(1, 257, 512, 16) > 0
     # chunked (one sequence of 512 channels): the launch without it names the query's size
     need = L.ssm_selective_scan_workspace(1, 4096, 512, 16)
     assert need > 0
