@@ -1,16 +1,17 @@
-"""GPU parity at BASELINE.json's full sizes. The whole problem runs on the GPU in one call;
-sampled sequences (a batch row and head, or a set of channels) are compared with the CPU oracle
-over their full length, and one property that holds at any size is checked on the whole output.
+"""GPU parity at BASELINE.json's full sizes. The whole problem runs on the GPU in one call
+and every output element and final state is compared with the CPU oracle (the C oracle's
+sequential recurrence, OpenMP over sequences: about half a second per configuration on 16
+cores); one property that holds at any size is checked on the whole output as well.
 
-- SSD, config 3 (B=8 L=4096 H=64 P=64 N=128, fp32 inputs): four sampled (batch, head)
-  sequences and their final states against the oracle, per element; the sequence run as two
-  halves, the second seeded with the first half's final state, gives the same y and final state
-  as one run (the chunk recurrence carried across launches).
-- SSD, config 3 with bf16 inputs: two sampled (batch, head) sequences and their final states.
+- SSD, config 3 (B=8 L=4096 H=64 P=64 N=128, fp32 inputs): all 512 (batch, head) sequences
+  and their final states against the oracle, per element; the sequence run as two halves,
+  the second seeded with the first half's final state, gives the same y and final state as
+  one run (the chunk recurrence carried across launches).
+- SSD, config 3 with bf16 inputs: all sequences and final states.
 - SSD, config 5 (B=1 L=65536 H=32, bf16 inputs; the segmented path: state-only pass, combine,
-  full pass): two sampled heads and their final states against the oracle.
-- Mamba-1 scan, config 2 (B=4 L=2048 D=1536 N=16, the single-pass kernel): 48 sampled channels
-  of every sequence and their final states against the oracle, per element.
+  full pass): all 32 heads and their final states.
+- Mamba-1 scan, config 2 (B=4 L=2048 D=1536 N=16, the single-pass kernel): all channels of
+  every sequence and their final states, per element.
 
 Tolerances as in test_gpu_kernels.py: fp32 per element |gpu - oracle| <= 1e-4 |oracle| +
 1e-5 max|oracle|; bf16 inputs max|gpu - oracle| / max(1, max|oracle|) <= 2e-2, the oracle
@@ -55,17 +56,36 @@ def host(t):
     return t.float().cpu().numpy()
 
 
+def _rows(a):
+    """Leading-axis slices of at most 2**24 elements (bounded float64 temporaries)."""
+    a = np.asarray(a)
+    if a.ndim == 0 or a.size <= (1 << 24):
+        return [a]
+    step = max(1, (1 << 24) // max(1, a.size // a.shape[0]))
+    return [a[i:i + step] for i in range(0, a.shape[0], step)]
+
+
 def check_f32(got, ref, what):
-    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    bound = F32_TOL * np.abs(ref) + F32_FLOOR * float(np.abs(ref).max())
-    ratio = float((np.abs(got - ref) / bound).max())
+    assert np.shape(got) == np.shape(ref), f"{what}: shape {np.shape(got)} vs {np.shape(ref)}"
+    scale = float(np.abs(ref).max())
+    ratio = 0.0
+    for g, r_ in zip(_rows(got), _rows(ref)):
+        g, r_ = g.astype(np.float64), r_.astype(np.float64)
+        assert np.isfinite(g).all(), f"{what}: non-finite values"
+        bound = F32_TOL * np.abs(r_) + F32_FLOOR * scale
+        ratio = max(ratio, float((np.abs(g - r_) / bound).max()))
     print(f"  {what}: worst |err| / bound {ratio:.3f}", flush=True)
     assert ratio <= 1.0, f"{what}: an element exceeds 1e-4 relative + 1e-5 of max ({ratio:.2f}x)"
 
 
 def check_bf16(got, ref, what):
-    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    e = float(np.abs(got - ref).max()) / max(1.0, float(np.abs(ref).max()))
+    assert np.shape(got) == np.shape(ref), f"{what}: shape {np.shape(got)} vs {np.shape(ref)}"
+    err = 0.0
+    for g, r_ in zip(_rows(got), _rows(ref)):
+        g, r_ = g.astype(np.float64), r_.astype(np.float64)
+        assert np.isfinite(g).all(), f"{what}: non-finite values"
+        err = max(err, float(np.abs(g - r_).max()))
+    e = err / max(1.0, float(np.abs(ref).max()))
     print(f"  {what}: err {e:.2e}", flush=True)
     assert e <= BF16_TOL, f"{what}: {e:.2e} beyond {BF16_TOL}"
 
@@ -86,11 +106,9 @@ def ssd_inputs(r, B, L, H, P, N, bc_scale):
     return x, dt, A, Bm, Cm, Dk
 
 
-def oracle_head(x, dt, A, Bm, Cm, Dk, b, h):
-    """The oracle on one (batch, head) sequence over its full length (one group)."""
-    y, hT = O.ssd(x[b:b + 1, :, h:h + 1], dt[b:b + 1, :, h:h + 1], A[h:h + 1], Bm[b:b + 1],
-                  Cm[b:b + 1], Dk[h:h + 1], return_state=True)
-    return y[0, :, 0], hT[0, 0]
+def oracle_all(x, dt, A, Bm, Cm, Dk):
+    """The oracle on every (batch, head) sequence over its full length (one group)."""
+    return O.ssd(x, dt, A, Bm, Cm, Dk, return_state=True)
 
 
 def test_ssd_config3_full_size_f32():
@@ -102,10 +120,10 @@ def test_ssd_config3_full_size_f32():
     hT = torch.zeros(B, H, P, N, device="cuda")
     y = K().ssd_chunk_scan(tx, tdt, tA, tB, tC, tD, None, True, hT=hT)
     yh, hTh = host(y), host(hT)
-    for b, h in ((0, 0), (3, 17), (5, 40), (7, 63)):
-        ry, rh = oracle_head(x, dt, A, Bm, Cm, Dk, b, h)
-        check_f32(yh[b, :, h], ry, f"y (b={b}, h={h})")
-        check_f32(hTh[b, h], rh, f"final state (b={b}, h={h})")
+    ry, rh = oracle_all(x, dt, A, Bm, Cm, Dk)
+    check_f32(yh, ry, "y (all 512 sequences)")
+    check_f32(hTh, rh, "final states (all 512)")
+    del ry, rh
     # two halves, the second seeded with the first half's final state
     Lh = L // 2
     hm = torch.zeros(B, H, P, N, device="cuda")
@@ -130,10 +148,9 @@ def test_ssd_config3_full_size_bf16():
     y = K().ssd_chunk_scan(dev(x, torch.bfloat16), dev(dt), dev(A), dev(Bm, torch.bfloat16),
                            dev(Cm, torch.bfloat16), dev(Dk), None, True, hT=hT)
     yh, hTh = host(y), host(hT)
-    for b, h in ((1, 2), (6, 51)):
-        ry, rh = oracle_head(x, dt, A, Bm, Cm, Dk, b, h)
-        check_bf16(yh[b, :, h], ry, f"y (b={b}, h={h})")
-        check_bf16(hTh[b, h], rh, f"final state (b={b}, h={h})")
+    ry, rh = oracle_all(x, dt, A, Bm, Cm, Dk)
+    check_bf16(yh, ry, "y (all 512 sequences)")
+    check_bf16(hTh, rh, "final states (all 512)")
 
 
 def test_ssd_config5_full_size_bf16():
@@ -146,10 +163,9 @@ def test_ssd_config5_full_size_bf16():
     y = K().ssd_chunk_scan(dev(x, torch.bfloat16), dev(dt), dev(A), dev(Bm, torch.bfloat16),
                            dev(Cm, torch.bfloat16), dev(Dk), None, True, hT=hT)
     yh, hTh = host(y), host(hT)
-    for h in (0, 21):
-        ry, rh = oracle_head(x, dt, A, Bm, Cm, Dk, 0, h)
-        check_bf16(yh[0, :, h], ry, f"y (h={h})")
-        check_bf16(hTh[0, h], rh, f"final state (h={h})")
+    ry, rh = oracle_all(x, dt, A, Bm, Cm, Dk)
+    check_bf16(yh, ry, "y (all 32 heads)")
+    check_bf16(hTh, rh, "final states (all 32 heads)")
 
 
 def test_scan_config2_full_size():
@@ -166,8 +182,6 @@ def test_scan_config2_full_size():
     hT = torch.zeros(B, D, N, device="cuda")
     y = K().selective_scan(dev(u), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk), dev(z), hT=hT)
     yh, hTh = host(y), host(hT)
-    idx = np.sort(r.choice(D, 48, replace=False))
-    ry, rh = O.selective_scan(u[:, :, idx], dt[:, :, idx], A[idx], Bm, Cm, Dk[idx], z[:, :, idx],
-                              return_state=True)
-    check_f32(yh[:, :, idx], ry, "y (48 channels, all sequences)")
-    check_f32(hTh[:, idx], rh, "final state (48 channels)")
+    ry, rh = O.selective_scan(u, dt, A, Bm, Cm, Dk, z, return_state=True)
+    check_f32(yh, ry, "y (all channels and sequences)")
+    check_f32(hTh, rh, "final states (all channels)")
