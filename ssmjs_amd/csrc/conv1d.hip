@@ -23,6 +23,17 @@ struct vec_t<1> { using type = float; };
 template <>
 struct vec_t<4> { using type = float4; };
 
+// a run's own rows, read by no other thread: streaming loads (ssm::load_nt4)
+template <int VEC>
+__device__ __forceinline__ void load_nt(const float* p, float (&v)[VEC]) {
+    if constexpr (VEC == 4) {
+        const float4 q = ssm::load_nt4(p);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+        v[0] = __builtin_nontemporal_load(p);
+    }
+}
+
 template <int VEC>
 __device__ __forceinline__ void load_v(const float* p, float (&v)[VEC]) {
     if constexpr (VEC == 4) {
@@ -33,12 +44,13 @@ __device__ __forceinline__ void load_v(const float* p, float (&v)[VEC]) {
     }
 }
 
+// outputs are read by the next launch only: streaming stores
 template <int VEC>
 __device__ __forceinline__ void store_v(float* p, const float (&v)[VEC]) {
     if constexpr (VEC == 4) {
-        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        ssm::store_nt4(make_float4(v[0], v[1], v[2], v[3]), p);
     } else {
-        *p = v[0];
+        __builtin_nontemporal_store(v[0], p);
     }
 }
 
@@ -47,9 +59,10 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 template <int VEC>
 __device__ __forceinline__ void store_v(__bf16* p, const float (&v)[VEC]) {
     if constexpr (VEC == 4) {
-        *reinterpret_cast<bf16x4_t*>(p) = bf16x4_t{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+        __builtin_nontemporal_store(bf16x4_t{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]},
+                                    reinterpret_cast<bf16x4_t*>(p));
     } else {
-        *p = (__bf16)v[0];
+        __builtin_nontemporal_store((__bf16)v[0], p);
     }
 }
 
@@ -90,10 +103,15 @@ __global__ __launch_bounds__(256) void conv1d_fwd(const float* __restrict__ x, l
     }
     if (t0 + kTT <= L) {
         // full run: all kTT input rows are issued before the first use (kTT + K - 1 loads in
-        // flight per thread), then the window slides over registers
+        // flight per thread), then the window slides over registers. The last K - 1 rows are
+        // also the next run's window (ordinary loads: that thread finds them in L2); the
+        // others stream.
         float xs[kTT][VEC];
 #pragma unroll
-        for (int i = 0; i < kTT; ++i) load_v<VEC>(xb + (long)(t0 + i) * ldx, xs[i]);
+        for (int i = 0; i < kTT; ++i) {
+            if (i < kTT - (K - 1)) load_nt<VEC>(xb + (long)(t0 + i) * ldx, xs[i]);
+            else load_v<VEC>(xb + (long)(t0 + i) * ldx, xs[i]);
+        }
 #pragma unroll
         for (int i = 0; i < kTT; ++i) {
             float out[VEC];

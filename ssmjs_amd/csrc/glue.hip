@@ -69,9 +69,10 @@ __global__ __launch_bounds__(256) void cast_bf16_kernel(const float* __restrict_
     const long r = i / cw;
     const int c = (int)(i % cw);
     if constexpr (V4) {
-        const float4 v = *reinterpret_cast<const float4*>(x + r * ldx + 4 * c);
-        *reinterpret_cast<bf16x4_t*>(y + r * ldy + 4 * c) =
-            bf16x4_t{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+        // streaming: each value is read and written once
+        const float4 v = ssm::load_nt4(x + r * ldx + 4 * c);
+        __builtin_nontemporal_store(bf16x4_t{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w},
+                                    reinterpret_cast<bf16x4_t*>(y + r * ldy + 4 * c));
     } else {
         y[r * ldy + c] = (__bf16)x[r * ldx + c];
     }
@@ -95,8 +96,8 @@ __global__ __launch_bounds__(kBlock) void gated_rmsnorm_row_kernel(
         const int e = 4 * (threadIdx.x + kBlock * r);
         u[r] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (e < n) {
-            const float4 xv = *reinterpret_cast<const float4*>(xr + e);
-            const float4 zv = *reinterpret_cast<const float4*>(zr + e);
+            const float4 xv = ssm::load_nt4(xr + e);   // x, z and y stream (used once)
+            const float4 zv = ssm::load_nt4(zr + e);
             u[r] = make_float4(xv.x * ssm::silu(zv.x), xv.y * ssm::silu(zv.y),
                                xv.z * ssm::silu(zv.z), xv.w * ssm::silu(zv.w));
         }
@@ -114,9 +115,10 @@ __global__ __launch_bounds__(kBlock) void gated_rmsnorm_row_kernel(
         const float o0 = u[r].x * rs * wv.x, o1 = u[r].y * rs * wv.y, o2 = u[r].z * rs * wv.z,
                     o3 = u[r].w * rs * wv.w;
         if constexpr (sizeof(OT) == 2) {
-            *reinterpret_cast<bf16x4_t*>(yr + e) = bf16x4_t{(__bf16)o0, (__bf16)o1, (__bf16)o2, (__bf16)o3};
+            __builtin_nontemporal_store(bf16x4_t{(__bf16)o0, (__bf16)o1, (__bf16)o2, (__bf16)o3},
+                                        reinterpret_cast<bf16x4_t*>(yr + e));
         } else {
-            *reinterpret_cast<float4*>(yr + e) = make_float4(o0, o1, o2, o3);
+            ssm::store_nt4(make_float4(o0, o1, o2, o3), yr + e);
         }
     }
 }

@@ -276,8 +276,10 @@ __global__ __launch_bounds__(256 * HPW, HPW > 1 ? 1 : 2) void ssd_kernel(SsdArgs
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         raw.dt = bload4(rd, od);
+        // x is read by this head only: streaming loads; B (and C) serve every head of the
+        // group on this XCD and stay ordinary, so the other heads find them in L2
 #pragma unroll
-        for (int k = 0; k < RW::XK; ++k) raw.x[k] = bload16<v8>(rx, ox + k * oxk);
+        for (int k = 0; k < RW::XK; ++k) raw.x[k] = ssm::bload16_nt<v8>(rx, ox + k * oxk);
 #pragma unroll
         for (int k = 0; k < RW::BPASS; ++k) raw.b[k] = bload16<v8>(rb, ob + k * obk);
         if constexpr (CST) {
@@ -527,9 +529,10 @@ __global__ __launch_bounds__(256 * HPW, HPW > 1 ? 1 : 2) void ssd_kernel(SsdArgs
                     const floatx4 s0 = swap_pair(Y[2 * hh]), s1 = swap_pair(Y[2 * hh + 1]);
                     const floatx4 v0 = podd ? s1 : Y[2 * hh];        // row 16wl + (l16 & ~1)
                     const floatx4 v1 = podd ? Y[2 * hh + 1] : s0;    // row 16wl + (l16 & ~1) + 1
-                    bstore16(make_float4(v0[0], v0[1], v0[2], v0[3]), ry, oy + 128u * hh);
-                    bstore16(make_float4(v1[0], v1[1], v1[2], v1[3]), ry,
-                             oy + (unsigned)(a.ldy * 4) + 128u * hh);
+                    // y streams out (read by the next launch only)
+                    ssm::bstore16_nt(make_float4(v0[0], v0[1], v0[2], v0[3]), ry, oy + 128u * hh);
+                    ssm::bstore16_nt(make_float4(v1[0], v1[1], v1[2], v1[3]), ry,
+                                     oy + (unsigned)(a.ldy * 4) + 128u * hh);
                 }
             }
         }
@@ -642,8 +645,10 @@ __global__ __launch_bounds__(256 * HPW, HPW > 1 ? 1 : 2) void ssd_state_kernel(S
         const auto rx = rsrc(x0 + r0 * a.ldx, span(qv, a.ldx, P, SZ));
         const auto rb = rsrc(b0 + r0 * a.ldb, span(qv, a.ldb, NN, SZ));
         r.dt = bload4(rd, od);
+        // streaming x loads, as in the full pass (with ordinary loads here, the full pass's
+        // streaming reads of the same x measured slower: 257.6 against 232.0 us at cfg5)
 #pragma unroll
-        for (int k = 0; k < RW::XK; ++k) r.x[k] = bload16<v8>(rx, ox + k * oxk);
+        for (int k = 0; k < RW::XK; ++k) r.x[k] = ssm::bload16_nt<v8>(rx, ox + k * oxk);
 #pragma unroll
         for (int k = 0; k < RW::BPASS; ++k) r.b[k] = bload16<v8>(rb, ob + k * obk);
     };
