@@ -63,19 +63,20 @@ METRIC = "SSM tokens/s on 1×MI355X (prefill + decode) + % of HBM/MFMA roofline"
 # read 1.0000 GiB each way). The commands and per-kernel counts sit with the rocprof summaries
 # in profiles/. Re-measured when the kernels change; None where not measured.
 TRAFFIC = {
-    ("cfg2", "m1.in_proj"): 345_610_228,               # gemm_f32_kernel<4>
-    ("cfg2", "m1.conv"): 110_209_453,                  # conv1d_fwd
-    ("cfg2", "m1.x_dt_proj"): 111_384_987,             # xproj_dt_kernel
-    ("cfg2", "m1.scan"): 205_000_625,                  # scan_w16_kernel
-    ("cfg2", "m1.out_proj"): 159_900_310,              # gemm_f32_kernel<3>
-    ("cfg3", "bf16"): 847_585_780,                     # ssd_kernel (two heads per workgroup)
+    ("cfg2", "m1.in_proj"): 345_239_515,               # gemm_f32_kernel<4>
+    ("cfg2", "m1.conv"): 103_171_772,                  # conv1d_fwd
+    ("cfg2", "m1.x_dt_proj"): 111_457_347,             # xproj_dt_kernel
+    ("cfg2", "m1.scan"): 205_006_791,                  # scan_w16_kernel
+    ("cfg2", "m1.out_proj"): 159_930_259,              # gemm_f32_kernel<3>
+    ("cfg3", "bf16"): 847_398_173,                     # ssd_kernel (two heads per workgroup)
     ("cfg3", "f32"): 1_132_551_840,                    # ssd_f32_kernel (two heads per workgroup)
-    ("cfg4", "m2.step.state_update"): 136_414_806,     # m2_update_kernel (timed on its own)
-    ("cfg5", "bf16"): 1_202_469_259,                   # state pass + combine + full pass
+    ("cfg4", "m2.step.state_update"): 136_414_850,     # m2_update_kernel (timed on its own)
+    ("cfg5", "bf16"): 1_200_922_061,                   # state pass + combine + full pass
 }
 # The commit of the build each TRAFFIC entry was measured on (profiles/hbm_traffic.md); an
 # entry goes stale when its kernel changes after that commit.
-TRAFFIC_MEASURED_AT = {k: "1b2f2f1" for k in TRAFFIC}
+TRAFFIC_MEASURED_AT = {k: "ff51241" for k in TRAFFIC}
+TRAFFIC_MEASURED_AT[("cfg3", "f32")] = "1b2f2f1"
 # rocprofv3's MfmaUtil (matrix-core busy cycles over the dispatch's active cycles) of the SSD
 # launches, averaged over a `--steps 3 --warmup 1` run (profiles/ssd_mfma_util.md)
 MFMA_BUSY = {("cfg3", "f32"): 0.728, ("cfg3", "bf16"): 0.174}
