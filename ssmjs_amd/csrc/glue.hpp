@@ -128,6 +128,10 @@ ssm_status launch_head(const float* xg, const float* ssq, int nssq, float inv_di
 // RMSNorm of a step.
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,
                          int d, hipStream_t st);
+// The one-token step's embedding gather with the first norm's operand in the same pass:
+// hid = E[ids] (M, d), then as launch_xg_ssq on hid with g; ids >= V flag *bad.
+ssm_status launch_embed_xg(const uint32_t* ids, const float* emb, float* hid, const float* g,
+                           float* xg, float* ssq, int M, int d, int V, int* bad, hipStream_t st);
 // Prefill projection (gemm.hip): Y = beta * Y + s[m] X W^T (+ bias) on the fp32 matrix
 // cores; with ssq, s[m] = 1 / sqrt(inv_div * sum_j ssq[m nssq + j] + eps) (a row RMSNorm of
 // X applied after the product), else 1.

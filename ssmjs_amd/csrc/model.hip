@@ -1315,9 +1315,16 @@ ssm_status trunk(ssm_model* m, const uint32_t* d_ids, int B, int L, ssm_state* s
     const Dims& d = m->dm;
     hipStream_t st = m->ctx->stream;
     const long T = (long)B * L;
-    SSM_TRY(ssm::launch_embed(d_ids, m->w + m->emb, w.hid, T, d.d, d.V, m->d_flag, st));
     bool normed = false;   // w.nrm holds the next layer's normalised input (one-token path)
     bool pre = false;      // w.xg / w.ssq_in hold the next layer's x * g and partial sums
+    if (L == 1 && s && d.nl > 0 && fused_step_ok(m, m->layers[0], B, w)) {
+        // the first fused layer's norm operand comes with the embedding gather
+        SSM_TRY(ssm::launch_embed_xg(d_ids, m->w + m->emb, w.hid, m->w + m->layers[0].norm,
+                                     w.xg, w.ssq_in, B, d.d, d.V, m->d_flag, st));
+        pre = true;
+    } else {
+        SSM_TRY(ssm::launch_embed(d_ids, m->w + m->emb, w.hid, T, d.d, d.V, m->d_flag, st));
+    }
     for (int l = 0; l < d.nl; ++l) {
         const LayerW& Ly = m->layers[l];
         float* ss = s ? s->ssm[l] : nullptr;

@@ -264,6 +264,35 @@ __global__ __launch_bounds__(256) void xg_ssq_kernel(const float* __restrict__ x
     if (ok && (n & 15) == 0) ssq[(long)m * (d / 16) + n / 16] = t;
 }
 
+// The embedding gather of a one-token step fused with the first RMSNorm's operand: hid (M, d)
+// = E[ids], xg = hid * g in fragment order and the partial sums of hid^2 per 16 columns, as
+// embed_kernel and xg_ssq_kernel would write them one after the other (ids past V flag *bad
+// and read row 0). M16 * d threads, d % 16 == 0, so the grid is whole blocks of 256.
+__global__ __launch_bounds__(256) void embed_xg_kernel(const uint32_t* __restrict__ ids,
+                                                       const float* __restrict__ emb,
+                                                       float* __restrict__ hid,
+                                                       const float* __restrict__ g,
+                                                       float* __restrict__ xg,
+                                                       float* __restrict__ ssq, int M, int d,
+                                                       int V, int* bad) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int m = (int)(i / d), n = (int)(i % d);
+    const bool ok = m < M;
+    float v = 0.f;
+    if (ok) {
+        uint32_t id = ids[m];
+        if (id >= (uint32_t)V) {
+            if (n == 0) atomicOr(bad, 1);
+            id = 0;
+        }
+        v = emb[(long)id * d + n];
+        hid[(long)m * d + n] = v;
+    }
+    xg[frag_off(m, n, d / 16)] = v * g[n];
+    const float t = sum16(v * v);
+    if (ok && (n & 15) == 0) ssq[(long)m * (d / 16) + n / 16] = t;
+}
+
 // W (N, K) row stride ldw -> fragment order, N padded with zero rows to whole 16-row tiles.
 // One thread per 16 bytes of the output; W is read as scalars (a layer's weights start at any
 // float offset of the checkpoint buffer, and this runs once per weight change).
@@ -381,6 +410,17 @@ ssm_status launch_stepproj(int epi, StepProj a, hipStream_t st) {
     }
     a.rotate = 1;
     return launch_pd<4>(epi, a, grid, st);
+}
+
+ssm_status launch_embed_xg(const uint32_t* ids, const float* emb, float* hid, const float* g,
+                           float* xg, float* ssq, int M, int d, int V, int* bad, hipStream_t st) {
+    SSM_REQUIRE(d % 16 == 0 && d / 16 <= kStepProjMaxSsq && M >= 0 && M <= kStepProjMaxRows,
+                "embed_xg: d_model %d, rows %d", d, M);
+    const long n = (long)((M + 15) / 16) * 16 * d;
+    if (n == 0) return SSM_OK;
+    embed_xg_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(ids, emb, hid, g, xg, ssq, M, d, V,
+                                                             bad);
+    return check_launch("embed_xg");
 }
 
 ssm_status launch_xg_ssq(const float* x, long ldx, const float* g, float* xg, float* ssq, int M,

@@ -289,6 +289,36 @@ def test_decode_graph_replay_matches_eager(device, monkeypatch):
     m.destroy()
 
 
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_decode_rejects_out_of_range_id(device, monkeypatch, mode):
+    """A token id at or past the vocabulary in a one-token step (whose embedding gather also
+    writes the first fused layer's norm operand) is reported as INVALID_ARG, eagerly and from
+    a replayed graph; the flag does not stick, so the next valid step succeeds and matches a
+    model that never saw the bad id from the same state."""
+    case(f"decode out-of-range id ({mode})")
+    from ssmjs_amd import _lib
+    monkeypatch.setenv("SSM_DECODE_GRAPH", "0" if mode == "eager" else "1")
+    m, _ = _model(device, ["mamba2", "mamba1"], N=64)
+    V = m.vocab
+    r = np.random.default_rng(11)
+    st = m.new_state(3)
+    for _ in range(2):   # from the second step on, graph mode replays a captured step
+        st.decode(r.integers(0, V, 3))
+    with pytest.raises(_lib.SsmError) as e:
+        st.decode(np.array([1, V, 2], np.uint32))
+    assert e.value.status == 1 and "out of range" in str(e.value)
+    img = st.read()
+    good = r.integers(0, V, 3)
+    lg, am = st.decode(good)
+    ref = m.new_state(3)
+    ref.write(img)
+    lg_ref, am_ref = ref.decode(good)
+    assert np.array_equal(lg, lg_ref) and np.array_equal(am, am_ref)
+    ref.destroy()
+    st.destroy()
+    m.destroy()
+
+
 def test_greedy_equals_reprefill(device):
     """generate() (recurrent) == tokenStream semantics (full re-prefill each step,
     src/session/streaming.ts:30-45) for topK = 1."""
