@@ -73,7 +73,7 @@ __device__ __forceinline__ float sum16(float v) {
 }
 
 template <int PD, int EPI>
-__global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD <= 4 ? 8 : 5) void stepproj_kernel(
+__global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD > 4 ? (EPI == EPI_CONV ? 4 : 5) : EPI == EPI_CONV ? 6 : 8) void stepproj_kernel(
     StepProj a) {
     constexpr bool CONV = EPI == EPI_CONV || EPI == EPI_CONVX;
     __shared__ float red[kNW][16][17];
@@ -96,6 +96,28 @@ __global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD <= 4 ? 8 : 5) v
         for (int u = 0; u < kSsqPer; ++u) {
             const int j = u * 16 + ej;
             sp[u] = bload4(rs, j < a.nssq ? (unsigned)(em * a.nssq + j) * 4u : kOOR);
+        }
+    }
+
+    // The conv epilogue's inputs (the cached inputs, the taps and the bias of this thread's
+    // channel), loaded here with the operands: they do not depend on the product, and loaded
+    // in the epilogue each would be a memory latency after the last MFMA (the state loads and
+    // the shift stores of one channel alias, so they were also serial there). Widths up to
+    // kConvPre; wider kernels keep the epilogue's own loads.
+    constexpr int kConvPre = 4;
+    const int ec = en - a.c0;
+    const bool conv_pre = CONV && em < a.M && en < a.N && ec >= 0 && ec < a.C && a.Kc <= kConvPre;
+    float csv[kConvPre - 1] = {}, cwv[kConvPre] = {}, cbv = 0.f;
+    if constexpr (CONV) {
+        if (conv_pre) {
+            const float* st = a.cst + ((long)em * a.C + ec) * (a.Kc - 1);
+#pragma unroll
+            for (int k = 0; k < kConvPre - 1; ++k)
+                if (k < a.Kc - 1) csv[k] = st[k];
+#pragma unroll
+            for (int k = 0; k < kConvPre; ++k)
+                if (k < a.Kc) cwv[k] = a.cw[(long)ec * a.Kc + k];
+            if (a.cb) cbv = a.cb[ec];
         }
     }
 
@@ -189,7 +211,27 @@ __global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD <= 4 ? 8 : 5) v
         const bool in_conv = c >= 0 && c < a.C;
         float u = 0.f;   // the conv output; 0 on padding rows
         if (ok && !in_conv) a.Y[(long)em * a.ldy + en] = v;
-        if (ok && in_conv) {
+        if (conv_pre) {
+            // same arithmetic order as the conv update kernel (conv1d.hip), on the prefetched
+            // inputs
+            const int Kc = a.Kc;
+            float* st = a.cst + ((long)em * a.C + c) * (Kc - 1);
+            float acc = cbv;
+#pragma unroll
+            for (int k = 0; k < kConvPre - 1; ++k)
+                if (k < Kc - 1) acc = fmaf(cwv[k], csv[k], acc);
+            float wl = cwv[0];
+#pragma unroll
+            for (int k = 1; k < kConvPre; ++k)
+                if (k == Kc - 1) wl = cwv[k];
+            acc = fmaf(wl, v, acc);
+#pragma unroll
+            for (int k = 1; k < kConvPre - 1; ++k)   // shift the cached inputs down
+                if (k < Kc - 1) st[k - 1] = csv[k];
+            if (Kc > 1) st[Kc - 2] = v;
+            u = silu_fast(acc);
+            a.Yc[(long)em * a.ldyc + c] = u;
+        } else if (ok && in_conv) {
             // same arithmetic order as the conv update kernel (conv1d.hip)
             const int Kc = a.Kc;
             const float* wc = a.cw + (long)c * Kc;
