@@ -359,7 +359,7 @@ void launch_nj(const GemmArgs& a, bool beta, hipStream_t st) {
 // memory straight into registers (one b128 per lane) through a ring of PD k blocks in
 // flight; the eight partial tiles meet in LDS and are added in wave order. dt_low stays in
 // LDS, in MFMA operand order, as the A operand of dt_proj; wave w then produces its share of
-// dt's 16-column blocks (K = R, Wdt from L2, again PD blocks in flight). xc is read once and
+// dt's 16-column blocks (K = R, Wdt from L2 in groups of column blocks). xc is read once and
 // dt_low never reaches memory. Loads and steps past a wave's range are issued anyway with
 // out-of-range offsets (they read zeros and their stores are dropped), so every wave runs
 // the same straight-line ring and the compiler's wait counts stay exact.
@@ -482,7 +482,11 @@ __global__ __launch_bounds__(XD_ROWS * 16, 1) void xproj_dt_kernel(XdArgs a) {
 #pragma unroll
     for (int kb = 0; kb < KB2; ++kb)
         owd[kb] = (16 * kb + 4 * q < a.R) ? (unsigned)((i16 * a.R + 16 * kb + 4 * q) * 4) : 0x80000000u;
-    floatx4 wd[PD][KB2];
+    // Wdt fragments in groups of DG column blocks, all of a group loaded before any of its
+    // outputs is stored: a load issued after stores counts as done only once those stores
+    // are (one in-order counter), so a ring refilled between the stores would wait for them
+    constexpr int DG = KB2 <= 3 ? 6 : 4;
+    floatx4 wd[DG][KB2];
     auto wfetch = [&](int buf, int cb) {
         const bool ok = cb < cb0 + cper;
         const unsigned rr = (unsigned)(16 * cb * a.R) * 4u;
@@ -510,16 +514,13 @@ __global__ __launch_bounds__(XD_ROWS * 16, 1) void xproj_dt_kernel(XdArgs a) {
                 ssm::bstore4(v, rdt, ((unsigned)((16 * rb + 4 * q + r) * a.lddt + c) * 4u) | oor);
             }
     };
+    for (int cb = cb0; cb < cb0 + cper; cb += DG) {
 #pragma unroll
-    for (int u = 0; u < PD - 1; ++u) wfetch(u, cb0 + u);
-    for (int cb = cb0; cb < cb0 + cper; cb += PD) {
+        for (int u = 0; u < DG; ++u) wfetch(u, cb + u);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < PD; ++u) {
-            wfetch((u + PD - 1) % PD, cb + u + PD - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            out(u, cb + u);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int u = 0; u < DG; ++u) out(u, cb + u);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
