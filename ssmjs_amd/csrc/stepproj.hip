@@ -121,6 +121,14 @@ __global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD > 4 ? (EPI == E
         }
     }
 
+    // The residual epilogue's inputs (this thread's element of Y and the next norm's weight),
+    // loaded here for the same reason; only this thread reads and writes that element.
+    float rsv = 0.f, g2v = 0.f;
+    if constexpr (EPI == EPI_RESID) {
+        if (em < a.M && en < a.N) rsv = a.Y[(long)em * a.ldy + en];
+        if (a.g2 && en < a.N) g2v = a.g2[en];
+    }
+
     // EPI_CONV with xpart: a tile of conv columns (16 channels; c0 and C are multiples of 16)
     // also projects its 16 x 16 conv outputs onto the next projection's RN columns on the
     // matrix cores (the tile's outputs as the A operand, its 16 rows of wxt as B). Wave w takes
@@ -277,13 +285,12 @@ __global__ __launch_bounds__(64 * kNW, EPI == EPI_CONVX ? 4 : PD > 4 ? (EPI == E
     } else {   // EPI_RESID
         float o = 0.f;
         if (ok) {
-            float* y = a.Y + (long)em * a.ldy + en;
-            o = *y + v;
-            *y = o;
+            o = rsv + v;
+            a.Y[(long)em * a.ldy + en] = o;
         }
         if (a.g2) {
             // rows past M (up to the tile's 16) get zeros: the next projection reads whole tiles
-            if (en < a.N) a.xg[frag_off(em, en, a.nt)] = ok ? o * a.g2[en] : 0.f;
+            if (en < a.N) a.xg[frag_off(em, en, a.nt)] = ok ? o * g2v : 0.f;
             const float t = sum16(o * o);
             if (ej == 0 && em < a.M) a.ssq_out[(long)em * a.nt + tn] = t;
         }
