@@ -397,20 +397,22 @@ def ssd_alg(B, L, H, P, N, esz, Q=256):
     return flops, nbytes
 
 
-def ssd_f32_issued_flops(B, L, H, G, N, P=64, h0=False):
-    """The MFMA work ssd_f32_kernel issues per launch (16x16x4 fp32 MFMAs, 2048 FLOPs each).
-    Chunks of 32 steps; a workgroup owns HPW heads of one group (2 when the heads per group
-    are even) and forms the group's three causal 16x16 C B^T tiles once for them (N / 4
-    MFMAs each). Each head's four waves (16 rows of the head dim each) then issue, per chunk:
-    state-to-output 2 x (N / 4), diagonal part 3 x 4 (the causal 16-step blocks), state
-    update (N / 16) x 2 x 4; without an initial state the first chunk of each sequence skips
-    the state-to-output part. At cfg3 this is 81.336 GFLOP, the figure of
-    SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 (profiles/ssd_mfma_util.md)."""
+def ssd_f32_issued_flops(B, L, H, G, N, P=64, h0=False, cb_prepass=True):
+    """The MFMA work of one fp32 SSD call (16x16x4 fp32 MFMAs, 2048 FLOPs each). Chunks of 32
+    steps; the three causal 16x16 C B^T tiles of a chunk (N / 4 MFMAs each) depend on the
+    group only: with cb_prepass (a workspace of ssm_ssd_workspace's size) ssd_f32_cb_kernel
+    forms them once per (batch, group, chunk) for all the group's heads; without it each
+    workgroup of HPW heads (2 when the heads per group are even) forms them once. Each head's
+    four waves (16 rows of the head dim each) issue, per chunk: state-to-output 2 x (N / 4),
+    diagonal part 3 x 4 (the causal 16-step blocks), state update (N / 16) x 2 x 4; without
+    an initial state the first chunk of each sequence skips the state-to-output part. At cfg3
+    this is 75.10 GFLOP with the pre-pass (81.336 GFLOP without, the figure of
+    SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 in profiles/ssd_mfma_util.md before the pre-pass)."""
     qf = 32
     hpw = 2 if (H // G) % 2 == 0 else 1
-    cbt = 3 * (N // 4)                                   # per workgroup and chunk
+    cbt = 3 * (N // 4)                                   # per tile set
     per_wave = 2 * (N // 4) + 3 * 4 + (N // 16) * 2 * 4
-    per_chunk_head = cbt / hpw + (P // 16) * per_wave
+    per_chunk_head = cbt * (G / H if cb_prepass else 1.0 / hpw) + (P // 16) * per_wave
     total = per_chunk_head * (B * L / qf) * H
     if not h0:
         total -= B * H * (P // 16) * 2 * (N // 4)

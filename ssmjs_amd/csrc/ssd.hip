@@ -1094,7 +1094,7 @@ extern "C" size_t ssm_ssd_workspace(int B, int L, int H, int Pd, int G, int N) {
     int nchunks, nseg, per;
     plan(B, L, H, nchunks, nseg, per);
     const size_t bf = nseg <= 1 ? 0 : sizeof(float) * (size_t)B * H * nseg * ((size_t)Pd * N + 1);
-    return std::max(bf, ssm::ssd_f32_workspace(B, L, H, Pd, N));
+    return std::max(bf, ssm::ssd_f32_workspace(B, L, H, G, Pd, N));
 }
 
 namespace ssm {
@@ -1191,9 +1191,11 @@ extern "C" ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, 
                             N, h0, hT, workspace, workspace_bytes, st);
     plan(B, L, H, a.nchunks, a.nseg, a.chunks_per_seg);
     if (a.nseg > 1) {
-        const size_t need = ssm_ssd_workspace(B, L, H, Pd, G, N);
+        // the bf16 kernel's own part: the segment states and decays
+        const size_t need = sizeof(float) * (size_t)B * H * a.nseg * ((size_t)P * N + 1);
         SSM_REQUIRE(workspace && workspace_bytes >= need,
-                    "ssm_ssd_chunk_scan: workspace of %zu bytes needed", need);
+                    "ssm_ssd_chunk_scan: workspace of %zu bytes needed",
+                    ssm_ssd_workspace(B, L, H, Pd, G, N));
         a.seg_state = (float*)workspace;
         a.seg_decay = a.seg_state + (size_t)B * H * a.nseg * P * N;
     }

@@ -9,7 +9,7 @@ namespace ssm {
 // Head dim 64 with d_state 64 or 128: the shapes the fp32 kernel takes.
 bool ssd_f32_shape(int Pd, int N);
 // Workspace bytes of ssd_f32 (segment states when long sequences are cut into segments).
-size_t ssd_f32_workspace(int B, int L, int H, int Pd, int N);
+size_t ssd_f32_workspace(int B, int L, int H, int G, int Pd, int N);
 // The SSD of ssm_ssd_chunk_scan for float32 inputs (arguments as there; shapes checked by the
 // caller). With ssq, the output carries the gated RMSNorm's element-wise part instead of y:
 // y <- u * gn with u = y * silu(z) (z (B*L, H*P), row stride ldz; gn (H*P)), and

@@ -6,8 +6,13 @@
 // the heads per group are even, else one); four waves per head own the four 16-row blocks of
 // the head dim (wave w of a head: p = 16w .. 16w+15) and walk the segment's chunks of
 // QF = 32 time steps in order. B, C and the raw C B^T tiles depend on the group only, so a
-// two-head workgroup stages B and C once and forms each C B^T tile once, scaled into both
-// heads' M^T. A small chunk is the cheaper one here: the state never leaves the registers,
+// two-head workgroup stages B and C once, and the C B^T tiles are formed once per (batch,
+// group, chunk) by a pre-pass (ssd_f32_cb_kernel, into the workspace) and prefetched a chunk
+// ahead, one tile per wave, then scaled into both heads' M^T; without room for them in the
+// workspace the workgroup forms each tile once itself. Between the chunk's two barriers the
+// tiles were the MFMA work of three waves while the others waited (the pre-pass took cfg3
+// from 693 to 645 µs plus 9.5 µs for the pre-pass, same bits). A small chunk is the cheaper
+// one here: the state never leaves the registers,
 // so nothing is paid per chunk in memory, while the quadratic in-chunk terms (C B^T and its
 // product with X) shrink with the chunk.
 //
@@ -69,6 +74,9 @@ struct F32Args {
     float* hT;
     float* seg_state;   // (B,H,nseg,P,N)
     float* seg_decay;   // (B,H,nseg)
+    // given: the raw C B^T tiles of every (batch, group, chunk) from ssd_f32_cb_kernel,
+    // (B, G, nchunks, 3 tiles, 64 lanes, 4) in accumulator order; else the full pass forms them
+    const float* cbw;
     int remap;
     // gated output (GATED): y <- u * gn with u = y * silu(z), and ssq (B*L, H) = sum over the
     // head's P channels of u^2 (the gated RMSNorm's element-wise part and its partial sums)
@@ -193,6 +201,17 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
     // scan_wave of each head scans that head's next chunk.
     const int rot = blockIdx.x & 3;
     const int scan_wave = (NCB + rot) & 3;
+    // With a.cbw the tiles come from the pre-pass: this wave's tile (t with (t + rot) & 3 ==
+    // wl, on the first head's waves) of chunk c is loaded one chunk ahead into cbv (chunks
+    // past the last read zeros).
+    const int tw = (wl - rot + 4) & 3;
+    const bool cb_wave = FULL && hw == 0 && tw < NCB && a.cbw != nullptr;
+    const auto rcb = rsrc(a.cbw ? a.cbw + ((long)b * a.G + g) * a.nchunks * NCB * 256 : a.x,
+                          a.cbw ? (unsigned)(a.nchunks * NCB * 256 * 4) : 0u);
+    floatx4 cbv{0.f, 0.f, 0.f, 0.f};
+    auto load_cb = [&](int c) {
+        if (cb_wave) cbv = bload16<floatx4>(rcb, (unsigned)((c * NCB + tw) * 256 + 4 * lane) * 4u);
+    };
 
     // raw inputs of one chunk: X[j = 16 jb + 4 q4 + s][p0 + l16], B and C staging rows, dt
     struct Raw {
@@ -279,6 +298,7 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
         const int qv0 = rows_of(c_begin);
         const auto rd0 = rsrc(d0 + (long)c_begin * QF * a.lddt, span(qv0, a.lddt, 1));
         if (wl == 0) scan_put(c_begin, bload4(rd0, (unsigned)(lane * a.lddt) * 4u), c_begin & 1);
+        load_cb(c_begin);
         load_raw(c_begin, c_begin + 1);
     } else {
         load_raw(c_begin, c_begin);
@@ -348,6 +368,7 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
                 // k = n in blocks of 16 (kk); kk and kk + 1 go to two accumulators whose MFMAs
                 // alternate, and the next pair's operands are read while this pair multiplies
                 floatx4 acc0{0.f, 0.f, 0.f, 0.f}, acc1{0.f, 0.f, 0.f, 0.f};
+                if (!cb_wave) {
                 const float* brw = &sm.b[buf][16 * jb + l16][4 * q4];
                 const float* crw = &sm.c[buf][16 * ib + l16][4 * q4];
                 float4 opv[2][4];
@@ -372,7 +393,9 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
                     acc0 = mfma4(o[0].w, o[1].w, acc0);
                     acc1 = mfma4(o[2].w, o[3].w, acc1);
                 }
-                // acc[r] = (C B^T)[i = 16 ib + l16][j = 16 jb + 4 q4 + r]; M^T of each head
+                }
+                // acc0[r] + acc1[r] = (C B^T)[i = 16 ib + l16][j = 16 jb + 4 q4 + r] (from the
+                // pre-pass: cbv[r], the same sum); M^T of each head
                 const int i = 16 * ib + l16;
 #pragma unroll
                 for (int k = 0; k < HPW; ++k) {
@@ -386,7 +409,8 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
                     for (int r = 0; r < 4; ++r) {
                         const int j = 16 * jb + 4 * q4 + r;
                         // the masked (j > i) exponent may overflow: select, never multiply by 0
-                        const float f = (acc0[r] + acc1[r]) * (ssm::ex2(aci - acja[r]) * dvja[r]);
+                        const float cbs = cb_wave ? cbv[r] : acc0[r] + acc1[r];
+                        const float f = cbs * (ssm::ex2(aci - acja[r]) * dvja[r]);
                         mv[r] = j < i ? f : (j == i ? f + Dh[k] : 0.f);
                     }
                     *reinterpret_cast<float4*>(&sm.m[k][i][16 * jb + 4 * q4]) =
@@ -398,6 +422,7 @@ __global__ __launch_bounds__(256 * HPW, 2) void ssd_f32_kernel(F32Args a) {
             float4 zc[GATED ? QB : 1];
 #pragma unroll
             for (int ib = 0; ib < (GATED ? QB : 1); ++ib) zc[ib] = raw.z[ib];
+            load_cb(c + 1);
             load_raw(c + 1, c + 2);
 
             // ---- Y^T[p][i] for the wave's 16 p and the chunk's QF rows i
@@ -528,6 +553,49 @@ __global__ void ssd_f32_seg_prefix(F32Args a, int PN) {
     ssm::seg_prefix_elem(a.seg_state, a.seg_decay, a.h0, a.nseg, PN, i / PN, (int)(i % PN), 1.f);
 }
 
+// The raw C B^T tiles of every chunk, formed once per (batch, group, chunk) for all of the
+// group's heads (the full pass would form them once per workgroup of two heads). Wave t of a
+// workgroup forms causal tile t with the full pass's own MFMA sequence on the same operand
+// values (B and C rows of the chunk, zeros past L), so the tile holds the same bits, and
+// stores it in accumulator order, one float4 per lane.
+template <int NN>
+__global__ __launch_bounds__(192) void ssd_f32_cb_kernel(F32Args a) {
+    constexpr int NB = NN / 16;
+    constexpr int NCB = 3;
+    const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const long id = blockIdx.x;   // (b, g, c), c fastest
+    const int c = (int)(id % a.nchunks);
+    const int bg = (int)(id / a.nchunks), g = bg % a.G, b = bg / a.G;
+    int ib = 0, jb = t;
+    while (jb > ib) { jb -= ib + 1; ++ib; }
+    const int qv = min(QF, a.L - c * QF);
+    const long r0 = (long)b * a.L + (long)c * QF;
+    const auto rb = rsrc(a.Bm + r0 * a.ldb + (long)g * NN, (unsigned)(((long)(qv - 1) * a.ldb + NN) * 4));
+    const auto rc = rsrc(a.Cm + r0 * a.ldc + (long)g * NN, (unsigned)(((long)(qv - 1) * a.ldc + NN) * 4));
+    float4 bo[NB], co[NB];
+#pragma unroll
+    for (int kk = 0; kk < NB; ++kk) {
+        bo[kk] = bload16<float4>(rb, (unsigned)((16 * jb + l16) * a.ldb + 16 * kk + 4 * q4) * 4u);
+        co[kk] = bload16<float4>(rc, (unsigned)((16 * ib + l16) * a.ldc + 16 * kk + 4 * q4) * 4u);
+    }
+    floatx4 acc0{0.f, 0.f, 0.f, 0.f}, acc1{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kp = 0; kp < NB / 2; ++kp) {
+        const float4 o0 = bo[2 * kp], o1 = co[2 * kp], o2 = bo[2 * kp + 1], o3 = co[2 * kp + 1];
+        acc0 = mfma4(o0.x, o1.x, acc0);
+        acc1 = mfma4(o2.x, o3.x, acc1);
+        acc0 = mfma4(o0.y, o1.y, acc0);
+        acc1 = mfma4(o2.y, o3.y, acc1);
+        acc0 = mfma4(o0.z, o1.z, acc0);
+        acc1 = mfma4(o2.z, o3.z, acc1);
+        acc0 = mfma4(o0.w, o1.w, acc0);
+        acc1 = mfma4(o2.w, o3.w, acc1);
+    }
+    const floatx4 sum = acc0 + acc1;
+    *reinterpret_cast<floatx4*>(const_cast<float*>(a.cbw) + (id * NCB + t) * 256 + 4 * lane) = sum;
+}
+
 void plan_f32(int B, int L, int H, int& nchunks, int& nseg, int& per) {
     nchunks = (int)ssm::cdiv(L, QF);
     const long bh = (long)B * H;
@@ -552,6 +620,11 @@ ssm_status launch(F32Args& a, hipStream_t st) {
         e = ssm::check_launch("ssd_f32_seg_prefix");
         if (e != SSM_OK) return e;
     }
+    if (a.cbw) {
+        ssd_f32_cb_kernel<NN><<<(unsigned)((long)a.B * a.G * a.nchunks), 192, 0, st>>>(a);
+        ssm_status e = ssm::check_launch("ssd_f32_cb");
+        if (e != SSM_OK) return e;
+    }
     // two heads per workgroup when heads 2k and 2k + 1 share a group
     const int hpw = ((a.H / a.G) % 2 == 0) ? 2 : 1;
     const int nwg = a.B * (a.H / hpw) * a.nseg;
@@ -572,12 +645,22 @@ namespace ssm {
 
 bool ssd_f32_shape(int Pd, int N) { return Pd == PF && (N == 64 || N == 128); }
 
-size_t ssd_f32_workspace(int B, int L, int H, int Pd, int N) {
-    if (!ssd_f32_shape(Pd, N) || B <= 0 || L <= 0 || H <= 0) return 0;
+// Workspace: the segment states and decays when the sequence is cut into segments, then
+// (at a 256-byte boundary) the C B^T tiles of the pre-pass, 3 KB per (batch, group, chunk).
+// A workspace without room for the tiles runs the full pass with its own tiles.
+static size_t f32_seg_bytes(int B, int H, int nseg, int Pd, int N) {
+    return nseg <= 1 ? 0 : sizeof(float) * (size_t)B * H * nseg * ((size_t)Pd * N + 1);
+}
+static size_t f32_cb_off(size_t seg) { return (seg + 255) & ~(size_t)255; }
+static size_t f32_cb_bytes(int B, int G, int nchunks) {
+    return sizeof(float) * (size_t)B * G * nchunks * 3 * 256;
+}
+
+size_t ssd_f32_workspace(int B, int L, int H, int G, int Pd, int N) {
+    if (!ssd_f32_shape(Pd, N) || B <= 0 || L <= 0 || H <= 0 || G <= 0) return 0;
     int nchunks, nseg, per;
     plan_f32(B, L, H, nchunks, nseg, per);
-    if (nseg <= 1) return 0;
-    return sizeof(float) * (size_t)B * H * nseg * ((size_t)Pd * N + 1);
+    return f32_cb_off(f32_seg_bytes(B, H, nseg, Pd, N)) + f32_cb_bytes(B, G, nchunks);
 }
 
 ssm_status ssd_f32(const float* x, long ldx, const float* dt, long lddt, const float* dt_bias,
@@ -599,13 +682,18 @@ ssm_status ssd_f32(const float* x, long ldx, const float* dt, long lddt, const f
     a.ldc = ldc; a.Dsk = Dsk; a.y = y; a.ldy = ldy; a.B = B; a.L = L; a.H = H; a.G = G;
     a.h0 = h0; a.hT = hT;
     plan_f32(B, L, H, a.nchunks, a.nseg, a.chunks_per_seg);
+    const size_t seg = f32_seg_bytes(B, H, a.nseg, PF, N);
     if (a.nseg > 1) {
-        const size_t need = ssd_f32_workspace(B, L, H, PF, N);
-        SSM_REQUIRE(workspace && workspace_bytes >= need,
-                    "ssm_ssd_chunk_scan: workspace of %zu bytes needed", need);
+        SSM_REQUIRE(workspace && workspace_bytes >= seg,
+                    "ssm_ssd_chunk_scan: workspace of %zu bytes needed",
+                    ssd_f32_workspace(B, L, H, G, PF, N));
         a.seg_state = (float*)workspace;
         a.seg_decay = a.seg_state + (size_t)B * H * a.nseg * PF * N;
     }
+    const size_t cbo = f32_cb_off(seg);
+    if (workspace && ((uintptr_t)workspace & 15) == 0 &&
+        workspace_bytes >= cbo + f32_cb_bytes(B, G, a.nchunks))
+        a.cbw = (const float*)((char*)workspace + cbo);
     return N == 128 ? launch<128>(a, st) : launch<64>(a, st);
 }
 
