@@ -69,18 +69,18 @@ TRAFFIC = {
     ("cfg2", "m1.scan"): 205_006_791,                  # scan_w16_kernel
     ("cfg2", "m1.out_proj"): 159_930_259,              # gemm_f32_kernel<3>
     ("cfg3", "bf16"): 847_398_173,                     # ssd_kernel (two heads per workgroup)
-    ("cfg3", "f32"): 1_132_551_840,                    # ssd_f32_kernel (two heads per workgroup)
+    ("cfg3", "f32"): 1_135_702_044,                    # ssd_f32_kernel (the C B^T pre-pass, ssd_f32_cb_kernel, adds 36.7 MB)
     ("cfg4", "m2.step.state_update"): 136_414_850,     # m2_update_kernel (timed on its own)
     ("cfg5", "bf16"): 1_200_922_061,                   # state pass + combine + full pass
 }
 # The commit of the build each TRAFFIC entry was measured on (profiles/hbm_traffic.md); an
 # entry goes stale when its kernel changes after that commit.
 TRAFFIC_MEASURED_AT = {k: "ff51241" for k in TRAFFIC}
-TRAFFIC_MEASURED_AT[("cfg3", "f32")] = "1b2f2f1"
+TRAFFIC_MEASURED_AT[("cfg3", "f32")] = "51fa711"
 # rocprofv3's MfmaUtil (matrix-core busy cycles over the dispatch's active cycles) of the SSD
 # launches, averaged over a `--steps 3 --warmup 1` run (profiles/ssd_mfma_util.md)
-MFMA_BUSY = {("cfg3", "f32"): 0.728, ("cfg3", "bf16"): 0.174}
-MFMA_BUSY_MEASURED_AT = "748ef90"
+MFMA_BUSY = {("cfg3", "f32"): 0.725, ("cfg3", "bf16"): 0.174}
+MFMA_BUSY_MEASURED_AT = {("cfg3", "f32"): "51fa711", ("cfg3", "bf16"): "748ef90"}
 
 
 def parse():
@@ -439,7 +439,8 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, wit
     flops, nbytes = ssd_alg(B, L, H, P, N, esz)
     prec = "bf16" if dtype == "bf16" else "f32"
     kern = ("ssd_kernel (bf16 inputs, v_mfma_f32_16x16x32_bf16)" if dtype == "bf16" else
-            "ssd_f32_kernel (fp32, v_mfma_f32_16x16x4_f32)")
+            "ssd_f32_kernel with its C B^T pre-pass ssd_f32_cb_kernel (fp32, "
+            "v_mfma_f32_16x16x4_f32)")
     key = (name[:4], dtype)
     out = {"value": T / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "warmup": warm,
            "dtype": dtype,
@@ -461,7 +462,7 @@ def ssd_workload(torch, np, dev, args, B, L, H, bc_std, name, default_dtype, wit
     # the matrix cores' busy fraction as the counters read it (rocprofv3 MfmaUtil of this
     # launch; profiles/ssd_mfma_util.md, with the build it was measured on)
     rl["mfma_busy_counter"] = MFMA_BUSY.get(key)
-    rl["mfma_busy_measured_at"] = MFMA_BUSY_MEASURED_AT if key in MFMA_BUSY else None
+    rl["mfma_busy_measured_at"] = MFMA_BUSY_MEASURED_AT.get(key)
     if with_cpu and not args.no_cpu_baseline:
         from oracle import oracle as O
         # the whole workload (every sequence and head, the same inputs as fp32), repeated
