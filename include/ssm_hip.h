@@ -144,7 +144,9 @@ ssm_status ssm_m1_state_update(const float* x, long ldx, const float* dt, long l
  * the workspace, the Mamba-1 chunked scan over H*P channels; otherwise a sequential kernel
  * (no workspace needed). The chunk length of the reference config (chunkLen) does not change
  * the result; the kernel uses its own internal chunk. `workspace` holds
- * ssm_ssd_workspace(...) bytes. */
+ * ssm_ssd_workspace(...) bytes: segment states for long sequences and, for float inputs, the
+ * C B^T tiles of every chunk (a workspace with room for the segment states only gives the
+ * same result more slowly). */
 size_t ssm_ssd_workspace(int B, int L, int H, int P, int G, int N);
 ssm_status ssm_ssd_chunk_scan(int in_dtype, const void* x, long ldx, const float* dt, long lddt,
                               const float* dt_bias, int softplus, float dt_min, float dt_max,
