@@ -313,6 +313,50 @@ def test_ssd_f32_elementwise_cfg3_dims(B, L, H, h0):
     check_elementwise(host(hd), hT, "final state")
 
 
+def _f32_seg_bytes(B, L, H, P, N):
+    """The segment-state part of the fp32 SSD's workspace (the library's plan: segments so that
+    B H segments reach 512 workgroups, chunks of 32 steps)."""
+    nch = -(-L // 32)
+    s = min(max(-(-512 // (B * H)), 1), nch)
+    per = -(-nch // s)
+    nseg = -(-nch // per)
+    return 0 if nseg <= 1 else 4 * B * H * nseg * (P * N + 1)
+
+
+@pytest.mark.parametrize("B,L,H,G,N,h0", [(8, 256, 64, 1, 128, False), (1, 4096, 8, 1, 128, True),
+                                          (2, 777, 8, 2, 64, True)])
+def test_ssd_f32_cb_prepass_same_bits(B, L, H, G, N, h0):
+    """With the workspace of ssm_ssd_workspace the fp32 SSD takes its C B^T tiles from the
+    pre-pass (formed once per batch, group and chunk); with a workspace that holds only the
+    segment states the kernel forms them itself. Both run the same MFMA sequence on the same
+    B and C values, so y and the final state are the same bits; one of them is also checked
+    against the oracle. One workgroup batch of 64 heads, a segmented single sequence, two
+    groups with d_state 64."""
+    case(f"ssd f32 C.B^T pre-pass B={B} L={L} H={H} G={G} N={N} h0={h0}")
+    r = rng(6000 + L + G)
+    P = 64
+    x, dt, A, Bm, Cm, Dk = _ssd_inputs(r, B, L, H, P, G, N)
+    h0a = (0.3 * r.standard_normal((B, H, P, N))).astype(np.float32) if h0 else None
+    tx, tdt, tA, tB, tC, tD = dev(x), dev(dt), dev(A), dev(Bm), dev(Cm), dev(Dk)
+    th0 = dev(h0a) if h0 else None
+    from ssmjs_amd import _lib
+    full = _lib.lib().ssm_ssd_workspace(B, L, H, P, G, N)
+    small = _f32_seg_bytes(B, L, H, P, N)
+    assert full >= small + 3 * 1024 * B * G * (-(-L // 32)), "the query leaves room for the tiles"
+    outs = []
+    for nbytes in (full, small):
+        ws = torch.empty(max(nbytes, 4), device="cuda", dtype=torch.uint8)
+        hd = torch.zeros(B, H, P, N, device="cuda")
+        y = K().ssd_chunk_scan(tx, tdt, tA, tB, tC, tD, None, True, h0=th0, hT=hd, workspace=ws)
+        outs.append((host(y), host(hd)))
+    assert np.array_equal(outs[0][0], outs[1][0]), "y differs between the two tile sources"
+    assert np.array_equal(outs[0][1], outs[1][1]), "final state differs"
+    if B * L <= 4096:
+        ref, hT = O.ssd(x, dt, A, Bm, Cm, Dk, h0=h0a, return_state=True)
+        check_elementwise(outs[0][0], ref, "y")
+        check_elementwise(outs[0][1], hT, "final state")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_ssd_negative_dt_without_softplus(dtype):
     """softplus off and no lower clamp (dt_min = -inf): dt' keeps the raw, partly negative
